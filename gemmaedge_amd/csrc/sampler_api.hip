@@ -1,0 +1,231 @@
+// C ABI of the gfx950 sampling path (include/gemmaedge_sampler.h).
+//
+// Conventions follow the reference's accelerator layer where it has one:
+// a cached availability probe (src/cuda_backend.cu:571-580), workspaces sized
+// once and reused (src/cuda_backend.cu:388-425), and a status return instead of
+// a C++ exception across the boundary. Unlike the reference there is no
+// process-wide lock (src/cuda_backend.cu:513): a handle belongs to one stream.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/gemmaedge_sampler.h"
+#include "sampler_internal.h"
+
+struct ge_sampler {
+    int device;
+    int max_rows;
+    int max_vocab;
+    int max_history;
+    uint32_t* tickets;
+    uint32_t* chunk_tau;
+    uint32_t* chunk_count;
+    uint64_t* cand;
+    uint32_t* seen;
+    int64_t cand_stride;
+    int64_t seen_stride;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(GE_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Switches the calling thread to `device` for the lifetime of the object.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int device) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != device) ok = hipSetDevice(device) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+bool device_is_gfx950(int device) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return false;
+    return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+}
+
+constexpr int64_t kMaxChunkLen = static_cast<int64_t>(ge::kBlock) * ge::kMaxEpt;
+
+}  // namespace
+
+extern "C" {
+
+const char* ge_sampler_last_error(void) { return g_last_error.c_str(); }
+
+int ge_sampler_max_top_k(void) { return ge::kMaxTopK; }
+
+int ge_sampler_available(void) {
+    static int cached = -1;
+    if (cached < 0) {
+        int n = 0;
+        int found = 0;
+        if (hipGetDeviceCount(&n) == hipSuccess) {
+            for (int d = 0; d < n && !found; ++d) found = device_is_gfx950(d) ? 1 : 0;
+        }
+        cached = found;
+    }
+    return cached;
+}
+
+int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, ge_sampler** out) {
+    if (!out) return fail(GE_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    if (max_rows < 1 || max_vocab < 1 || max_history < 0)
+        return fail(GE_ERR_INVALID_ARG, "max_rows=%d max_vocab=%d max_history=%d", max_rows,
+                    max_vocab, max_history);
+    if (static_cast<int64_t>(max_vocab) > kMaxChunkLen * ge::kMaxChunks)
+        return fail(GE_ERR_CAPACITY, "max_vocab %d above %lld", max_vocab,
+                    static_cast<long long>(kMaxChunkLen * ge::kMaxChunks));
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n)
+        return fail(GE_ERR_NO_DEVICE, "device %d not present (%d devices)", device, n);
+    if (!device_is_gfx950(device)) return fail(GE_ERR_NO_DEVICE, "device %d is not gfx950", device);
+    DeviceGuard guard(device);
+    if (!guard.ok) return fail(GE_ERR_DEVICE, "hipSetDevice(%d) failed", device);
+
+    ge_sampler* s = new ge_sampler{};
+    s->device = device;
+    s->max_rows = max_rows;
+    s->max_vocab = max_vocab;
+    s->max_history = max_history;
+    s->cand_stride = (static_cast<int64_t>(max_vocab) + kMaxChunkLen - 1) / kMaxChunkLen * kMaxChunkLen;
+    s->seen_stride = (static_cast<int64_t>(max_vocab) + 31) / 32;
+    const size_t rows = static_cast<size_t>(max_rows);
+    hipError_t e = hipSuccess;
+    auto alloc = [&](void** p, size_t bytes) {
+        if (e == hipSuccess) e = hipMalloc(p, bytes);
+    };
+    alloc(reinterpret_cast<void**>(&s->tickets), rows * sizeof(uint32_t));
+    alloc(reinterpret_cast<void**>(&s->chunk_tau), rows * ge::kMaxChunks * sizeof(uint32_t));
+    alloc(reinterpret_cast<void**>(&s->chunk_count), rows * ge::kMaxChunks * sizeof(uint32_t));
+    alloc(reinterpret_cast<void**>(&s->cand), rows * static_cast<size_t>(s->cand_stride) * sizeof(uint64_t));
+    alloc(reinterpret_cast<void**>(&s->seen), rows * static_cast<size_t>(s->seen_stride) * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(s->tickets, 0, rows * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(s->seen, 0, rows * static_cast<size_t>(s->seen_stride) * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        ge_sampler_destroy(s);
+        return hip_fail(e, "ge_sampler_create");
+    }
+    *out = s;
+    return GE_OK;
+}
+
+void ge_sampler_destroy(ge_sampler* s) {
+    if (!s) return;
+    DeviceGuard guard(s->device);
+    (void)hipFree(s->tickets);
+    (void)hipFree(s->chunk_tau);
+    (void)hipFree(s->chunk_count);
+    (void)hipFree(s->cand);
+    (void)hipFree(s->seen);
+    delete s;
+}
+
+int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
+    if (!s || !args) return fail(GE_ERR_INVALID_ARG, "sampler or args is NULL");
+    const ge_sample_args& x = *args;
+    if (x.vocab < 1) return fail(GE_ERR_INVALID_ARG, "cannot sample empty logits");  // generation.cpp:63
+    if (!x.logits || !x.tokens_out) return fail(GE_ERR_INVALID_ARG, "logits or tokens_out is NULL");
+    if (x.dtype != GE_DTYPE_F32 && x.dtype != GE_DTYPE_BF16)
+        return fail(GE_ERR_INVALID_ARG, "dtype %d", x.dtype);
+    if (x.rows < 1) return fail(GE_ERR_INVALID_ARG, "rows %d", x.rows);
+    if (x.rows > s->max_rows || x.vocab > s->max_vocab)
+        return fail(GE_ERR_CAPACITY, "rows %d / vocab %d above handle capacity %d / %d", x.rows,
+                    x.vocab, s->max_rows, s->max_vocab);
+    if (x.row_stride < x.vocab) return fail(GE_ERR_INVALID_ARG, "row_stride %lld < vocab %d",
+                                            static_cast<long long>(x.row_stride), x.vocab);
+    if (x.ring) {
+        if (!x.ring_len || x.ring_capacity < 1)
+            return fail(GE_ERR_INVALID_ARG, "ring needs ring_len and ring_capacity >= 1");
+        if (x.history) return fail(GE_ERR_INVALID_ARG, "history and ring are exclusive");
+    }
+    if (x.history && !x.history_offsets) return fail(GE_ERR_INVALID_ARG, "history without offsets");
+    const bool maybe_sampling = x.row_params != nullptr || !(x.params.temperature <= 0.0f);
+    if (maybe_sampling && !x.uniforms) return fail(GE_ERR_INVALID_ARG, "uniforms required when sampling");
+
+    int gpt = 16;
+    if (!x.row_params) {
+        const ge_sample_params& p = x.params;
+        const uint32_t v = static_cast<uint32_t>(x.vocab);
+        const uint32_t k = p.temperature <= 0.0f ? 1u : (p.top_k ? (p.top_k < v ? p.top_k : v) : v);
+        if (k > static_cast<uint32_t>(ge::kMaxTopK))
+            return fail(GE_ERR_UNSUPPORTED, "effective top_k %u above %d (full-order path not built)",
+                        k, ge::kMaxTopK);
+        gpt = k <= 64 ? 1 : (k <= 256 ? 4 : 16);
+    }
+
+    // Launch geometry: 64 logits per thread when there are enough rows to fill
+    // the chip, else 16 so a single row still spreads over 64+ workgroups.
+    const int64_t chunks64 = (x.vocab + kMaxChunkLen - 1) / kMaxChunkLen;
+    const int64_t chunks16 = (x.vocab + ge::kBlock * 16 - 1) / (ge::kBlock * 16);
+    int ept = (static_cast<int64_t>(x.rows) * chunks64 >= 512 || chunks16 > ge::kMaxChunks) ? 64 : 16;
+    const int chunk_len = ge::kBlock * ept;
+    const int cpr = static_cast<int>((x.vocab + chunk_len - 1) / chunk_len);
+
+    const size_t esize = x.dtype == GE_DTYPE_BF16 ? 2 : 4;
+    const bool vec_ok = (reinterpret_cast<uintptr_t>(x.logits) % 16 == 0) &&
+                        ((static_cast<uint64_t>(x.row_stride) * esize) % 16 == 0);
+
+    ge::DevArgs a{};
+    a.logits = x.logits;
+    a.dtype = x.dtype;
+    a.rows = x.rows;
+    a.vocab = x.vocab;
+    a.row_stride = x.row_stride;
+    a.params = x.params;
+    a.row_params = x.row_params;
+    a.history = x.history;
+    a.history_offsets = x.history_offsets;
+    a.ring = x.ring;
+    a.ring_len = x.ring_len;
+    a.ring_capacity = x.ring_capacity;
+    a.uniforms = x.uniforms;
+    a.tokens = x.tokens_out;
+    a.probs = x.probs_out;
+    a.flags = x.flags_out;
+    a.tickets = s->tickets;
+    a.chunk_tau = s->chunk_tau;
+    a.chunk_count = s->chunk_count;
+    a.cand = s->cand;
+    a.seen = s->seen;
+    a.cand_stride = s->cand_stride;
+    a.seen_stride = s->seen_stride;
+    a.cpr = cpr;
+    a.chunk_len = chunk_len;
+    a.vec_ok = vec_ok ? 1 : 0;
+
+    DeviceGuard guard(s->device);
+    if (!guard.ok) return fail(GE_ERR_DEVICE, "hipSetDevice(%d) failed", s->device);
+    const hipError_t e = ge::launch_select(a, static_cast<hipStream_t>(stream), ept, gpt);
+    if (e != hipSuccess) return hip_fail(e, "launch");
+    return GE_OK;
+}
+
+}  // extern "C"

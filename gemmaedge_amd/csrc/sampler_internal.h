@@ -1,0 +1,56 @@
+// Internal launch interface between the C ABI (sampler_api.hip) and the
+// kernels (sampler_kernels.hip). Not installed; no reference counterpart.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gemmaedge_sampler.h"
+
+namespace ge {
+
+constexpr int kBlock = 256;        // threads per workgroup (4 wave64)
+constexpr int kMaxTopK = 1024;     // largest k of the selection path
+constexpr int kSurvivorCap = 2048; // LDS survivors of the merge stage
+constexpr int kMaxChunks = 256;    // chunks (workgroups) per row
+constexpr int kMaxEpt = 64;        // elements per thread in the streaming pass
+
+// Device-side view of one ge_sample call plus the handle's workspace.
+struct DevArgs {
+    const void* logits;
+    int32_t dtype;
+    int32_t rows;
+    int32_t vocab;
+    int64_t row_stride;           // elements
+    ge_sample_params params;
+    const ge_sample_params* row_params;
+    const int32_t* history;
+    const int32_t* history_offsets;
+    int32_t* ring;
+    int32_t* ring_len;
+    int32_t ring_capacity;
+    const float* uniforms;
+    int32_t* tokens;
+    float* probs;
+    int32_t* flags;
+
+    // Workspace (allocated by ge_sampler_create, sized for max_rows x max_vocab).
+    uint32_t* tickets;            // [max_rows]          zero between calls
+    uint32_t* chunk_tau;          // [max_rows * kMaxChunks]
+    uint32_t* chunk_count;        // [max_rows * kMaxChunks]
+    uint64_t* cand;               // [max_rows * cand_stride]  (raw key << 32 | index)
+    uint32_t* seen;               // [max_rows * seen_stride]  zero between calls
+    int64_t cand_stride;          // entries per row, >= cpr * chunk_len
+    int64_t seen_stride;          // words per row, >= ceil(vocab / 32)
+
+    // Launch geometry of the streaming pass.
+    int32_t cpr;                  // chunks per row
+    int32_t chunk_len;            // kBlock * ept
+    int32_t vec_ok;               // rows are 16-byte aligned
+};
+
+// Launches the fused select/sample kernel for rows whose k <= kMaxTopK.
+// ept in {16, 64}; gpt in {1, 4, 16}. Returns a hipError_t.
+hipError_t launch_select(const DevArgs& a, hipStream_t stream, int ept, int gpt);
+
+}  // namespace ge

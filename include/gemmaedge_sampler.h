@@ -1,0 +1,141 @@
+/*
+ * gemmaedge_sampler.h — C ABI of the MI355X (gfx950) token-sampling path.
+ *
+ * This library replaces the reference's CPU sampler dispatch:
+ *   gemmaedge::sample_token(const std::vector<float>& logits,
+ *                           const SamplingConfig&, std::mt19937_64&)
+ *     declared include/gemmaedge/generation.h:69-71, body src/generation.cpp:60-127,
+ *   plus the final-logit softcap loop of Gemma4Session::forward,
+ *     src/generation.cpp:431-437,
+ * with one stream-ordered device call over a batch of logits rows that are
+ * already resident in device memory. The C++ drop-in with the reference's
+ * exact signature sits on top of it (include/gemmaedge/sampling.h).
+ *
+ * Plain C types only; no exceptions cross this boundary. Every entry point
+ * returns a status code (GE_OK or a negative GE_ERR_*); ge_sampler_last_error()
+ * gives the calling thread's last message.
+ *
+ * Semantics per row (same order as the reference, plus the build's penalty):
+ *   v = logit (bf16 widened exactly, src/tensor.cpp:226-231)
+ *   v = softcap * tanh(v / softcap)          if softcap > 0     (generation.cpp:431-437)
+ *   v = v > 0 ? v / r : v * r                for each UNIQUE history id (r = penalty)
+ *   temperature <= 0: greedy, first maximum  (generation.cpp:66-70)
+ *   else top-k (k = top_k ? min(top_k, V) : V), softmax with f32 exp and a double
+ *   denominator, min-p / top-p, inverse-CDF draw of u * mass  (generation.cpp:79-126)
+ * Ties are broken by the lowest token index. Transcendentals round exactly as
+ * glibc 2.35 tanhf/expf do, so ids are bit-identical to the CPU reference.
+ */
+#ifndef GEMMAEDGE_SAMPLER_H
+#define GEMMAEDGE_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define GE_OK 0
+#define GE_ERR_INVALID_ARG (-1)  /* bad pointer/size/param; cf. generation.cpp:63 */
+#define GE_ERR_UNSUPPORTED (-2)  /* a combination this build does not implement */
+#define GE_ERR_DEVICE (-3)       /* HIP runtime error */
+#define GE_ERR_NO_DEVICE (-4)    /* no usable gfx950 device */
+#define GE_ERR_CAPACITY (-5)     /* rows / vocab above what the handle was created for */
+
+/* Logits element types. */
+#define GE_DTYPE_F32 0
+#define GE_DTYPE_BF16 1
+
+/* Per-row output flags (ge_sample_args.flags_out). */
+#define GE_FLAG_NEAR_BOUNDARY 1  /* draw within 1e-6 of an adjacent CDF boundary */
+#define GE_FLAG_UNSUPPORTED 2    /* row's parameters need a path this build lacks; token = -1 */
+
+/* One row's sampling parameters: the reference SamplingConfig
+ * (include/gemmaedge/generation.h:55-61: temperature, top_k, top_p, min_p)
+ * plus the softcap (Gemma4Config::final_logit_softcap, gemma4_model.h:25,
+ * applied at generation.cpp:431-437) and the build's repetition penalty.
+ * The seed is not here: uniforms are supplied per row instead. */
+typedef struct ge_sample_params {
+    float temperature;        /* <= 0 -> greedy */
+    uint32_t top_k;           /* 0 -> disabled (k = vocab) */
+    float top_p;
+    float min_p;
+    float softcap;            /* <= 0 -> no softcap */
+    float repetition_penalty; /* 1 -> no penalty */
+} ge_sample_params;
+
+typedef struct ge_sample_args {
+    /* Logits: device memory, row r starts at logits + r * row_stride elements. */
+    const void* logits;
+    int32_t dtype;            /* GE_DTYPE_F32 or GE_DTYPE_BF16 */
+    int32_t rows;             /* >= 1 */
+    int32_t vocab;            /* >= 1; the reference's logits.size() */
+    int64_t row_stride;       /* elements, >= vocab */
+
+    /* Parameters: `params` for every row, unless row_params (device array of
+     * `rows` entries) is non-NULL. */
+    ge_sample_params params;
+    const ge_sample_params* row_params;
+
+    /* Penalty history, one of:
+     *  (a) history + history_offsets (device): row r's ids are
+     *      history[history_offsets[r] .. history_offsets[r+1]);
+     *  (b) a device ring for graph replay: row r's ids are
+     *      ring[r * ring_capacity + i], i < min(ring_len[r], ring_capacity);
+     *      after sampling the kernel stores the row's token at
+     *      ring[r * ring_capacity + ring_len[r] % ring_capacity] and
+     *      increments ring_len[r] (all on the device, no host sync).
+     * Duplicates are allowed; ids outside [0, vocab) are ignored. */
+    const int32_t* history;
+    const int32_t* history_offsets;
+    int32_t* ring;
+    int32_t* ring_len;
+    int32_t ring_capacity;
+
+    /* Uniforms in [0, 1), device, one per row (ignored for greedy rows): the
+     * value the reference draws with generate_canonical<float, 24> from its
+     * mt19937_64 (src/generation.cpp:118-119). */
+    const float* uniforms;
+
+    /* Outputs (device). probs_out / flags_out may be NULL. */
+    int32_t* tokens_out;
+    float* probs_out;         /* probability of the chosen token after top-k
+                                 normalisation (generation.cpp:100); 1 for greedy */
+    int32_t* flags_out;       /* GE_FLAG_* bits */
+} ge_sample_args;
+
+typedef struct ge_sampler ge_sampler;
+
+/* 1 if a gfx950 device is usable by this process, else 0. Cached after the
+ * first call (cf. is_cuda_available, src/cuda_backend.cu:571-580). */
+int ge_sampler_available(void);
+
+/* Create a sampler on `device` for up to max_rows rows of up to max_vocab
+ * entries. Allocates every workspace now; ge_sample never allocates.
+ * max_history is the largest per-row history length that will be passed. */
+int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history,
+                      ge_sampler** out);
+
+void ge_sampler_destroy(ge_sampler* sampler);
+
+/* Sample one token per row. Stream-ordered and asynchronous on `stream`
+ * (a hipStream_t; NULL = the default stream); no host synchronisation and no
+ * allocation, so it can be captured into a HIP graph. One handle must not be
+ * used by two streams at once. */
+int ge_sample(ge_sampler* sampler, void* stream, const ge_sample_args* args);
+
+/* Thread-local message describing the last failure on this thread. */
+const char* ge_sampler_last_error(void);
+
+/* Largest top_k handled by the selection path of this build. Rows whose
+ * effective k exceeds it (top_k disabled or larger) take the full-order path,
+ * which this build implements for bf16 logits only; fp32 rows get
+ * GE_FLAG_UNSUPPORTED (or GE_ERR_UNSUPPORTED when known on the host). */
+int ge_sampler_max_top_k(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GEMMAEDGE_SAMPLER_H */
