@@ -1,0 +1,380 @@
+#!/usr/bin/env python3
+"""Benchmark of the GemmaEdge token-sampling path on one MI355X.
+
+Headline (BASELINE.json metric): rows/s of the sampler at V=262144, batch 64
+(config C2: fp32 N(0,3) + peaks, softcap 30, T 0.7, top-k 40, top-p 0.9,
+penalty 1.15 over 2048-id histories), with the dominant kernel's achieved HBM
+bandwidth against the 8 TB/s peak; batch-1 latency (C1), C3, C4 and the C5
+decode sweep are reported as extra fields.
+
+A "step" is one ge_sample call over the whole batch with every input already
+resident in HBM. The K timed steps are one HIP-graph replay of K captured
+launches, bracketed by torch.cuda.synchronize(), so the host's launch rate does
+not limit the figure. Kernel durations for the roofline are measured with HIP
+events on the launch stream, queued behind a spin kernel so that no host gap
+falls inside an event pair.
+
+The CPU baseline leg times the oracle (oracle/ge_oracle.cpp, a C++ restatement
+of the reference sampler) on the same C2 rows on the host's cores; its outputs
+also give the same-run parity counts.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--extras C1,C3,C4,C5]
+
+Prints progress to stderr and ONE JSON line to stdout.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, GB/s
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "select_kernel_C2_traffic.txt")
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description="GemmaEdge sampler benchmark (one MI355X)")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--extras", default="C1,C3,C4,C5",
+                    help="comma list of extra configs to report (C1,C3,C4,C5) or ''")
+    ap.add_argument("--c5-steps", type=int, default=1024)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target wall time of the oracle baseline sample")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="short run for rocprofv3: C2 launches plus a copy-kernel calibration")
+    return ap.parse_args()
+
+
+class Bound:
+    """A workload resident on the device with a prebuilt ge_sample_args."""
+
+    def __init__(self, sampler, w, torch):
+        from gemmaedge_amd import sampler as S
+        from gemmaedge_amd.workloads import to_device
+
+        self.w = w
+        self.torch = torch
+        self.logits, self.hist, self.offs, self.uni = to_device(w)
+        rows = w.rows
+        self.tokens = torch.empty(rows, dtype=torch.int32, device="cuda")
+        self.probs = torch.empty(rows, dtype=torch.float32, device="cuda")
+        self.flags = torch.empty(rows, dtype=torch.int32, device="cuda")
+        a = S.SampleArgs()
+        a.logits = self.logits.data_ptr()
+        a.dtype = S.GE_DTYPE_BF16 if w.dtype == "bf16" else S.GE_DTYPE_F32
+        a.rows = rows
+        a.vocab = w.vocab
+        a.row_stride = w.vocab
+        a.params = S.SamplingConfig(**w.params).params()
+        a.history = None if self.hist is None else self.hist.data_ptr()
+        a.history_offsets = None if self.offs is None else self.offs.data_ptr()
+        a.uniforms = self.uni.data_ptr()
+        a.tokens_out = self.tokens.data_ptr()
+        a.probs_out = self.probs.data_ptr()
+        a.flags_out = self.flags.data_ptr()
+        self.args = a
+        self.sampler = sampler
+        self.lib = S.load_library()
+        self.S = S
+
+    def launch(self, stream_ptr):
+        rc = self.lib.ge_sample(self.sampler._h, ctypes.c_void_p(stream_ptr), ctypes.byref(self.args))
+        if rc != 0:
+            raise RuntimeError(f"ge_sample failed ({rc}): {self.S.last_error()}")
+
+    def run_once(self):
+        self.launch(self.torch.cuda.current_stream().cuda_stream)
+        return self.outputs()
+
+    def outputs(self):
+        self.torch.cuda.synchronize()
+        return (self.tokens.cpu().numpy(), self.probs.cpu().numpy(), self.flags.cpu().numpy())
+
+
+def kernel_durations_us(torch, b: Bound, n: int):
+    """Per-launch durations from HIP events on the launch stream; a spin kernel
+    first keeps the GPU busy while the host queues every event pair."""
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2.5e7))
+    for e0, e1 in ev:
+        e0.record(stream)
+        b.launch(stream.cuda_stream)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return np.array([e0.elapsed_time(e1) * 1000.0 for e0, e1 in ev])
+
+
+def capture(torch, b: Bound, steps: int):
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            cap = torch.cuda.current_stream()
+            for _ in range(steps):
+                b.launch(cap.cuda_stream)
+    torch.cuda.synchronize()
+    return g
+
+
+def timed_graph(torch, b: Bound, steps: int, warmup: int):
+    """W eager warmup launches, then EXACTLY `steps` launches as one graph
+    replay bracketed by synchronize(). Returns seconds."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        b.launch(stream.cuda_stream)
+    torch.cuda.synchronize()
+    g = capture(torch, b, steps)
+    g.replay()  # untimed: first replay uploads the graph
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return t1 - t0
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    if not os.path.exists(PROFILE_TRAFFIC):
+        return None
+    vals = {}
+    for line in open(PROFILE_TRAFFIC):
+        if "=" in line and not line.lstrip().startswith("#"):
+            k, v = line.split("=", 1)
+            vals[k.strip()] = v.strip()
+    try:
+        return float(vals["traffic_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline_leg(w, seconds: float, gpu_out):
+    """CPU baseline: the oracle over the same C2 rows, one row per thread on
+    the host's cores (capped by OMP_NUM_THREADS), repeated for about `seconds`.
+    Its outputs are also the same-run parity reference."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ge_oracle as O
+
+    nthreads = os.cpu_count() or 1
+    nthreads = max(1, min(nthreads, int(os.environ.get("OMP_NUM_THREADS", nthreads))))
+    params = O.make_params(**w.params)
+    hist = w.history if w.history.size else None
+    offs = w.offsets if w.history.size else None
+    t0 = time.perf_counter()
+    ora = O.run(w.logits, params, history=hist, offsets=offs, uniforms=w.uniforms, nthreads=nthreads)
+    first = time.perf_counter() - t0
+    reps = max(1, int(seconds / max(first, 1e-3)))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        O.run(w.logits, params, history=hist, offsets=offs, uniforms=w.uniforms, nthreads=nthreads)
+    dt = time.perf_counter() - t0
+    rows = reps * w.rows
+    base = {"value": rows / dt, "unit": "rows/s", "cores": nthreads, "kind": "port",
+            "sample": f"{reps} passes over the {w.rows}-row {w.name} batch ({rows} rows, "
+                      f"{dt:.1f} s wall), oracle/ge_oracle.cpp, one row per thread"}
+    tokens, probs, flags = gpu_out
+    rel = np.abs(probs.astype(np.float64) - ora.probs) / np.maximum(np.abs(ora.probs), 1e-30)
+    par = {"rows": int(w.rows), "token_mismatches": int(np.sum(tokens != ora.tokens)),
+           "near_boundary_draws": int(np.sum(ora.flags)),
+           "max_prob_rel_err": float(np.nanmax(rel)) if rel.size else 0.0}
+    return base, par
+
+
+def bench_c1(torch, sampler, W):
+    out = {}
+    for greedy in (False, True):
+        w = W.c1(greedy=greedy)
+        b = Bound(sampler, w, torch)
+        d = kernel_durations_us(torch, b, 200)
+        g = timed_graph(torch, b, 200, 10)
+        out["C1_greedy" if greedy else "C1"] = {
+            "us_per_token_kernel_p50": float(np.median(d)),
+            "us_per_token_kernel_p99": float(np.percentile(d, 99)),
+            "us_per_token_graph_back_to_back": g / 200 * 1e6,
+            "bytes_per_launch": w.bytes_per_row()}
+    return out
+
+
+def bench_throughput(torch, sampler, w, name):
+    b = Bound(sampler, w, torch)
+    tok, _, flags = b.run_once()
+    if np.any(flags & 2):
+        return {name: {"status": "unsupported in this build (rows flagged GE_FLAG_UNSUPPORTED)"}}
+    d = kernel_durations_us(torch, b, 30)
+    bytes_launch = w.bytes_per_row() * w.rows
+    gbs = bytes_launch / (np.mean(d) * 1e-6) / 1e9
+    return {name: {"rows": w.rows, "rows_per_s": w.rows / (np.mean(d) * 1e-6),
+                   "kernel_us": float(np.mean(d)), "GBps": gbs, "frac_peak": gbs / HBM_PEAK_GBS}}
+
+
+def c5_sweep(torch, sampler, W, steps):
+    """Batch-1 decode sweep: one captured graph (the sampling launch) replayed
+    per step; the history ring and its length live on the device and grow by
+    each sampled token. New logits/uniform are copied in outside the timed pair."""
+    from gemmaedge_amd import sampler as S
+
+    w = W.c5_steps(steps=steps)
+    cap = int(w.notes["ring_capacity"])
+    all_logits = torch.from_numpy(w.logits).cuda()
+    uni_all = torch.from_numpy(w.uniforms).cuda()
+    logits = torch.empty(w.vocab, dtype=torch.float32, device="cuda")
+    uni = torch.empty(1, dtype=torch.float32, device="cuda")
+    ring = torch.zeros((1, cap), dtype=torch.int32, device="cuda")
+    ring_len = torch.zeros(1, dtype=torch.int32, device="cuda")
+    tokens = torch.empty(1, dtype=torch.int32, device="cuda")
+    probs = torch.empty(1, dtype=torch.float32, device="cuda")
+    flags = torch.empty(1, dtype=torch.int32, device="cuda")
+    a = S.SampleArgs()
+    a.logits = logits.data_ptr()
+    a.dtype = S.GE_DTYPE_F32
+    a.rows = 1
+    a.vocab = w.vocab
+    a.row_stride = w.vocab
+    a.params = S.SamplingConfig(**w.params).params()
+    a.ring = ring.data_ptr()
+    a.ring_len = ring_len.data_ptr()
+    a.ring_capacity = cap
+    a.uniforms = uni.data_ptr()
+    a.tokens_out = tokens.data_ptr()
+    a.probs_out = probs.data_ptr()
+    a.flags_out = flags.data_ptr()
+    lib = S.load_library()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            rc = lib.ge_sample(sampler._h, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
+                               ctypes.byref(a))
+    if rc != 0:
+        raise RuntimeError(S.last_error())
+    torch.cuda.synchronize()
+    ring.zero_()
+    ring_len.zero_()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        logits.copy_(all_logits[i])
+        uni.copy_(uni_all[i:i + 1])
+        ev[i][0].record(stream)
+        g.replay()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    us = np.array([e0.elapsed_time(e1) * 1000.0 for e0, e1 in ev])
+    return {"steps": steps, "p50_us": float(np.median(us)), "p99_us": float(np.percentile(us, 99)),
+            "mean_us": float(np.mean(us)), "history_len_final": int(ring_len.item())}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
+                                   "(rows shard across GPUs without communication, see DESIGN.md)"}))
+        sys.exit(2)
+    import torch
+
+    from gemmaedge_amd import Sampler, available
+    from gemmaedge_amd import workloads as W
+
+    if not torch.cuda.is_available() or not available():
+        print(json.dumps({"error": "no gfx950 GPU visible"}))
+        sys.exit(1)
+    sampler = Sampler(max_rows=512, max_vocab=W.VOCAB, max_history=8192)
+
+    log("generating C2 (64 x 262144 fp32)")
+    w = W.c2()
+    b = Bound(sampler, w, torch)
+    bytes_launch = w.bytes_per_row() * w.rows
+
+    if args.profile_pass:
+        stream = torch.cuda.current_stream()
+        for _ in range(args.steps):
+            b.launch(stream.cuda_stream)
+        torch.cuda.synchronize()
+        src = torch.empty(256 * 2**20 // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"profile pass: {args.steps} C2 launches, 5 copies of {src.numel() * 4} bytes")
+        print(json.dumps({"profile_pass": True, "c2_launches": args.steps, "copy_bytes": src.numel() * 4}))
+        return
+
+    log(f"timing {args.steps} steps (warmup {args.warmup})")
+    seconds = timed_graph(torch, b, args.steps, args.warmup)
+    ms = seconds / args.steps * 1e3
+    rows_per_s = w.rows * args.steps / seconds
+    d = kernel_durations_us(torch, b, 100)
+    achieved = bytes_launch / (np.mean(d) * 1e-6) / 1e9
+    log(f"C2: {ms * 1e3:.2f} us/step, kernel {np.mean(d):.2f} us, {achieved:.0f} GB/s")
+    gpu_out = b.run_once()
+
+    extras = {}
+    for name in [x for x in args.extras.split(",") if x]:
+        log(f"extra {name}")
+        try:
+            if name == "C1":
+                extras.update(bench_c1(torch, sampler, W))
+            elif name == "C3":
+                extras.update(bench_throughput(torch, sampler, W.c3(), "C3"))
+            elif name == "C4":
+                extras.update(bench_throughput(torch, sampler, W.c4(), "C4"))
+            elif name == "C5":
+                extras["C5"] = c5_sweep(torch, sampler, W, args.c5_steps)
+        except Exception as e:  # report, do not hide
+            extras[name] = {"error": repr(e)}
+        torch.cuda.empty_cache()
+
+    cpu, par = None, None
+    if not args.no_cpu_baseline:
+        log("CPU baseline leg (oracle) ...")
+        cpu, par = cpu_baseline_leg(w, args.cpu_seconds, gpu_out)
+        log(f"C2 parity: {par}")
+
+    result = {
+        "metric": "sampler rows/s at V=262144, batch 64 (C2)",
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Philox logits, mt19937_64 uniforms)",
+        "config": {"workload": "C2: 64 rows x V=262144 fp32, softcap 30, T 0.7, top-k 40, "
+                               "top-p 0.9, penalty 1.15, H=2048", "rows": w.rows, "vocab": w.vocab},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(),
+                     "kernel": "select_kernel<float,64,1>", "kernel_us_mean": float(np.mean(d)),
+                     "bytes_per_launch": bytes_launch},
+        "cpu_baseline": cpu,
+        "parity": {"C2": par},
+        "extras": extras,
+    }
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -23,12 +23,9 @@ struct ge_sampler {
     int max_vocab;
     int max_history;
     uint32_t* tickets;
-    uint32_t* chunk_tau;
     uint32_t* chunk_count;
     uint64_t* cand;
-    uint32_t* seen;
     int64_t cand_stride;
-    int64_t seen_stride;
 };
 
 namespace {
@@ -115,19 +112,15 @@ int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, 
     s->max_vocab = max_vocab;
     s->max_history = max_history;
     s->cand_stride = (static_cast<int64_t>(max_vocab) + kMaxChunkLen - 1) / kMaxChunkLen * kMaxChunkLen;
-    s->seen_stride = (static_cast<int64_t>(max_vocab) + 31) / 32;
     const size_t rows = static_cast<size_t>(max_rows);
     hipError_t e = hipSuccess;
     auto alloc = [&](void** p, size_t bytes) {
         if (e == hipSuccess) e = hipMalloc(p, bytes);
     };
     alloc(reinterpret_cast<void**>(&s->tickets), rows * sizeof(uint32_t));
-    alloc(reinterpret_cast<void**>(&s->chunk_tau), rows * ge::kMaxChunks * sizeof(uint32_t));
     alloc(reinterpret_cast<void**>(&s->chunk_count), rows * ge::kMaxChunks * sizeof(uint32_t));
     alloc(reinterpret_cast<void**>(&s->cand), rows * static_cast<size_t>(s->cand_stride) * sizeof(uint64_t));
-    alloc(reinterpret_cast<void**>(&s->seen), rows * static_cast<size_t>(s->seen_stride) * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(s->tickets, 0, rows * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(s->seen, 0, rows * static_cast<size_t>(s->seen_stride) * sizeof(uint32_t));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         ge_sampler_destroy(s);
@@ -141,10 +134,8 @@ void ge_sampler_destroy(ge_sampler* s) {
     if (!s) return;
     DeviceGuard guard(s->device);
     (void)hipFree(s->tickets);
-    (void)hipFree(s->chunk_tau);
     (void)hipFree(s->chunk_count);
     (void)hipFree(s->cand);
-    (void)hipFree(s->seen);
     delete s;
 }
 
@@ -185,7 +176,7 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     // the chip, else 16 so a single row still spreads over 64+ workgroups.
     const int64_t chunks64 = (x.vocab + kMaxChunkLen - 1) / kMaxChunkLen;
     const int64_t chunks16 = (x.vocab + ge::kBlock * 16 - 1) / (ge::kBlock * 16);
-    int ept = (static_cast<int64_t>(x.rows) * chunks64 >= 512 || chunks16 > ge::kMaxChunks) ? 64 : 16;
+    int ept = (static_cast<int64_t>(x.rows) * chunks64 >= 16 || chunks16 > ge::kMaxChunks) ? 64 : 16;
     const int chunk_len = ge::kBlock * ept;
     const int cpr = static_cast<int>((x.vocab + chunk_len - 1) / chunk_len);
 
@@ -211,12 +202,9 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     a.probs = x.probs_out;
     a.flags = x.flags_out;
     a.tickets = s->tickets;
-    a.chunk_tau = s->chunk_tau;
     a.chunk_count = s->chunk_count;
     a.cand = s->cand;
-    a.seen = s->seen;
     a.cand_stride = s->cand_stride;
-    a.seen_stride = s->seen_stride;
     a.cpr = cpr;
     a.chunk_len = chunk_len;
     a.vec_ok = vec_ok ? 1 : 0;

@@ -36,12 +36,9 @@ struct DevArgs {
 
     // Workspace (allocated by ge_sampler_create, sized for max_rows x max_vocab).
     uint32_t* tickets;            // [max_rows]          zero between calls
-    uint32_t* chunk_tau;          // [max_rows * kMaxChunks]
     uint32_t* chunk_count;        // [max_rows * kMaxChunks]
-    uint64_t* cand;               // [max_rows * cand_stride]  (raw key << 32 | index)
-    uint32_t* seen;               // [max_rows * seen_stride]  zero between calls
+    uint64_t* cand;               // [max_rows * cand_stride]  composite keys of final values
     int64_t cand_stride;          // entries per row, >= cpr * chunk_len
-    int64_t seen_stride;          // words per row, >= ceil(vocab / 32)
 
     // Launch geometry of the streaming pass.
     int32_t cpr;                  // chunks per row

@@ -210,3 +210,18 @@ def c5_steps(seed: int = 5, steps: int = 1024, vocab: int = VOCAB) -> Workload:
 
 
 CONFIGS = {"C1": c1, "C2": c2, "C3": c3, "C4": c4, "C5": c5_steps}
+
+
+def to_device(w: Workload, device="cuda"):
+    """Copy a workload's inputs to the GPU: (logits, history, offsets, uniforms);
+    bf16 logits become a torch.bfloat16 view of the same bits."""
+    import torch
+
+    if w.dtype == "bf16":
+        logits = torch.from_numpy(np.ascontiguousarray(w.logits).view(np.int16)).to(device).view(torch.bfloat16)
+    else:
+        logits = torch.from_numpy(np.ascontiguousarray(w.logits)).to(device)
+    hist = torch.from_numpy(w.history.astype(np.int32)).to(device) if w.history.size else None
+    offs = torch.from_numpy(w.offsets.astype(np.int32)).to(device) if w.history.size else None
+    uni = torch.from_numpy(w.uniforms.astype(np.float32)).to(device)
+    return logits, hist, offs, uni

@@ -12,17 +12,7 @@ def oracle_params(p: dict) -> O.Params:
     return O.make_params(**p)
 
 
-def to_device(w: W.Workload, device="cuda"):
-    import torch
-
-    if w.dtype == "bf16":
-        logits = torch.from_numpy(w.logits.view(np.int16)).to(device).view(torch.bfloat16)
-    else:
-        logits = torch.from_numpy(w.logits).to(device)
-    hist = torch.from_numpy(w.history.astype(np.int32)).to(device) if w.history.size else None
-    offs = torch.from_numpy(w.offsets.astype(np.int32)).to(device) if w.history.size else None
-    uni = torch.from_numpy(w.uniforms.astype(np.float32)).to(device)
-    return logits, hist, offs, uni
+to_device = W.to_device
 
 
 def run_gpu(sampler, w: W.Workload):
