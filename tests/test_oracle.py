@@ -113,8 +113,10 @@ def test_softcap_closed_form_and_monotone():
     c = 30.0
     out = O.transform_row(x, O.make_params(softcap=c))
     exact = c * np.tanh(x.astype(np.float64) / c)
-    # glibc tanhf is accurate to a couple of ulps; three float ulps of slack.
-    assert np.all(np.abs(out - exact) <= 3 * np.spacing(np.abs(exact).astype(np.float32)) + 1e-45)
+    # Division, glibc tanhf (about 2 ulp) and the product round three times:
+    # the result stays within 4 float ulps of the exact c * tanh(x / c)
+    # (3.34 ulp measured on 200k samples). A dropped term or sign fails this.
+    assert np.all(np.abs(out - exact) <= 4 * np.spacing(np.abs(exact).astype(np.float32)) + 1e-45)
     assert np.all(np.abs(out) <= c)
     order = np.argsort(x, kind="stable")
     assert np.all(np.diff(out[order]) >= 0)  # monotone non-decreasing
