@@ -136,7 +136,8 @@ def capture(torch, b: Bound, steps: int):
 
 def timed_graph(torch, b: Bound, steps: int, warmup: int):
     """W eager warmup launches, then EXACTLY `steps` launches as one graph
-    replay bracketed by synchronize(). Returns seconds."""
+    replay bracketed by synchronize(). Returns (wall seconds, seconds between
+    HIP events recorded on the launch stream around the replay)."""
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         b.launch(stream.cuda_stream)
@@ -144,11 +145,14 @@ def timed_graph(torch, b: Bound, steps: int, warmup: int):
     g = capture(torch, b, steps)
     g.replay()  # untimed: first replay uploads the graph
     torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    e0.record(stream)
     g.replay()
+    e1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    return t1 - t0
+    return t1 - t0, e0.elapsed_time(e1) * 1e-3
 
 
 def read_traffic():
@@ -204,7 +208,7 @@ def bench_c1(torch, sampler, W):
         w = W.c1(greedy=greedy)
         b = Bound(sampler, w, torch)
         d = kernel_durations_us(torch, b, 200)
-        g = timed_graph(torch, b, 200, 10)
+        g, _ = timed_graph(torch, b, 200, 10)
         out["C1_greedy" if greedy else "C1"] = {
             "us_per_token_kernel_p50": float(np.median(d)),
             "us_per_token_kernel_p99": float(np.percentile(d, 99)),
@@ -320,12 +324,14 @@ def main():
         return
 
     log(f"timing {args.steps} steps (warmup {args.warmup})")
-    seconds = timed_graph(torch, b, args.steps, args.warmup)
+    seconds, ev_seconds = timed_graph(torch, b, args.steps, args.warmup)
     ms = seconds / args.steps * 1e3
     rows_per_s = w.rows * args.steps / seconds
-    d = kernel_durations_us(torch, b, 100)
-    achieved = bytes_launch / (np.mean(d) * 1e-6) / 1e9
-    log(f"C2: {ms * 1e3:.2f} us/step, kernel {np.mean(d):.2f} us, {achieved:.0f} GB/s")
+    launch_us = ev_seconds / args.steps * 1e6  # average launch duration, HIP events
+    achieved = bytes_launch / (launch_us * 1e-6) / 1e9
+    d = kernel_durations_us(torch, b, 100)   # one launch per event pair
+    log(f"C2: {ms * 1e3:.2f} us/step, {launch_us:.2f} us/launch (events), isolated {np.mean(d):.2f} us, "
+        f"{achieved:.0f} GB/s")
     gpu_out = b.run_once()
 
     extras = {}
@@ -367,8 +373,8 @@ def main():
                                "top-p 0.9, penalty 1.15, H=2048", "rows": w.rows, "vocab": w.vocab},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(),
-                     "kernel": "select_kernel<float,64,1>", "kernel_us_mean": float(np.mean(d)),
-                     "bytes_per_launch": bytes_launch},
+                     "kernel": "select_kernel<float,64,1>", "kernel_us_mean": launch_us,
+                     "kernel_us_isolated_p50": float(np.median(d)), "bytes_per_launch": bytes_launch},
         "cpu_baseline": cpu,
         "parity": {"C2": par},
         "extras": extras,
