@@ -20,11 +20,12 @@
 //            it on FMA-capable x86-64 hosts, so the reduction and polynomial
 //            below use fused multiply-adds exactly where that build does.
 //
-// The 32-entry table is computed from the mathematics: entry i is the
-// IEEE double nearest 2^(i/32) with (i << 47) subtracted from its bits.
-// tests/test_math_exhaustive.py checks every fp32 input of both functions
-// against the host's glibc, on the CPU (this header compiled for the host)
-// and on the GPU.
+// The 32-entry table holds, for entry i, the bits of the IEEE double nearest
+// 2^(i/32) minus (i << 47); tests/test_math.py recomputes every entry from
+// 2^(i/32) in 60-digit decimal arithmetic. tests/test_math.py also checks
+// every fp32 input of both functions against the host's glibc (this header
+// compiled for the host by tests/cpp/math_check.hip) and digests of the
+// device build's outputs on the GPU.
 //
 // Every function here is evaluated with floating-point contraction off; the
 // fused operations are explicit fma() calls.

@@ -68,3 +68,23 @@ def test_device_build_matches_glibc_digests(lib, fn, name):
     want = golden()[name]
     bad = [b for b in range(256) if got[b] != want[b]]
     assert not bad, f"{name}: digest mismatch in blocks {bad[:16]} (inputs block << 24)"
+
+
+def test_exp2_table_is_computed_from_mathematics():
+    """Each entry of the expf table is the double nearest 2^(i/32), with
+    (i << 47) subtracted from its bit pattern so that adding k << 47 for
+    k = 32*e + i scales it by 2^e (gemmaedge_amd/csrc/ge_math.h)."""
+    import re
+    import struct
+    from decimal import Decimal, getcontext
+
+    text = open(os.path.join(HERE, "..", "gemmaedge_amd", "csrc", "ge_math.h")).read()
+    body = text[text.index("#define GE_EXP2_TABLE"):]
+    body = body[:body.index("}")]
+    entries = [int(x, 16) for x in re.findall(r"0x([0-9a-f]+)ull", body)]
+    assert len(entries) == 32
+    getcontext().prec = 60
+    for i, bits in enumerate(entries):
+        nearest = float(Decimal(2) ** (Decimal(i) / Decimal(32)))  # correctly rounded
+        want = struct.unpack("<Q", struct.pack("<d", nearest))[0] - (i << 47)
+        assert bits == want, i
