@@ -1,0 +1,246 @@
+// Exact replay of a sequential floating-point accumulation in closed form.
+//
+// The reference's softmax denominator (double), its top-p cumulative and the
+// subtract walk of its draw (float) are left-to-right sums over the
+// probabilities in sorted order (src/generation.cpp:96-97, 105-113, 120-124).
+// When many consecutive terms are equal — every token of one bf16 value has
+// the same probability — the same addend a is applied n times. Inside one
+// binade of the accumulator (all values sharing one ulp U) each step changes
+// the accumulator by the same whole number of ulps, D = round(a / U), so n
+// steps collapse to one multiplication:
+//
+//   ascending   s + a  ->  s + D*U   valid while the exact result stays below
+//                                    the binade's top (m + D <= 2^P - 1);
+//   descending  c - a  ->  c - D*U   valid while it stays above the binade's
+//                                    bottom (m - D >= 2^(P-1) + 1).
+//
+// (m = s / U is an integer and P is the precision: 24 for float, 53 for
+// double.) Ties to even make a step depend on the parity of m when a / U has
+// fraction exactly 1/2: the result is the even one of the two neighbours, so
+// from an even m every step adds (or removes) the even one of floor(a/U) and
+// floor(a/U) + 1, and from an odd m one ordinary rounded operation makes m
+// even first. The step
+// that leaves the binade is also taken as an ordinary operation, after which
+// the next binade's ulp applies. A run of n equal addends therefore costs
+// O(binades crossed + ties) operations instead of O(n).
+//
+// Everything is held exactly in double: accumulator values are float or
+// double numbers, m < 2^53, and a / U is a power-of-two scaling of a float.
+// Host and device share this code; tests/cpp/chain_check.hip compares it with
+// plain loops on the CPU.
+#pragma once
+
+#include <stdint.h>
+
+#include <cmath>
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define GE_CHAIN_HD __host__ __device__ inline
+#else
+#define GE_CHAIN_HD inline
+#endif
+
+#pragma clang fp contract(off)
+
+namespace ge {
+namespace chain {
+
+template <typename Acc>
+struct AccTraits;
+template <>
+struct AccTraits<float> {
+    static constexpr int P = 24;          // significand bits
+    static constexpr int kMinNormalExp = -126;
+};
+template <>
+struct AccTraits<double> {
+    static constexpr int P = 53;
+    static constexpr int kMinNormalExp = -1022;
+};
+
+constexpr uint64_t kNone = ~static_cast<uint64_t>(0);
+
+struct Binade {
+    int uexp;     // ulp U = 2^uexp
+    uint64_t m;   // accumulator / U
+    uint64_t hi;  // largest m an ascending step may produce and stay exact
+    uint64_t lo;  // smallest m a descending step may produce and stay exact
+};
+
+GE_CHAIN_HD uint64_t dbits(double d) { return __builtin_bit_cast(uint64_t, d); }
+
+// Binade of s >= 0 (finite, representable in Acc). Values below the first
+// normal binade share its ulp, so [0, 2^(kMinNormalExp+1)) is one region in
+// which every operation on Acc numbers is exact.
+template <typename Acc>
+GE_CHAIN_HD Binade binade_of(double s) {
+    constexpr int P = AccTraits<Acc>::P;
+    Binade b;
+    b.hi = (static_cast<uint64_t>(1) << P) - 1;
+    const int ex = static_cast<int>((dbits(s) >> 52) & 0x7ff);
+    const int e = ex - 1023;  // s in [2^e, 2^(e+1)) for normal doubles
+    if (s == 0.0 || ex == 0 || e <= AccTraits<Acc>::kMinNormalExp) {
+        b.uexp = AccTraits<Acc>::kMinNormalExp - (P - 1);
+        b.lo = 1;
+    } else {
+        b.uexp = e - (P - 1);
+        b.lo = (static_cast<uint64_t>(1) << (P - 1)) + 1;
+    }
+    b.m = static_cast<uint64_t>(std::ldexp(s, -b.uexp));
+    return b;
+}
+
+// Increment of one step of addend a >= 0 in binade b: D = a / U rounded to
+// the nearest integer. tie: the fraction is exactly 1/2, and D is then the
+// even neighbour (the increment from an even m); big: a alone reaches the
+// binade's top (the step leaves the binade at once).
+struct Step {
+    uint64_t D;
+    bool tie;
+    bool big;
+};
+
+template <typename Acc>
+GE_CHAIN_HD Step step_of(const Binade& b, double a) {
+    constexpr int P = AccTraits<Acc>::P;
+    Step st{0, false, false};
+    if (a >= std::ldexp(1.0, b.uexp + P)) {
+        st.big = true;
+        return st;
+    }
+    const double A = std::ldexp(a, -b.uexp);
+    const double D0 = std::floor(A);
+    const double f = A - D0;
+    const uint64_t d0 = static_cast<uint64_t>(D0);
+    st.tie = f == 0.5;
+    st.D = st.tie ? d0 + (d0 & 1u) : d0 + (f > 0.5 ? 1u : 0u);
+    return st;
+}
+
+template <typename Acc>
+GE_CHAIN_HD double add_once(double s, double a) {
+    return static_cast<double>(static_cast<Acc>(s) + static_cast<Acc>(a));
+}
+template <typename Acc>
+GE_CHAIN_HD double sub_once(double s, double a) {
+    return static_cast<double>(static_cast<Acc>(s) - static_cast<Acc>(a));
+}
+
+// Smallest m whose value m * 2^uexp is >= thr (thr > 0, below the binade top).
+GE_CHAIN_HD uint64_t threshold_m(double thr, int uexp) {
+    return static_cast<uint64_t>(std::ceil(std::ldexp(thr, -uexp)));
+}
+
+// s <- s + a applied n times in Acc arithmetic, as a left-to-right loop would.
+// thr: stop at the first step whose result is >= thr (NaN: never). Returns the
+// number of steps taken (including the stopping one); hit tells whether the
+// threshold stopped it.
+template <typename Acc>
+GE_CHAIN_HD uint64_t asc_run(double& s, double a, uint64_t n, double thr, bool& hit) {
+    constexpr int P = AccTraits<Acc>::P;
+    hit = false;
+    uint64_t done = 0;
+    while (done < n) {
+        if (!(a > 0.0)) {  // a == 0: the value never changes
+            if (s >= thr) {
+                hit = true;
+                return done + 1;
+            }
+            return n;
+        }
+        if (s == 0.0) {    // 0 + a == a exactly
+            s = add_once<Acc>(s, a);
+            ++done;
+            if (s >= thr) {
+                hit = true;
+                return done;
+            }
+            continue;
+        }
+        Binade b = binade_of<Acc>(s);
+        const Step st = step_of<Acc>(b, a);
+        if (st.big || (st.tie && (b.m & 1u))) {
+            s = add_once<Acc>(s, a);
+            ++done;
+            if (s >= thr) {
+                hit = true;
+                return done;
+            }
+            continue;
+        }
+        const uint64_t rem = n - done;
+        const uint64_t jv = st.D ? (b.hi - b.m) / st.D : kNone;  // steps that stay exact
+        uint64_t jh = kNone;                                     // steps to reach thr
+        if (thr == thr) {
+            if (!(thr > 0.0)) {
+                jh = 1;
+            } else if (thr < std::ldexp(1.0, b.uexp + P)) {
+                const uint64_t tm = threshold_m(thr, b.uexp);
+                if (b.m >= tm) jh = 1;
+                else if (st.D) jh = (tm - b.m + st.D - 1) / st.D;
+            }
+        }
+        uint64_t j = rem < jv ? rem : jv;
+        if (jh < j) j = jh;
+        b.m += j * st.D;
+        s = std::ldexp(static_cast<double>(b.m), b.uexp);
+        done += j;
+        if (j == jh) {
+            hit = true;
+            return done;
+        }
+        if (done < n) {    // the step that leaves the binade
+            s = add_once<Acc>(s, a);
+            ++done;
+            if (s >= thr) {
+                hit = true;
+                return done;
+            }
+        }
+    }
+    return n;
+}
+
+// c <- c - a applied up to n times in Acc arithmetic, stopping before the
+// first step at which c <= a (the reference's `choice -= p; if (choice <= 0)`:
+// c - a rounds to <= 0 exactly when c <= a). Returns the number of steps
+// taken before the stop (stop = true), or n.
+template <typename Acc>
+GE_CHAIN_HD uint64_t desc_run(double& c, double a, uint64_t n, bool& stop) {
+    stop = false;
+    uint64_t done = 0;
+    while (done < n) {
+        if (c <= a) {
+            stop = true;
+            return done;
+        }
+        if (!(a > 0.0)) return n;  // c - 0 == c
+        Binade b = binade_of<Acc>(c);
+        const Step st = step_of<Acc>(b, a);  // a < c, so never big
+        if (st.tie && (b.m & 1u)) {
+            c = sub_once<Acc>(c, a);
+            ++done;
+            continue;
+        }
+        if (st.D == 0 && b.m >= b.lo) return n;  // rounds back to c forever
+        const uint64_t jv = (st.D && b.m >= b.lo) ? (b.m - b.lo) / st.D : 0;
+        const uint64_t rem = n - done;
+        const uint64_t j = rem < jv ? rem : jv;
+        b.m -= j * st.D;
+        c = std::ldexp(static_cast<double>(b.m), b.uexp);
+        done += j;
+        if (done < n) {    // the step that leaves the binade, or a stop
+            if (c <= a) {
+                stop = true;
+                return done;
+            }
+            c = sub_once<Acc>(c, a);
+            ++done;
+        }
+    }
+    return n;
+}
+
+}  // namespace chain
+}  // namespace ge

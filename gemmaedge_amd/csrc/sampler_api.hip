@@ -26,6 +26,16 @@ struct ge_sampler {
     uint32_t* chunk_count;
     uint64_t* cand;
     int64_t cand_stride;
+    // Full-order path (bf16 rows with k > kMaxTopK); allocated when max_vocab > kMaxTopK.
+    uint64_t* fo_items;
+    float* fo_aux;
+    uint32_t* fo_pre;
+    uint64_t* fo_extras;
+    uint32_t* fo_bitmap;
+    uint32_t* fo_meta;
+    int64_t fo_items_stride;
+    int32_t fo_extras_cap;
+    int64_t fo_bitmap_words;
 };
 
 namespace {
@@ -121,6 +131,20 @@ int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, 
     alloc(reinterpret_cast<void**>(&s->chunk_count), rows * ge::kMaxChunks * sizeof(uint32_t));
     alloc(reinterpret_cast<void**>(&s->cand), rows * static_cast<size_t>(s->cand_stride) * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMemset(s->tickets, 0, rows * sizeof(uint32_t));
+    if (max_vocab > ge::kMaxTopK) {
+        s->fo_items_stride = ge::fo_items_stride(max_history);
+        s->fo_extras_cap = max_history < ge::kFoExtrasCap ? (max_history > 0 ? max_history : 1) : ge::kFoExtrasCap;
+        s->fo_bitmap_words = (static_cast<int64_t>(max_vocab) + 31) / 32;
+        const size_t items = rows * static_cast<size_t>(s->fo_items_stride);
+        const size_t words = rows * static_cast<size_t>(s->fo_bitmap_words);
+        alloc(reinterpret_cast<void**>(&s->fo_items), items * sizeof(uint64_t));
+        alloc(reinterpret_cast<void**>(&s->fo_aux), items * sizeof(float));
+        alloc(reinterpret_cast<void**>(&s->fo_pre), items * sizeof(uint32_t));
+        alloc(reinterpret_cast<void**>(&s->fo_extras), rows * static_cast<size_t>(s->fo_extras_cap) * sizeof(uint64_t));
+        alloc(reinterpret_cast<void**>(&s->fo_bitmap), words * sizeof(uint32_t));
+        alloc(reinterpret_cast<void**>(&s->fo_meta), rows * 4 * sizeof(uint32_t));
+        if (e == hipSuccess) e = hipMemset(s->fo_bitmap, 0, words * sizeof(uint32_t));
+    }
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         ge_sampler_destroy(s);
@@ -136,6 +160,12 @@ void ge_sampler_destroy(ge_sampler* s) {
     (void)hipFree(s->tickets);
     (void)hipFree(s->chunk_count);
     (void)hipFree(s->cand);
+    (void)hipFree(s->fo_items);
+    (void)hipFree(s->fo_aux);
+    (void)hipFree(s->fo_pre);
+    (void)hipFree(s->fo_extras);
+    (void)hipFree(s->fo_bitmap);
+    (void)hipFree(s->fo_meta);
     delete s;
 }
 
@@ -161,16 +191,27 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     const bool maybe_sampling = x.row_params != nullptr || !(x.params.temperature <= 0.0f);
     if (maybe_sampling && !x.uniforms) return fail(GE_ERR_INVALID_ARG, "uniforms required when sampling");
 
+    // Rows with k > kMaxTopK (top-k disabled or large) take the full-order
+    // kernels, which this build has for bf16 logits.
     int gpt = 16;
+    bool run_select = true;
+    bool run_full = false;
     if (!x.row_params) {
         const ge_sample_params& p = x.params;
         const uint32_t v = static_cast<uint32_t>(x.vocab);
         const uint32_t k = p.temperature <= 0.0f ? 1u : (p.top_k ? (p.top_k < v ? p.top_k : v) : v);
-        if (k > static_cast<uint32_t>(ge::kMaxTopK))
-            return fail(GE_ERR_UNSUPPORTED, "effective top_k %u above %d (full-order path not built)",
-                        k, ge::kMaxTopK);
+        if (k > static_cast<uint32_t>(ge::kMaxTopK)) {
+            if (x.dtype != GE_DTYPE_BF16)
+                return fail(GE_ERR_UNSUPPORTED, "effective top_k %u above %d needs bf16 logits in this build",
+                            k, ge::kMaxTopK);
+            run_select = false;
+            run_full = true;
+        }
         gpt = k <= 64 ? 1 : (k <= 256 ? 4 : 16);
+    } else {
+        run_full = x.dtype == GE_DTYPE_BF16 && x.vocab > ge::kMaxTopK;
     }
+    if (run_full && !s->fo_items) return fail(GE_ERR_CAPACITY, "handle has no full-order workspace");
 
     // Launch geometry: 64 logits per thread when there are enough rows to fill
     // the chip, else 16 so a single row still spreads over 64+ workgroups.
@@ -208,11 +249,27 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     a.cpr = cpr;
     a.chunk_len = chunk_len;
     a.vec_ok = vec_ok ? 1 : 0;
+    a.fo_items = s->fo_items;
+    a.fo_aux = s->fo_aux;
+    a.fo_pre = s->fo_pre;
+    a.fo_extras = s->fo_extras;
+    a.fo_bitmap = s->fo_bitmap;
+    a.fo_meta = s->fo_meta;
+    a.fo_items_stride = s->fo_items_stride;
+    a.fo_extras_cap = s->fo_extras_cap;
+    a.fo_bitmap_words = s->fo_bitmap_words;
 
     DeviceGuard guard(s->device);
     if (!guard.ok) return fail(GE_ERR_DEVICE, "hipSetDevice(%d) failed", s->device);
-    const hipError_t e = ge::launch_select(a, static_cast<hipStream_t>(stream), ept, gpt);
-    if (e != hipSuccess) return hip_fail(e, "launch");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (run_select) {
+        const hipError_t e = ge::launch_select(a, st, ept, gpt);
+        if (e != hipSuccess) return hip_fail(e, "launch");
+    }
+    if (run_full) {
+        const hipError_t e = ge::launch_full_order(a, st);
+        if (e != hipSuccess) return hip_fail(e, "launch (full order)");
+    }
     return GE_OK;
 }
 

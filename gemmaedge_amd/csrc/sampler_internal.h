@@ -44,10 +44,36 @@ struct DevArgs {
     int32_t cpr;                  // chunks per row
     int32_t chunk_len;            // kBlock * ept
     int32_t vec_ok;               // rows are 16-byte aligned
+
+    // Full-order path workspace (bf16 rows whose k exceeds kMaxTopK); NULL when
+    // the handle's max_vocab cannot produce such rows.
+    uint64_t* fo_items;           // [max_rows * fo_items_stride]  (value bits << 32) | count
+    float* fo_aux;                // [max_rows * fo_items_stride]  per-item probability
+    uint32_t* fo_pre;             // [max_rows * fo_items_stride]  elements before the item
+    uint64_t* fo_extras;          // [max_rows * fo_extras_cap]    penalised tokens, composite keys
+    uint32_t* fo_bitmap;          // [max_rows * fo_bitmap_words]  history bitmap, zero between calls
+    uint32_t* fo_meta;            // [max_rows * 4]                items, extras, NaN count, status
+    int64_t fo_items_stride;
+    int32_t fo_extras_cap;        // <= kFoExtrasCap
+    int64_t fo_bitmap_words;
 };
+
+// Full-order path sizes.
+constexpr int kFoBins = 65536;                 // bf16 order keys
+constexpr int kFoNonNanBins = 65536 - 254;     // bf16 patterns that are not NaN
+constexpr int kFoExtrasCap = 8192;             // penalised tokens per row it handles
+
+inline int64_t fo_items_stride(int max_history) {
+    const int64_t extras = max_history < kFoExtrasCap ? (max_history > 0 ? max_history : 0) : kFoExtrasCap;
+    return (kFoNonNanBins + extras + 1 + 63) / 64 * 64;
+}
 
 // Launches the fused select/sample kernel for rows whose k <= kMaxTopK.
 // ept in {16, 64}; gpt in {1, 4, 16}. Returns a hipError_t.
 hipError_t launch_select(const DevArgs& a, hipStream_t stream, int ept, int gpt);
+
+// Launches the two full-order kernels (bf16 rows with k > kMaxTopK; other
+// rows are skipped). Returns a hipError_t.
+hipError_t launch_full_order(const DevArgs& a, hipStream_t stream);
 
 }  // namespace ge

@@ -754,6 +754,9 @@ __global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
                               : (p.top_k ? min(p.top_k, static_cast<uint32_t>(V))
                                          : static_cast<uint32_t>(V));  // generation.cpp:80
     if (k > static_cast<uint32_t>(kMaxTopK)) {
+        // bf16 rows belong to the full-order kernels, which the host launches
+        // whenever the handle has their workspace.
+        if (a.dtype == GE_DTYPE_BF16 && a.fo_items) return;
         if (chunk == 0 && tid == 0) {
             a.tokens[row] = -1;
             if (a.probs) a.probs[row] = 0.0f;
