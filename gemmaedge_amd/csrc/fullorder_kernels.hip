@@ -117,13 +117,42 @@ __device__ __forceinline__ double rld(double v, int lane) {
     return __builtin_bit_cast(double, rl64(__builtin_bit_cast(uint64_t, v), lane));
 }
 
+// Wave-wide inclusive scans with DPP (no LDS round trips): row_shr 1, 2, 4,
+// 8 scan each row of 16 lanes (lanes shifted in from outside the row read
+// 0), then row_bcast 15 / 31 carry row totals into rows 1, 3 and 2, 3.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(x), kCtrl, kRowMask, 0xf, true));
+}
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ double dpp_f64(double x) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = dpp_u32<kCtrl, kRowMask>(static_cast<uint32_t>(b));
+    const uint32_t hi = dpp_u32<kCtrl, kRowMask>(static_cast<uint32_t>(b >> 32));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
+
 __device__ __forceinline__ uint32_t wave_incl_u32(uint32_t v) {
-    const int lane = __lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t t = __shfl_up(v, d, 64);
-        if (lane >= d) v += t;
-    }
+    v += dpp_u32<kRowShr1, 0xf>(v);
+    v += dpp_u32<kRowShr2, 0xf>(v);
+    v += dpp_u32<kRowShr4, 0xf>(v);
+    v += dpp_u32<kRowShr8, 0xf>(v);
+    v += dpp_u32<kRowBcast15, 0xa>(v);
+    v += dpp_u32<kRowBcast31, 0xc>(v);
+    return v;
+}
+
+// Exact while every partial sum stays below 2^53.
+__device__ __forceinline__ double wave_incl_f64(double v) {
+    v += dpp_f64<kRowShr1, 0xf>(v);
+    v += dpp_f64<kRowShr2, 0xf>(v);
+    v += dpp_f64<kRowShr4, 0xf>(v);
+    v += dpp_f64<kRowShr8, 0xf>(v);
+    v += dpp_f64<kRowBcast15, 0xa>(v);
+    v += dpp_f64<kRowBcast31, 0xc>(v);
     return v;
 }
 
@@ -143,8 +172,8 @@ __device__ __forceinline__ uint64_t wave_incl_u64_sat(uint64_t v) {
 }
 
 __device__ __forceinline__ uint64_t sat_mul(uint64_t n, uint64_t d) {
-    if (n == 0 || d == 0) return 0;
-    return d > kSat / n ? kSat : n * d;
+    const uint64_t lo = n * d;
+    return (__umul64hi(n, d) != 0 || lo > kSat) ? kSat : lo;
 }
 
 // Block-wide exclusive scan of one u32 per thread; returns the total too.
@@ -199,6 +228,129 @@ __device__ __forceinline__ uint32_t bin_count(const HistShared& sh, uint32_t bin
     uint32_t c = (sh.hist[bin_word(bin)] >> bin_shift(bin)) & 0xFFFFu;
     for (uint32_t i = 0; i < nspill; ++i) c += sh.spill[i] == bin ? 32768u : 0u;
     return c;
+}
+
+// Counts two bf16 tokens (one 32-bit word) without branches: a token with
+// sign s and bits x has bin x | 0x8000 (s = 0: high field of word x & 0x7FFF)
+// or ~x & 0xFFFF (s = 1: low field of word (x ^ 0x7FFF) & 0x7FFF). skip bit 0 /
+// bit 1 drop the low / high token.
+__device__ __forceinline__ void count_pair(HistShared& sh, uint32_t x, uint32_t skip) {
+    const uint32_t sg = (x >> 15) & 0x00010001u;
+    const uint32_t y = x ^ (sg * 0x7FFFu);
+    const uint32_t inc_lo = (skip & 1u) ? 0u : (0x10000u >> ((sg & 1u) << 4));
+    const uint32_t inc_hi = (skip & 2u) ? 0u : (0x10000u >> ((sg >> 16) << 4));
+    atomicAdd(&sh.hist[y & 0x7FFFu], inc_lo);
+    atomicAdd(&sh.hist[(y >> 16) & 0x7FFFu], inc_hi);
+}
+
+// Moves every field that reached 32768 to the spill list. At most kSubChunk
+// counts arrive between sweeps, so a field below 32768 after a sweep cannot
+// pass 65535 before the next one. Reads four words at a time and rejects
+// them together in the common case that no field has its top bit set.
+__device__ __forceinline__ void sweep(HistShared& sh, int tid) {
+    __syncthreads();
+    uint4* h4 = reinterpret_cast<uint4*>(sh.hist);
+    for (uint32_t q = tid; q < kWords / 4; q += kThreads) {
+        const uint4 x4 = h4[q];
+        if (((x4.x | x4.y | x4.z | x4.w) & 0x80008000u) == 0u) continue;
+        const uint32_t xs[4] = {x4.x, x4.y, x4.z, x4.w};
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = 4 * q + i;
+            const uint32_t x = xs[i];
+            uint32_t sub = 0;
+            if ((x & 0xFFFFu) >= 0x8000u) {
+                sub += 0x8000u;
+                const uint32_t sp = atomicAdd(&sh.counters[1], 1u);
+                if (sp < kSpillCap) sh.spill[sp] = w;
+            }
+            if ((x >> 16) >= 0x8000u) {
+                sub += 0x80000000u;
+                const uint32_t sp = atomicAdd(&sh.counters[1], 1u);
+                if (sp < kSpillCap) sh.spill[sp] = w + kWords;
+            }
+            if (sub) sh.hist[w] = x - sub;
+        }
+    }
+    __syncthreads();
+}
+
+// Streams one row into the histogram. PEN: skip the tokens marked in the
+// row's history bitmap. The loop is software-pipelined: the next sub-chunk's
+// 16-byte loads are in flight while this one is counted and swept (the two
+// variants keep the bitmap loads out of the unpenalised loop, so its wait
+// counts only cover the data being counted).
+template <bool PEN>
+__device__ __forceinline__ void stream_row(HistShared& sh, const uint16_t* rowp, int V, bool vec,
+                                           const uint32_t* bitmap, int tid) {
+    constexpr int kVec = kSubChunk / (kThreads * 8);  // uint4 of 8 tokens per thread per sub-chunk
+    const int vec_end = vec ? (V / kSubChunk) * kSubChunk : 0;
+    if (vec_end > 0) {
+        uint4 cur[kVec];
+        uint32_t cbm[kVec];
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) {
+            const int pos = (j * kThreads + tid) * 8;
+            cur[j] = *reinterpret_cast<const uint4*>(rowp + pos);
+            cbm[j] = PEN ? (bitmap[pos >> 5] >> (pos & 31)) : 0u;
+        }
+        auto count_cur = [&]() {
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) {
+                count_pair(sh, cur[j].x, cbm[j] & 3u);
+                count_pair(sh, cur[j].y, (cbm[j] >> 2) & 3u);
+                count_pair(sh, cur[j].z, (cbm[j] >> 4) & 3u);
+                count_pair(sh, cur[j].w, (cbm[j] >> 6) & 3u);
+            }
+        };
+        // Two sub-chunks ahead: cur is counted while nxt and nxt2 load.
+        uint4 nxt[kVec];
+        uint32_t nbm[kVec];
+        auto load_into = [&](uint4* q, uint32_t* bm, int base) {
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) {
+                const int pos = base + (j * kThreads + tid) * 8;
+                q[j] = *reinterpret_cast<const uint4*>(rowp + pos);
+                bm[j] = PEN ? (bitmap[pos >> 5] >> (pos & 31)) : 0u;
+            }
+        };
+        if (kSubChunk < vec_end) load_into(nxt, nbm, kSubChunk);
+        int base = 0;
+        for (; base + 2 * kSubChunk < vec_end; base += kSubChunk) {
+            uint4 nxt2[kVec];
+            uint32_t nbm2[kVec];
+            load_into(nxt2, nbm2, base + 2 * kSubChunk);
+            count_cur();
+            sweep(sh, tid);
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) {
+                cur[j] = nxt[j];
+                cbm[j] = nbm[j];
+                nxt[j] = nxt2[j];
+                nbm[j] = nbm2[j];
+            }
+        }
+        if (base + kSubChunk < vec_end) {  // second to last
+            count_cur();
+            sweep(sh, tid);
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) {
+                cur[j] = nxt[j];
+                cbm[j] = nbm[j];
+            }
+        }
+        count_cur();
+        sweep(sh, tid);
+    }
+    for (int base = vec_end; base < V; base += kSubChunk) {
+        for (int j = 0; j < kSubChunk / kThreads; ++j) {
+            const int idx = base + j * kThreads + tid;
+            if (idx < V) {
+                const bool skip = PEN && ((bitmap[idx >> 5] >> (idx & 31)) & 1u);
+                count_pair(sh, rowp[idx], skip ? 3u : 2u);  // the pair's high token is empty
+            }
+        }
+        sweep(sh, tid);
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
@@ -305,113 +457,84 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
     for (uint32_t w = tid; w < kWords; w += kThreads) sh.hist[w] = 0u;
     __syncthreads();
 
-    auto count_token = [&](uint32_t bits16) {
-        const uint32_t bin = bin_of(bits16);
-        atomicAdd(&sh.hist[bin_word(bin)], 1u << bin_shift(bin));
-    };
-    auto penalised = [&](int idx) -> bool {
-        return pen && ((bitmap[idx >> 5] >> (idx & 31)) & 1u);
-    };
-    const bool vec = a.vec_ok != 0;
-    constexpr int kVecPerThread = kSubChunk / (kThreads * 8);  // 4 uint4 of 8 bf16
-    for (int base = 0; base < V; base += kSubChunk) {
-        if (vec && base + kSubChunk <= V) {
-            uint4 q[kVecPerThread];
-            uint32_t bm[kVecPerThread];
-#pragma unroll
-            for (int j = 0; j < kVecPerThread; ++j) {
-                const int pos = base + (j * kThreads + tid) * 8;
-                q[j] = *reinterpret_cast<const uint4*>(rowp + pos);
-                bm[j] = pen ? (bitmap[pos >> 5] >> (pos & 31)) : 0u;
-            }
-#pragma unroll
-            for (int j = 0; j < kVecPerThread; ++j) {
-                const uint32_t w4[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
-#pragma unroll
-                for (int h = 0; h < 8; ++h) {
-                    if ((bm[j] >> h) & 1u) continue;
-                    count_token((w4[h >> 1] >> ((h & 1) * 16)) & 0xFFFFu);
-                }
-            }
-        } else {
-            for (int j = 0; j < kSubChunk / kThreads; ++j) {
-                const int idx = base + j * kThreads + tid;
-                if (idx < V && !penalised(idx)) count_token(rowp[idx]);
-            }
-        }
-        __syncthreads();
-        // Sweep: at most kSubChunk counts arrive between sweeps, so a field
-        // below 32768 after a sweep cannot pass 65535 before the next one.
-        for (uint32_t w = tid; w < kWords; w += kThreads) {
-            const uint32_t x = sh.hist[w];
-            uint32_t sub = 0;
-            if ((x & 0xFFFFu) >= 0x8000u) {
-                sub += 0x8000u;
-                const uint32_t s = atomicAdd(&sh.counters[1], 1u);
-                if (s < kSpillCap) sh.spill[s] = w;
-            }
-            if ((x >> 16) >= 0x8000u) {
-                sub += 0x80000000u;
-                const uint32_t s = atomicAdd(&sh.counters[1], 1u);
-                if (s < kSpillCap) sh.spill[s] = w + kWords;
-            }
-            if (sub) sh.hist[w] = x - sub;
-        }
-        __syncthreads();
-    }
+    if (pen) stream_row<true>(sh, rowp, V, a.vec_ok != 0, bitmap, tid);
+    else stream_row<false>(sh, rowp, V, a.vec_ok != 0, bitmap, tid);
     const uint32_t nspill = min(sh.counters[1], static_cast<uint32_t>(kSpillCap));
 
-    // 3. Items in descending order. Thread t owns bins hb - j, j = 0..63,
-    //    hb = 65535 - 64 t (bit j of its mask).
-    const uint32_t hb = 65535u - 64u * static_cast<uint32_t>(tid);
-    uint64_t mask = 0;
+    // 3. Items in descending order. Wave w owns bins 65535 - 4096 w - 64 j - l
+    //    for j = 0..63 (step) and l = 0..63 (lane): each step reads 64
+    //    consecutive histogram words. Group g = 64 w + j has mask sh.mask[g]
+    //    (bit l: non-empty, non-NaN) and sh.off[g] items before it.
+    const int lane = __lane_id();
+    const int wave = tid >> 6;
+    const uint32_t wtop = 65535u - 4096u * static_cast<uint32_t>(wave);
+    uint32_t wcount = 0;
     uint32_t nan_local = 0;
     for (int j = 0; j < 64; ++j) {
-        const uint32_t bin = hb - j;
+        const uint32_t bin = wtop - 64u * j - lane;
         const uint32_t c = bin_count(sh, bin, nspill);
-        if (c) {
-            if (bin_is_nan(bin)) nan_local += c;
-            else mask |= 1ull << j;
-        }
+        const bool nz = c != 0 && !bin_is_nan(bin);
+        if (c && bin_is_nan(bin)) nan_local += c;
+        const uint64_t m = __ballot(nz);
+        if (lane == 0) sh.mask[wave * 64 + j] = m;
+        wcount += static_cast<uint32_t>(__popcll(m));
     }
-    uint32_t nbins_total;
-    const uint32_t off = block_excl_scan(static_cast<uint32_t>(__popcll(mask)), sh.scan, nbins_total);
-    sh.off[tid] = off;
-    sh.mask[tid] = mask;
+    if (lane == 0) sh.scan[wave] = wcount;
     if (nan_local) atomicAdd(&sh.counters[2], nan_local);
     __syncthreads();
-
-    // Bin items: position = bins before + penalised tokens with a larger final value.
-    {
-        uint32_t c = 0;  // penalised tokens with thr_bin > bin (thr_bin is non-increasing)
-        {
-            uint32_t lo = 0, hi = E;
-            while (lo < hi) {
-                const uint32_t mid = (lo + hi) >> 1;
-                if (sh.thr_bin[mid] > hb) lo = mid + 1;
-                else hi = mid;
-            }
-            c = lo;
-        }
-        uint32_t rank = 0;
+    uint32_t nbins_total = 0;
+    uint32_t wbefore = 0;
+    for (int w = 0; w < kWaves; ++w) {
+        const uint32_t x = sh.scan[w];
+        if (w < wave) wbefore += x;
+        nbins_total += x;
+    }
+    if (lane == 0) {
+        uint32_t run = wbefore;
         for (int j = 0; j < 64; ++j) {
-            if (!((mask >> j) & 1u)) continue;
-            const uint32_t bin = hb - j;
-            while (c < E && sh.thr_bin[c] > bin) ++c;
-            const uint32_t cnt = bin_count(sh, bin, nspill);
-            items[off + rank + c] = (static_cast<uint64_t>(f2u(bin_value(bin, cap))) << 32) | cnt;
-            ++rank;
+            sh.off[wave * 64 + j] = run;
+            run += static_cast<uint32_t>(__popcll(sh.mask[wave * 64 + j]));
         }
+    }
+    __syncthreads();
+
+    // Bin items, in two passes: first (bin, count) pairs at their rank among
+    // the bins, staged in the decide kernel's per-item arrays (unused until
+    // then); then, densely over all threads, the final value of each and its
+    // place among the penalised items.
+    uint32_t* stage_bin = reinterpret_cast<uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
+    uint32_t* stage_cnt = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
+    for (int j = 0; j < 64; ++j) {
+        const int g = wave * 64 + j;
+        const uint64_t m = sh.mask[g];
+        if (!((m >> lane) & 1u)) continue;
+        const uint32_t bin = wtop - 64u * j - lane;
+        const uint32_t r = sh.off[g] + static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1)));
+        stage_bin[r] = bin;
+        stage_cnt[r] = bin_count(sh, bin, nspill);
+    }
+    __syncthreads();
+    for (uint32_t r = tid; r < nbins_total; r += kThreads) {
+        const uint32_t bin = stage_bin[r];
+        uint32_t c = 0;  // penalised tokens with thr_bin > bin (thr_bin is non-increasing)
+        uint32_t lo = 0, hi = E;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (sh.thr_bin[mid] > bin) lo = mid + 1;
+            else hi = mid;
+        }
+        c = lo;
+        items[r + c] = (static_cast<uint64_t>(f2u(bin_value(bin, cap))) << 32) | stage_cnt[r];
     }
     // Penalised items: position = own rank + bins with a final value >= its own.
     for (uint32_t e = tid; e < E; e += kThreads) {
         const uint32_t tb = sh.thr_bin[e];
         uint32_t nb = 0;
         if (tb <= kHighBin) {
-            const uint32_t t = (65535u - tb) >> 6;
-            const uint32_t jt = (65535u - 64u * t) - tb;  // bit of bin tb in thread t's mask
-            const uint64_t upto = jt == 63 ? ~0ull : ((2ull << jt) - 1);
-            nb = sh.off[t] + static_cast<uint32_t>(__popcll(sh.mask[t] & upto));
+            const uint32_t g = (65535u - tb) >> 6;        // group holding bin tb
+            const uint32_t l = (65535u - tb) & 63u;       // its lane: bins >= tb are lanes 0..l
+            const uint64_t upto = l == 63 ? ~0ull : ((2ull << l) - 1);
+            nb = sh.off[g] + static_cast<uint32_t>(__popcll(sh.mask[g] & upto));
         }
         const uint32_t key = composite_key(extras[e]);
         items[e + nb] = (static_cast<uint64_t>(f2u(key_value(key))) << 32) | 1u;
@@ -430,99 +553,222 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
 // ---- kernel 2: probabilities, exact chains, token ----------------------------
 
 struct ChainPos {
-    int item;       // item holding the next (or the event) element
-    uint32_t off;   // elements of that item before it
-    uint32_t elem;  // global element index
+    int item;       // item holding element `elem`
+    uint32_t elem;  // global element index (next to consume, or the event element)
 };
 
-// Replays elements [cp.elem, L) of the accumulation described by items
-// (count in the low 32 bits) and per-item addends, with one wave. kDesc:
-// c -= a, stopping at the first element with c <= a; else s += a, stopping
-// at the first element whose sum is >= thr (NaN: never). On an event returns
-// true with cp at the event element. Otherwise returns false with cp.elem == L
-// and (cp.item, cp.off - 1) the last element consumed. Requires cp.elem < L.
-template <typename Acc, bool kDesc>
-__device__ bool wave_chain(const uint64_t* items, const float* add, int G, ChainPos& cp, uint32_t L,
-                           double& s, double thr) {
+// Item boundaries and addends: start(i) is the index of item i's first
+// element, start(G) the element count. One view reads LDS copies (rows whose
+// items fit), the other the global arrays; each is a single address space,
+// so the compiler emits ds_read or global_load rather than flat loads.
+struct LdsView {
+    const uint32_t* pre;
+    const float* add;
+    __device__ __forceinline__ uint32_t start(int i) const { return pre[i]; }
+    __device__ __forceinline__ float addend(int i) const { return add[i]; }
+};
+struct GlobalView {
+    const uint32_t* pre;
+    const float* add;
+    __device__ __forceinline__ uint32_t start(int i) const { return pre[i]; }
+    __device__ __forceinline__ float addend(int i) const { return add[i]; }
+};
+
+// Replays elements [cp.elem, L) of the accumulation described by the items,
+// with one wave, 64 items per step. kDesc: c -= a, stopping at the first
+// element with c <= a; else s += a, stopping at the first element whose sum
+// is >= thr (NaN: never). Returns true on an event with cp at the event
+// element; otherwise false with cp.elem == L and cp.item holding element L-1.
+// Requires cp.elem < L <= start(G).
+//
+// Each lane takes one item: its increment in the current binade (count x
+// whole ulps) is scanned across the wave; lanes before the first one that
+// would leave the binade, tie or reach the threshold are applied at once,
+// and that lane runs the closed form of chain_math.h.
+template <typename Acc, bool kDesc, typename View>
+__device__ bool wave_chain(const View& iv, int G, ChainPos& cp, uint32_t L, double& s, double thr) {
     constexpr int P = chain::AccTraits<Acc>::P;
+    constexpr bool kF32 = P == 24;
     const int lane = __lane_id();
     while (cp.elem < L && cp.item < G) {
-        const int idx = cp.item + lane;
-        uint32_t n = 0;
+        const int i = cp.item + lane;
+        uint32_t nt = 0, lo_e = 0;
         double av = 0.0;
-        if (idx < G) {
-            n = static_cast<uint32_t>(items[idx]);
-            av = static_cast<double>(add[idx]);
+        if (i < G) {
+            const uint32_t st = iv.start(i);
+            const uint32_t en = iv.start(i + 1);
+            lo_e = max(st, cp.elem);
+            const uint32_t hi_e = min(en, L);
+            nt = hi_e > lo_e ? hi_e - lo_e : 0u;
+            av = static_cast<double>(iv.addend(i));
         }
-        if (lane == 0) n -= cp.off;
-        const uint32_t cincl = wave_incl_u32(n);
-        const uint32_t cexcl = cincl - n;
-        const uint32_t room = L - cp.elem;
-        const uint32_t nt = cexcl >= room ? 0u : min(n, room - cexcl);
         const chain::Binade b = chain::binade_of<Acc>(s);
         const chain::Step st = chain::step_of<Acc>(b, av);
-        const uint64_t tot = (nt && !st.big) ? sat_mul(nt, st.D) : 0;
-        const uint64_t incl = wave_incl_u64_sat(tot);
         bool ev = false;
-        if (nt) {
-            if (kDesc) {
-                // big: a reaches past c's binade, so c <= a and the walk stops here
-                ev = st.big || st.tie || b.m < b.lo + incl;
-            } else {
-                uint64_t tm = chain::kNone;
-                if (thr == thr) {
-                    if (!(thr > 0.0)) tm = 0;
-                    else if (thr < std::ldexp(1.0, b.uexp + P)) tm = chain::threshold_m(thr, b.uexp);
+        double incl_d = 0.0;
+        uint64_t incl_u = 0;
+        if (kF32) {
+            // room in a float binade < 2^24: capping each lane at 2^40 keeps
+            // every partial sum exact in double and every exit detected
+            double tot = 0.0;
+            if (nt && !st.big) tot = min(static_cast<double>(nt) * static_cast<double>(st.D), 1099511627776.0);
+            incl_d = wave_incl_f64(tot);
+            const double m = static_cast<double>(b.m);
+            if (nt) {
+                if (kDesc) {
+                    ev = st.big || st.tie || m - incl_d < static_cast<double>(b.lo);
+                } else {
+                    double tm = 1e300;
+                    if (thr == thr) {
+                        if (!(thr > 0.0)) tm = 0.0;
+                        else if (thr < std::ldexp(1.0, b.uexp + P))
+                            tm = static_cast<double>(chain::threshold_m(thr, b.uexp));
+                    }
+                    ev = st.big || st.tie || m + incl_d > static_cast<double>(b.hi) || m + incl_d >= tm;
                 }
-                ev = st.big || st.tie || b.m + incl > b.hi || b.m + incl >= tm;
+            }
+        } else {
+            const uint64_t tot = (nt && !st.big) ? sat_mul(nt, st.D) : 0;
+            incl_u = wave_incl_u64_sat(tot);
+            if (nt) {
+                if (kDesc) {
+                    ev = st.big || st.tie || b.m < b.lo + incl_u;
+                } else {
+                    uint64_t tm = chain::kNone;
+                    if (thr == thr) {
+                        if (!(thr > 0.0)) tm = 0;
+                        else if (thr < std::ldexp(1.0, b.uexp + P)) tm = chain::threshold_m(thr, b.uexp);
+                    }
+                    ev = st.big || st.tie || b.m + incl_u > b.hi || b.m + incl_u >= tm;
+                }
             }
         }
+        auto applied = [&](int upto) -> uint64_t {  // ulps added by lanes < upto
+            if (upto == 0) return 0;
+            return kF32 ? static_cast<uint64_t>(rld(incl_d, upto - 1)) : rl64(incl_u, upto - 1);
+        };
         const uint64_t evmask = __ballot(ev);
         if (evmask == 0) {
-            const uint64_t total = rl64(incl, 63);
+            const uint64_t total = applied(64);
             const uint64_t m2 = kDesc ? b.m - total : b.m + total;
             s = std::ldexp(static_cast<double>(m2), b.uexp);
-            const uint32_t all = rl32(cincl, 63);
-            if (all >= room) {  // the last element lies in this tile
-                const uint64_t lm = __ballot(n && cexcl < room && room <= cincl);
-                const int l = static_cast<int>(__builtin_ctzll(lm));
-                const uint32_t before = rl32(cexcl, l);
-                cp.off = (l == 0 ? cp.off : 0u) + (room - before);
-                cp.item += l;
+            const int next = cp.item + 64;
+            const uint32_t tile_end = next < G ? iv.start(next) : iv.start(G);
+            if (tile_end >= L) {  // the last element lies in this tile
+                const uint64_t lm = __ballot(nt && lo_e + nt == L);
+                cp.item += static_cast<int>(__builtin_ctzll(lm));
                 cp.elem = L;
                 return false;
             }
-            cp.elem += all;
-            cp.item += 64;
-            cp.off = 0;
+            cp.elem = tile_end;
+            cp.item = next;
             continue;
         }
         const int f = static_cast<int>(__builtin_ctzll(evmask));
-        const uint64_t before = f ? rl64(incl, f - 1) : 0;
+        const uint64_t before = applied(f);
         const uint64_t m2 = kDesc ? b.m - before : b.m + before;
         s = std::ldexp(static_cast<double>(m2), b.uexp);
-        cp.elem += rl32(cexcl, f);
+        cp.elem = rl32(lo_e, f);
         const uint32_t nf = rl32(nt, f);
         const double af = rld(av, f);
-        const uint32_t offf = f == 0 ? cp.off : 0u;
         bool evt = false;
         const uint64_t used = kDesc ? chain::desc_run<Acc>(s, af, nf, evt)
                                     : chain::asc_run<Acc>(s, af, nf, thr, evt);
         cp.item += f;
         if (evt) {
-            const uint32_t at = static_cast<uint32_t>(kDesc ? used : used - 1);
-            cp.off = offf + at;
-            cp.elem += at;
+            cp.elem += static_cast<uint32_t>(kDesc ? used : used - 1);
+            return true;
+        }
+        cp.elem += nf;
+        if (cp.elem >= L) return false;
+        cp.item += 1;
+    }
+    return false;
+}
+
+// The same walk for a float accumulator, in 32-bit integer arithmetic: the
+// accumulator is carried as its float bits, each lane's increment comes from
+// the bit fields of its addend (chain_math.h step_bits), increments are capped
+// at 2^24 (more than any binade holds, so the cap never hides an exit) and
+// scanned as u32 with DPP. Addends are floats, read as bits from the view.
+template <bool kDesc, typename View>
+__device__ bool wave_chain_f32(const View& iv, int G, ChainPos& cp, uint32_t L, double& s, double thr) {
+    const int lane = __lane_id();
+    const uint32_t tb = f2u(static_cast<float>(thr));
+    uint32_t sb = f2u(static_cast<float>(s));
+    while (cp.elem < L && cp.item < G) {
+        const int i = cp.item + lane;
+        uint32_t nt = 0, lo_e = 0, ab = 0;
+        if (i < G) {
+            const uint32_t st = iv.start(i);
+            const uint32_t en = iv.start(i + 1);
+            lo_e = max(st, cp.elem);
+            const uint32_t hi_e = min(en, L);
+            nt = hi_e > lo_e ? hi_e - lo_e : 0u;
+            ab = f2u(iv.addend(i));
+        }
+        const chain::StepBits bb = chain::binade_bits(sb);
+        uint32_t D;
+        bool tie, big;
+        chain::step_bits(ab, bb.uexp, D, tie, big);
+        uint32_t tot = 0;
+        if (nt && !big) {
+            const uint32_t lo32 = nt * D;
+            tot = (__umulhi(nt, D) != 0u || lo32 > 0x1000000u) ? 0x1000000u : lo32;
+        }
+        const uint32_t incl = wave_incl_u32(tot);  // <= 2^30
+        bool ev = false;
+        if (nt) {
+            if (kDesc) {
+                ev = big || tie || bb.m < bb.lo + incl;
+            } else {
+                const uint32_t tm = chain::threshold_bits(tb, bb.uexp);
+                ev = big || tie || bb.m + incl > chain::kHiF || bb.m + incl >= tm;
+            }
+        }
+        const uint64_t evmask = __ballot(ev);
+        const int f = evmask ? static_cast<int>(__builtin_ctzll(evmask)) : 64;
+        const uint32_t before = f ? rl32(incl, f - 1) : 0u;
+        const uint32_t m2 = kDesc ? bb.m - before : bb.m + before;
+        // back to float bits: the low region's bits are m itself; a normal
+        // binade keeps its exponent field (m stays in [2^23, 2^24))
+        sb = (sb >> 23) <= 1u ? m2 : ((sb & 0x7F800000u) | (m2 & 0x7FFFFFu));
+        if (f == 64) {
+            const int next = cp.item + 64;
+            const uint32_t tile_end = iv.start(next < G ? next : G);
+            if (tile_end >= L) {  // the last element lies in this tile
+                const uint64_t lm = __ballot(nt && lo_e + nt == L);
+                cp.item += static_cast<int>(__builtin_ctzll(lm));
+                cp.elem = L;
+                s = static_cast<double>(u2f(sb));
+                return false;
+            }
+            cp.elem = tile_end;
+            cp.item = next;
+            continue;
+        }
+        cp.elem = rl32(lo_e, f);
+        const uint32_t nf = rl32(nt, f);
+        const double af = static_cast<double>(u2f(rl32(ab, f)));
+        double sd = static_cast<double>(u2f(sb));
+        bool evt = false;
+        const uint64_t used = kDesc ? chain::desc_run_f32(sd, af, nf, evt)
+                                    : chain::asc_run_f32(sd, af, nf, thr, evt);
+        sb = f2u(static_cast<float>(sd));
+        cp.item += f;
+        if (evt) {
+            cp.elem += static_cast<uint32_t>(kDesc ? used : used - 1);
+            s = sd;
             return true;
         }
         cp.elem += nf;
         if (cp.elem >= L) {
-            cp.off = offf + nf;
+            s = sd;
             return false;
         }
         cp.item += 1;
-        cp.off = 0;
     }
+    s = static_cast<double>(u2f(sb));
     return false;
 }
 
@@ -544,16 +790,25 @@ __device__ int wave_find_item(const uint32_t* pre, int G, uint32_t x) {
     return lo;
 }
 
+constexpr int kDThreads = 512;
+constexpr int kDWaves = kDThreads / 64;
+constexpr int kStage = 8192;  // items whose count and probability are staged in LDS
+
 struct DecideShared {
-    uint32_t gx_ids[kFoExtrasCap];  // penalised tokens of the selected value, ascending
-    double dred[kWaves];
-    int ired[kWaves];
-    uint32_t ured[kWaves];
-    uint32_t scan[kWaves];
+    union {
+        struct {
+            uint32_t pre[kStage + 1];  // item boundaries (elements before each item)
+            float add[kStage];         // per-item probability
+        } st;
+        uint32_t gx_ids[kFoExtrasCap];  // penalised tokens of the selected value, ascending
+    };
+    double dred[kDWaves];
+    int ired[kDWaves];
+    uint32_t ured[kDWaves];
+    uint32_t scan[kDWaves];
     double den;
-    float choice;
-    uint32_t keep, pos, group_rank, group_total, forward, gx_count;
-    uint32_t blo, bhi, nan_group, found;
+    uint32_t pos, group_rank, group_total, forward, gx_count;
+    uint32_t blo, bhi, nan_group, near;
     int32_t token;
     int item;
 };
@@ -565,7 +820,43 @@ __device__ __forceinline__ T wave_reduce(T v, Op op) {
     return v;
 }
 
-__global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
+// Block-wide exclusive scan for kDThreads threads.
+__device__ __forceinline__ uint32_t dblock_excl_scan(uint32_t v, uint32_t* scratch, uint32_t& total) {
+    const int lane = __lane_id();
+    const int wave = threadIdx.x >> 6;
+    const uint32_t incl = wave_incl_u32(v);
+    if (lane == 63) scratch[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < kDWaves; ++w) {
+        const uint32_t x = scratch[w];
+        if (w < wave) before += x;
+        total += x;
+    }
+    __syncthreads();
+    return before + incl - v;
+}
+
+// First index in [lo, hi) whose predicate is false, for a predicate that is
+// true on a prefix; 64-way search with one wave.
+template <typename Pred>
+__device__ uint32_t wave_partition_point(uint32_t lo, uint32_t hi, Pred pred) {
+    const int lane = __lane_id();
+    while (hi > lo) {
+        const uint32_t step = (hi - lo + 63) / 64;
+        const uint32_t probe = lo + static_cast<uint32_t>(lane) * step;
+        const uint64_t m = __ballot(probe < hi && pred(probe));
+        if (m == 0) break;  // pred(lo) is false
+        const int last = 63 - static_cast<int>(__builtin_clzll(m));
+        lo = lo + static_cast<uint32_t>(last) * step + 1;
+        hi = min(hi, lo - 1 + step);
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     __shared__ DecideShared sh;
     const int tid = threadIdx.x;
     const int lane = __lane_id();
@@ -597,7 +888,7 @@ __global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
         // The bitmap is all zero again after every call.
         if (pen) {
             __syncthreads();
-            for (int i = tid; i < H; i += kThreads) {
+            for (int i = tid; i < H; i += kDThreads) {
                 const int32_t id = hist[i];
                 if (id >= 0 && id < V) bitmap[id >> 5] = 0u;
             }
@@ -614,36 +905,41 @@ __global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
     const uint64_t* extras = a.fo_extras + static_cast<int64_t>(row) * a.fo_extras_cap;
     const uint32_t E = meta[kMetaExtras];
 
-    // 4a. Per item: elements before it, exp, certificate of the double sum.
-    //     generation.cpp:94-97: p = exp((l - max) * (1/T)) in float.
+    // 4a. Per item: elements before it, exp, certificate of the double sum;
+    //     512 items per round. generation.cpp:94-97: p = exp((l - max) * (1/T)).
     const float inv_temp = 1.0f / p.temperature;
     const float vmax = u2f(static_cast<uint32_t>(items[0] >> 32));
     const float p0 = expf_glibc((vmax - vmax) * inv_temp);
-    const int per = (G + kThreads - 1) / kThreads;
-    const int i_begin = min(G, tid * per);
-    const int i_end = min(G, i_begin + per);
-    uint32_t local = 0;
-    for (int i = i_begin; i < i_end; ++i) local += static_cast<uint32_t>(items[i]);
-    uint32_t total_elems;
-    uint32_t run = block_excl_scan(local, sh.scan, total_elems);
     double S = 0.0;
     int minlsb = INT_MAX;
     bool nan = false;
-    for (int i = i_begin; i < i_end; ++i) {
-        const uint32_t n = static_cast<uint32_t>(items[i]);
-        pre[i] = run;
-        const uint32_t nk = run >= k ? 0u : min(n, k - run);
-        run += n;
-        const float v = u2f(static_cast<uint32_t>(items[i] >> 32));
-        const float pe = expf_glibc((v - vmax) * inv_temp);
-        aux[i] = pe;
-        if (nk) {
-            if (pe != pe) nan = true;
-            else if (pe > 0.0f) {
-                minlsb = min(minlsb, lsb_exp(pe));
-                S += static_cast<double>(nk) * static_cast<double>(pe);
+    uint32_t run_base = 0;
+    for (int r0 = 0; r0 < G; r0 += kDThreads) {
+        const int i = r0 + tid;
+        const uint64_t it = i < G ? items[i] : 0ull;
+        const uint32_t n = static_cast<uint32_t>(it);
+        uint32_t tot;
+        const uint32_t pi = run_base + dblock_excl_scan(n, sh.scan, tot);
+        run_base += tot;
+        if (i < G) {
+            pre[i] = pi;
+            if (i <= kStage) sh.st.pre[i] = pi;
+            const uint32_t nk = pi >= k ? 0u : min(n, k - pi);
+            const float pe = expf_glibc((u2f(static_cast<uint32_t>(it >> 32)) - vmax) * inv_temp);
+            aux[i] = pe;
+            if (i < kStage) sh.st.add[i] = pe;
+            if (nk) {
+                if (pe != pe) nan = true;
+                else if (pe > 0.0f) {
+                    minlsb = min(minlsb, lsb_exp(pe));
+                    S += static_cast<double>(nk) * static_cast<double>(pe);
+                }
             }
         }
+    }
+    if (tid == 0) {
+        pre[G] = run_base;
+        if (G <= kStage) sh.st.pre[G] = run_base;
     }
     S = wave_reduce(S, [](double x, double y) { return x + y; });
     minlsb = wave_reduce(minlsb, [](int x, int y) { return min(x, y); });
@@ -654,35 +950,31 @@ __global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
         sh.ured[wave] = nanw;
     }
     __syncthreads();
-    if (tid == 0) {
-        double St = 0.0;
-        int ml = INT_MAX;
-        uint32_t nn = 0;
-        for (int w = 0; w < kWaves; ++w) {
-            St += sh.dred[w];
-            ml = min(ml, sh.ired[w]);
-            nn |= sh.ured[w];
-        }
-        sh.dred[0] = St;
-        sh.ired[0] = ml;
-        sh.ured[0] = nn;
+    double Sp = 0.0;
+    int ml = INT_MAX;
+    uint32_t nn = 0;
+    for (int w = 0; w < kDWaves; ++w) {
+        Sp += sh.dred[w];
+        ml = min(ml, sh.ired[w]);
+        nn |= sh.ured[w];
     }
-    __syncthreads();
-    const bool any_nan = sh.ured[0] != 0;
+    const bool any_nan = nn != 0;
     // Every term is a multiple of 2^minlsb; if the sum needs at most 53 bits
     // above that, every partial sum in every order is exact, so the parallel
     // sum equals the reference's sequential one (generation.cpp:97).
-    const double Sp = sh.dred[0];
-    const bool certified = !any_nan && (Sp == 0.0 || sh.ired[0] >= exp_of(Sp) - 51);
+    const bool certified = !any_nan && (Sp == 0.0 || ml >= exp_of(Sp) - 51);
     if (wave == 0) {
         double den = Sp;
         if (any_nan) {
             den = __builtin_nan("");
         } else if (!certified) {
-            ChainPos cp{0, 1, 1};
-            double s = static_cast<double>(p0);
-            if (k > 1) wave_chain<double, false>(items, aux, G, cp, k, s, __builtin_nan(""));
-            den = s;
+            ChainPos cp{0, 1};
+            double s2 = static_cast<double>(p0);
+            if (k > 1) {
+                if (G <= kStage) wave_chain<double, false>(LdsView{sh.st.pre, sh.st.add}, G, cp, k, s2, __builtin_nan(""));
+                else wave_chain<double, false>(GlobalView{pre, aux}, G, cp, k, s2, __builtin_nan(""));
+            }
+            den = s2;
         }
         if (lane == 0) sh.den = den;
     }
@@ -694,16 +986,20 @@ __global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
     const float q0 = p0 * inv;
     const float minimum = q0 * p.min_p;
     int first_low = INT_MAX;
-    for (int i = i_begin; i < i_end; ++i) {
+    for (int i = tid; i < G; i += kDThreads) {
         const float q = aux[i] * inv;
         aux[i] = q;
-        if (i >= 1 && pre[i] < k && q < minimum && first_low == INT_MAX) first_low = i;
+        if (i < kStage) sh.st.add[i] = q;
+        if (i >= 1 && first_low == INT_MAX && q < minimum && pre[i] < k) first_low = i;
     }
     first_low = wave_reduce(first_low, [](int x, int y) { return min(x, y); });
+    __syncthreads();  // every reader of sh.ired above is done
     if (lane == 0) sh.ired[wave] = first_low;
     __syncthreads();
-    if (wave == 0) {
-        int fl = lane < kWaves ? sh.ired[lane] : INT_MAX;
+    // Wave 0 decides: top-p cut, draw, near-boundary flag, selected value's
+    // group. The item view is LDS when the row's items fit, else global.
+    auto decide = [&](const auto& iv) {
+        int fl = lane < kDWaves ? sh.ired[lane] : INT_MAX;
         fl = wave_reduce(fl, [](int x, int y) { return min(x, y); });
         // generation.cpp:106-115: min-p stops before element e >= 1 with p_e < minimum.
         uint32_t keff = k;
@@ -713,7 +1009,6 @@ __global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
         }
         uint32_t keep, pos;
         int item;
-        float choice = __builtin_nanf("");
         bool near = false;
         if (any_nan) {
             // NaN probabilities: no cut fires and the walk never stops.
@@ -722,19 +1017,19 @@ __global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
             item = wave_find_item(pre, G, pos);
         } else {
             // generation.cpp:105-113: fp32 cumulative, top-p stop needs keep > 0.
-            double s = static_cast<double>(q0);
-            ChainPos cp{0, 1, 1};
+            double s2 = static_cast<double>(q0);
+            ChainPos cp{0, 1};
             keep = keff;
-            if (keff > 1 && wave_chain<float, false>(items, aux, G, cp, keff, s, static_cast<double>(p.top_p)))
+            if (keff > 1 && wave_chain_f32<false>(iv, G, cp, keff, s2, static_cast<double>(p.top_p)))
                 keep = cp.elem + 1;
-            const float mass = static_cast<float>(s);
+            const float mass = static_cast<float>(s2);
             // random.h:1864-1871 and generation.cpp:118-124.
             const float u = a.uniforms[row];
-            choice = u * (mass - 0.0f) + 0.0f;
+            const float choice = u * (mass - 0.0f) + 0.0f;
             if (choice > 0.0f && choice < __builtin_inff()) {
-                ChainPos w{0, 0, 0};
+                ChainPos w{0, 0};
                 double c = static_cast<double>(choice);
-                if (wave_chain<float, true>(items, aux, G, w, keep, c, 0.0)) {
+                if (wave_chain_f32<true>(iv, G, w, keep, c, 0.0)) {
                     pos = w.elem;
                     item = w.item;
                 } else {
@@ -749,132 +1044,82 @@ __global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
                 item = wave_find_item(pre, G, pos);
             }
             // Near-boundary flag: sequential double sums of the probabilities
-            // before and through the chosen position (as the oracle defines it).
+            // before and through the chosen position, as the oracle defines it.
             double c_before = 0.0;
             if (pos > 0) {
                 // exact parallel sum when certified, else the closed-form chain
                 double sum = 0.0;
-                int ml = INT_MAX;
+                int mlb = INT_MAX;
                 for (int i0 = 0; i0 <= item; i0 += 64) {
                     const int i = i0 + lane;
                     if (i <= item) {
-                        const uint32_t n = static_cast<uint32_t>(items[i]);
-                        const uint32_t pi = pre[i];
-                        const uint32_t cnt = pi >= pos ? 0u : min(n, pos - pi);
-                        const float q = aux[i];
-                        if (cnt && q > 0.0f) {
-                            sum += static_cast<double>(cnt) * static_cast<double>(q);
-                            ml = min(ml, lsb_exp(q));
+                        const uint32_t st = iv.start(i);
+                        const uint32_t en = min(iv.start(i + 1), pos);
+                        const float q = iv.addend(i);
+                        if (en > st && q > 0.0f) {
+                            sum += static_cast<double>(en - st) * static_cast<double>(q);
+                            mlb = min(mlb, lsb_exp(q));
                         }
                     }
                 }
                 sum = wave_reduce(sum, [](double x, double y) { return x + y; });
-                ml = wave_reduce(ml, [](int x, int y) { return min(x, y); });
-                if (sum == 0.0 || ml >= exp_of(sum) - 51) {
+                mlb = wave_reduce(mlb, [](int x, int y) { return min(x, y); });
+                if (sum == 0.0 || mlb >= exp_of(sum) - 51) {
                     c_before = sum;
                 } else {
-                    ChainPos cp2{0, 1, 1};
+                    ChainPos cp2{0, 1};
                     double sb = static_cast<double>(q0);
-                    if (pos > 1) wave_chain<double, false>(items, aux, G, cp2, pos, sb, __builtin_nan(""));
+                    if (pos > 1) wave_chain<double, false>(iv, G, cp2, pos, sb, __builtin_nan(""));
                     c_before = sb;
                 }
             }
-            const double c_at = c_before + static_cast<double>(aux[item]);
+            const double c_at = c_before + static_cast<double>(iv.addend(item));
             const double ch = static_cast<double>(choice);
             near = (pos > 0 && __builtin_fabs(ch - c_before) < 1e-6) ||
                    (pos + 1 < keep && __builtin_fabs(ch - c_at) < 1e-6);
         }
-        if (lane == 0) {
-            sh.keep = keep;
-            sh.pos = pos;
-            sh.item = item;
-            sh.choice = choice;
-            sh.found = near ? 1u : 0u;  // reused below; flag kept in a register copy
-        }
-    }
-    __syncthreads();
-    const uint32_t pos = sh.pos;
-    const int item = sh.item;
-    const bool near = sh.found != 0;
-    __syncthreads();
 
-    // 6. The selected value's group: items with the same order key are
-    //    adjacent; its tokens are the bins with that key (not penalised) and
-    //    the penalised tokens with that key.
-    const float cap = p.softcap;
-    if (wave == 0) {
-        const uint32_t key = order_key(u2f(static_cast<uint32_t>(items[item] >> 32)));
+        // 6. The selected value's group: items with the same order key are
+        //    adjacent; its tokens are the bins with that key (not penalised)
+        //    and the penalised tokens with that key.
+        const float cap = p.softcap;
+        auto item_key = [&](int i) { return order_key(u2f(static_cast<uint32_t>(items[i] >> 32))); };
+        const uint32_t key = item_key(item);
         int is = item, ie = item;
         for (;;) {  // first item of the group
             const int i = is - 1 - lane;
-            const bool same = i >= 0 && order_key(u2f(static_cast<uint32_t>(items[i] >> 32))) == key;
-            const uint64_t m = __ballot(same);
+            const uint64_t m = __ballot(i >= 0 && item_key(i) == key);
             const int run_len = m == ~0ull ? 64 : static_cast<int>(__builtin_ctzll(~m));
             is -= run_len;
             if (run_len < 64) break;
         }
         for (;;) {  // last item of the group
             const int i = ie + 1 + lane;
-            const bool same = i < G && order_key(u2f(static_cast<uint32_t>(items[i] >> 32))) == key;
-            const uint64_t m = __ballot(same);
+            const uint64_t m = __ballot(i < G && item_key(i) == key);
             const int run_len = m == ~0ull ? 64 : static_cast<int>(__builtin_ctzll(~m));
             ie += run_len;
             if (run_len < 64) break;
         }
-        const uint32_t first = pre[is];
-        const uint32_t total = pre[ie] + static_cast<uint32_t>(items[ie]) - first;
+        const uint32_t first = iv.start(is);
+        const uint32_t total = iv.start(ie + 1) - first;
         const uint32_t rank = pos - first;
         // bins [blo, bhi] whose final value has this key (empty when blo > bhi)
         uint32_t blo = 1, bhi = 0;
         const bool nan_group = key == kKeyNaN;
         if (!nan_group) {
-            // lower_bound of key, and of key + 1, over [kLowBin, kHighBin + 1)
-            uint32_t bounds[2];
-            for (int t = 0; t < 2; ++t) {
-                const uint32_t want = key + static_cast<uint32_t>(t);
-                uint32_t lo = kLowBin, hi = kHighBin + 1;  // first bin with bin_key >= want in [lo, hi]
-                while (hi > lo) {
-                    const uint32_t span = hi - lo;
-                    const uint32_t step = (span + 63) / 64;
-                    const uint32_t probe = lo + static_cast<uint32_t>(lane) * step;
-                    const bool below = probe < hi && bin_key(probe, cap) < want;
-                    const uint64_t m = __ballot(below);
-                    if (m == 0) break;  // bin lo already >= want
-                    const int last = 63 - static_cast<int>(__builtin_clzll(m));
-                    lo = lo + static_cast<uint32_t>(last) * step + 1;
-                    hi = min(hi, lo - 1 + step);
-                }
-                bounds[t] = lo;
-            }
-            blo = bounds[0];
-            bhi = bounds[1] - 1;
+            blo = wave_partition_point(kLowBin, kHighBin + 1, [&](uint32_t b) { return bin_key(b, cap) < key; });
+            bhi = wave_partition_point(blo, kHighBin + 1, [&](uint32_t b) { return bin_key(b, cap) <= key; }) - 1;
         }
-        // penalised tokens with this key: a contiguous run of the sorted extras
+        // penalised tokens with this key: a run of the sorted extras
         uint32_t xs = 0, xe = 0;
         if (E > 0) {
-            uint32_t b2[2];
-            for (int t = 0; t < 2; ++t) {
-                // first extra whose key is <= key - t... keys are descending:
-                // count of extras with key > (key - 1 + t) ... computed as lower bounds
-                const uint32_t want = key + 1u - static_cast<uint32_t>(t);  // t=0: > key, t=1: >= key
-                uint32_t lo = 0, hi = E;  // first index with composite_key < want
-                while (hi > lo) {
-                    const uint32_t span = hi - lo;
-                    const uint32_t step = (span + 63) / 64;
-                    const uint32_t probe = lo + static_cast<uint32_t>(lane) * step;
-                    const bool ge_want = probe < hi && composite_key(extras[probe]) >= want;
-                    const uint64_t m = __ballot(ge_want);
-                    if (m == 0) break;
-                    const int last = 63 - static_cast<int>(__builtin_clzll(m));
-                    lo = lo + static_cast<uint32_t>(last) * step + 1;
-                    hi = min(hi, lo - 1 + step);
-                }
-                b2[t] = lo;
-            }
-            xs = b2[0];  // extras with key > this key come first
-            xe = b2[1];  // ... then those equal to it
+            xs = wave_partition_point(0, E, [&](uint32_t x) { return composite_key(extras[x]) > key; });
+            xe = wave_partition_point(xs, E, [&](uint32_t x) { return composite_key(extras[x]) >= key; });
         }
         if (lane == 0) {
+            sh.pos = pos;
+            sh.item = item;
+            sh.near = near ? 1u : 0u;
             sh.group_rank = rank;
             sh.group_total = total;
             sh.blo = blo;
@@ -882,17 +1127,25 @@ __global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
             sh.nan_group = nan_group ? 1u : 0u;
             sh.gx_count = xe - xs;
             sh.forward = (rank <= (total - 1) / 2) ? 1u : 0u;
-            sh.found = 0;
             sh.token = -1;
         }
+        // (the LDS staging area is no longer read; gx_ids reuses it)
         for (uint32_t x = xs + static_cast<uint32_t>(lane); x < xe; x += 64)
             sh.gx_ids[x - xs] = composite_index(extras[x]);
+    };
+    if (wave == 0) {
+        if (G <= kStage) decide(LdsView{sh.st.pre, sh.st.add});
+        else decide(GlobalView{pre, aux});
     }
     __syncthreads();
 
     // Locate the token: the rank-th lowest index of the group (or the
-    // (total-1-rank)-th highest), in batches of 8192 tokens from that end.
+    // (total-1-rank)-th highest), in batches of 8192 tokens from that end;
+    // each thread covers 16 consecutive tokens of a batch, and the next
+    // batch's loads are in flight while this one is scanned.
     {
+        constexpr int kPer = 16;
+        constexpr int kBatch = kDThreads * kPer;
         const bool fwd = sh.forward != 0;
         uint32_t want = fwd ? sh.group_rank : sh.group_total - 1 - sh.group_rank;
         const uint32_t blo = sh.blo, bhi = sh.bhi;
@@ -913,53 +1166,61 @@ __global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
             while (b0 < b1) { const uint32_t m = (b0 + b1) >> 1; if (sh.gx_ids[m] < hi) b0 = m + 1; else b1 = m; }
             return b0 - a0;
         };
-        const int nb = (V + 8191) / 8192;
-        for (int bi = 0; bi < nb; ++bi) {
-            const int batch = fwd ? bi : nb - 1 - bi;
-            const int slot = fwd ? tid : kThreads - 1 - tid;  // scan order of this thread's 8 tokens
-            const int lo = batch * 8192 + tid * 8;
-            uint32_t w4[4] = {0, 0, 0, 0};
-            uint32_t valid = 0;  // bit h: token lo + h exists
-            if (vec && lo + 8 <= V) {
-                const uint4 q = *reinterpret_cast<const uint4*>(rowp + lo);
-                w4[0] = q.x; w4[1] = q.y; w4[2] = q.z; w4[3] = q.w;
-                valid = 0xFFu;
+        auto load16 = [&](int lo, uint32_t* w8, uint32_t& valid) {
+            valid = 0;
+            if (vec && lo + kPer <= V) {
+                const uint4 q1 = *reinterpret_cast<const uint4*>(rowp + lo);
+                const uint4 q2 = *reinterpret_cast<const uint4*>(rowp + lo + 8);
+                w8[0] = q1.x; w8[1] = q1.y; w8[2] = q1.z; w8[3] = q1.w;
+                w8[4] = q2.x; w8[5] = q2.y; w8[6] = q2.z; w8[7] = q2.w;
+                valid = 0xFFFFu;
             } else {
-                for (int h = 0; h < 8; ++h) {
+                for (int h = 0; h < 8; ++h) w8[h] = 0;
+                for (int h = 0; h < kPer; ++h) {
                     if (lo + h < V) {
-                        w4[h >> 1] |= static_cast<uint32_t>(rowp[lo + h]) << ((h & 1) * 16);
+                        w8[h >> 1] |= static_cast<uint32_t>(rowp[lo + h]) << ((h & 1) * 16);
                         valid |= 1u << h;
                     }
                 }
             }
-            uint32_t mm = 0;  // matching bin tokens
-            for (int h = 0; h < 8; ++h) {
-                if (((valid >> h) & 1u) && bin_match((w4[h >> 1] >> ((h & 1) * 16)) & 0xFFFFu)) mm |= 1u << h;
+        };
+        const int nb = (V + kBatch - 1) / kBatch;
+        uint32_t cur[8], nxt[8];
+        uint32_t cvalid = 0, nvalid = 0;
+        {
+            const int batch = fwd ? 0 : nb - 1;
+            load16(batch * kBatch + tid * kPer, cur, cvalid);
+        }
+        for (int bi = 0; bi < nb; ++bi) {
+            const int batch = fwd ? bi : nb - 1 - bi;
+            const int lo = batch * kBatch + tid * kPer;
+            if (bi + 1 < nb) {
+                const int nbatch = fwd ? bi + 1 : nb - 2 - bi;
+                load16(nbatch * kBatch + tid * kPer, nxt, nvalid);
+            }
+            uint32_t mm = 0;  // matching non-penalised tokens
+            for (int h = 0; h < kPer; ++h) {
+                if (((cvalid >> h) & 1u) && bin_match((cur[h >> 1] >> ((h & 1) * 16)) & 0xFFFFu)) mm |= 1u << h;
             }
             if (mm && pen) {
+                // 16 tokens at a multiple of 16 lie in one bitmap word
                 const uint32_t word = bitmap[lo >> 5] >> (lo & 31);
                 mm &= ~word;
             }
-            const uint32_t hi = static_cast<uint32_t>(min(lo + 8, V));
+            const uint32_t hi = static_cast<uint32_t>(min(lo + kPer, V));
             const uint32_t cnt = static_cast<uint32_t>(__popc(mm)) +
                                  (lo < V ? gx_in(static_cast<uint32_t>(lo), hi) : 0u);
-            // exclusive scan in slot order
-            const int swave = slot >> 6, slane = slot & 63;
-            (void)swave;
-            (void)slane;
-            // scan by thread index, then mirror for the backward direction
             uint32_t tot;
-            const uint32_t ex_fwd = block_excl_scan(cnt, sh.scan, tot);
+            const uint32_t ex_fwd = dblock_excl_scan(cnt, sh.scan, tot);
             const uint32_t ex = fwd ? ex_fwd : tot - ex_fwd - cnt;
             if (want < tot) {
                 if (want >= ex && want < ex + cnt) {
-                    // this thread holds it: walk its tokens in scan order
                     uint32_t r2 = want - ex;
                     int found = -1;
-                    for (int s2 = 0; s2 < 8 && found < 0; ++s2) {
-                        const int h = fwd ? s2 : 7 - s2;
+                    for (int s2 = 0; s2 < kPer && found < 0; ++s2) {
+                        const int h = fwd ? s2 : kPer - 1 - s2;
+                        if (!((cvalid >> h) & 1u)) continue;
                         const uint32_t idx = static_cast<uint32_t>(lo + h);
-                        if (!((valid >> h) & 1u)) continue;
                         uint32_t here = (mm >> h) & 1u;
                         if (!here && gx) here = gx_in(idx, idx + 1);
                         if (here) {
@@ -972,10 +1233,12 @@ __global__ __launch_bounds__(kThreads) void fo_decide_kernel(DevArgs a) {
                 break;
             }
             want -= tot;
+            for (int h = 0; h < 8; ++h) cur[h] = nxt[h];
+            cvalid = nvalid;
         }
     }
     __syncthreads();
-    finish(sh.token, aux[item], near ? GE_FLAG_NEAR_BOUNDARY : 0);
+    finish(sh.token, aux[sh.item], sh.near ? GE_FLAG_NEAR_BOUNDARY : 0);
 }
 
 }  // namespace
@@ -985,7 +1248,7 @@ hipError_t launch_full_order(const DevArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(fo_hist_kernel, dim3(a.rows), dim3(kThreads), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(fo_decide_kernel, dim3(a.rows), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(fo_decide_kernel, dim3(a.rows), dim3(kDThreads), 0, stream, a);
     return hipGetLastError();
 }
 

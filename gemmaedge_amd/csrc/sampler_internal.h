@@ -65,7 +65,7 @@ constexpr int kFoExtrasCap = 8192;             // penalised tokens per row it ha
 
 inline int64_t fo_items_stride(int max_history) {
     const int64_t extras = max_history < kFoExtrasCap ? (max_history > 0 ? max_history : 0) : kFoExtrasCap;
-    return (kFoNonNanBins + extras + 1 + 63) / 64 * 64;
+    return (kFoNonNanBins + extras + 2 + 63) / 64 * 64;  // items + NaN item + end boundary
 }
 
 // Launches the fused select/sample kernel for rows whose k <= kMaxTopK.

@@ -87,11 +87,12 @@ Case make_case(std::mt19937_64& g, bool desc) {
     return c;
 }
 
-template <typename Acc>
+template <typename Acc, bool kF32 = false>
 bool check_asc(const Case& c) {
     double s1 = c.s;
     bool hit1 = false;
-    const uint64_t k1 = asc_run<Acc>(s1, c.a, c.n, c.thr, hit1);
+    const uint64_t k1 = kF32 ? ge::chain::asc_run_f32(s1, c.a, c.n, c.thr, hit1)
+                             : asc_run<Acc>(s1, c.a, c.n, c.thr, hit1);
     Acc s = static_cast<Acc>(c.s);
     uint64_t k2 = c.n;
     bool hit2 = false;
@@ -106,11 +107,11 @@ bool check_asc(const Case& c) {
     return k1 == k2 && hit1 == hit2 && bits_of<Acc>(s1) == bits_of<Acc>(static_cast<double>(s));
 }
 
-template <typename Acc>
+template <typename Acc, bool kF32 = false>
 bool check_desc(const Case& c) {
     double c1 = c.s;
     bool stop1 = false;
-    const uint64_t k1 = desc_run<Acc>(c1, c.a, c.n, stop1);
+    const uint64_t k1 = kF32 ? ge::chain::desc_run_f32(c1, c.a, c.n, stop1) : desc_run<Acc>(c1, c.a, c.n, stop1);
     Acc v = static_cast<Acc>(c.s);
     uint64_t k2 = c.n;
     bool stop2 = false;
@@ -127,7 +128,7 @@ bool check_desc(const Case& c) {
 
 // A chain of runs with descending addends (as sorted probabilities are),
 // replayed run by run, against one loop over every element.
-template <typename Acc, bool kDesc>
+template <typename Acc, bool kDesc, bool kF32 = false>
 bool check_sequence(std::mt19937_64& g) {
     const int runs = 1 + static_cast<int>(g() % 200);
     std::vector<double> a(runs);
@@ -149,7 +150,9 @@ bool check_sequence(std::mt19937_64& g) {
     bool ev1 = false;
     for (int i = 0; i < runs && !ev1; ++i) {
         bool ev = false;
-        const uint64_t k = kDesc ? desc_run<Acc>(s1, a[i], n[i], ev) : asc_run<Acc>(s1, a[i], n[i], thr, ev);
+        uint64_t k;
+        if (kF32) k = kDesc ? ge::chain::desc_run_f32(s1, a[i], n[i], ev) : ge::chain::asc_run_f32(s1, a[i], n[i], thr, ev);
+        else k = kDesc ? desc_run<Acc>(s1, a[i], n[i], ev) : asc_run<Acc>(s1, a[i], n[i], thr, ev);
         pos1 += k;
         ev1 = ev;
     }
@@ -181,8 +184,61 @@ bool check_sequence(std::mt19937_64& g) {
 
 }  // namespace
 
+static bool check_udiv(std::mt19937_64& g) {
+    const uint64_t a = g() >> (10 + g() % 54);  // below 2^54
+    uint64_t b = g() >> (g() % 64);
+    if (b == 0) b = 1;
+    return ge::chain::udiv(a, b) == a / b;
+}
+
+// The bit-field step of a float accumulator against the double-based one.
+static bool check_step_bits(std::mt19937_64& g) {
+    const int e = static_cast<int>(g() % 60) - 50;
+    float s = random_float(g, (g() % 16 == 0) ? -149 + static_cast<int>(g() % 4) : e, 1 + static_cast<int>(g() % 24));
+    if (g() % 50 == 0) s = 0.0f;
+    int ea = e - static_cast<int>(g() % 40) + 3;
+    if (ea < -149) ea = -149;
+    float a = random_float(g, ea, 1 + static_cast<int>(g() % 24));
+    if (g() % 50 == 0) a = 0.0f;
+    uint32_t sb, ab;
+    std::memcpy(&sb, &s, 4);
+    std::memcpy(&ab, &a, 4);
+    const ge::chain::Binade b1 = ge::chain::binade_of<float>(static_cast<double>(s));
+    const ge::chain::StepBits b2 = ge::chain::binade_bits(sb);
+    if (b1.m != b2.m || b1.lo != b2.lo || b1.uexp != b2.uexp) return false;
+    const ge::chain::Step st = ge::chain::step_of<float>(b1, static_cast<double>(a));
+    uint32_t D;
+    bool tie, big;
+    ge::chain::step_bits(ab, b2.uexp, D, tie, big);
+    if (st.big != big) return false;
+    if (!big && (st.D != D || st.tie != tie)) return false;
+    // threshold in ulps
+    float thr = random_float(g, e + static_cast<int>(g() % 6) - 3, 1 + static_cast<int>(g() % 24));
+    switch (g() % 10) {
+        case 0: thr = -thr; break;
+        case 1: thr = 0.0f; break;
+        case 2: thr = std::nanf(""); break;
+        case 3: thr = INFINITY; break;
+        default: break;
+    }
+    uint32_t tb;
+    std::memcpy(&tb, &thr, 4);
+    const uint32_t tm = ge::chain::threshold_bits(tb, b2.uexp);
+    uint64_t want;
+    if (thr != thr || thr == INFINITY) want = ge::chain::kNoThreshold;
+    else if (!(thr > 0.0f)) want = 0;
+    else {
+        const double td = std::ceil(std::ldexp(static_cast<double>(thr), -b2.uexp));
+        want = td >= 16777216.0 ? ge::chain::kNoThreshold : static_cast<uint64_t>(td);
+    }
+    return tm == want;
+}
+
 // which: 0 float asc, 1 float desc, 2 double asc, 3 double desc,
-//        4 float asc sequences, 5 float desc sequences, 6 double asc sequences.
+//        4 float asc sequences, 5 float desc sequences, 6 double asc sequences,
+//        7 the corrected double quotient,
+//        8 / 9 float asc / desc through the 32-bit versions, 10 / 11 their chained runs,
+//        12 the bit-field step and threshold of a float accumulator.
 // Returns the number of mismatching trials (or -1 for a bad `which`).
 extern "C" long long ge_test_chain_random(int which, unsigned long long seed, int trials) {
     std::mt19937_64 g(seed);
@@ -197,6 +253,12 @@ extern "C" long long ge_test_chain_random(int which, unsigned long long seed, in
             case 4: ok = check_sequence<float, false>(g); break;
             case 5: ok = check_sequence<float, true>(g); break;
             case 6: ok = check_sequence<double, false>(g); break;
+            case 7: ok = check_udiv(g); break;
+            case 8: ok = check_asc<float, true>(make_case<float>(g, false)); break;
+            case 9: ok = check_desc<float, true>(make_case<float>(g, true)); break;
+            case 10: ok = check_sequence<float, false, true>(g); break;
+            case 11: ok = check_sequence<float, true, true>(g); break;
+            case 12: ok = check_step_bits(g); break;
             default: return -1;
         }
         if (!ok) ++bad;

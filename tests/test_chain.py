@@ -32,6 +32,12 @@ def lib():
     (4, "float ascending, chained runs", 20000),
     (5, "float descending, chained runs", 20000),
     (6, "double ascending, chained runs", 20000),
+    (7, "corrected double quotient", 1000000),
+    (8, "float ascending, 32-bit version", 200000),
+    (9, "float descending, 32-bit version", 200000),
+    (10, "float ascending chained runs, 32-bit version", 20000),
+    (11, "float descending chained runs, 32-bit version", 20000),
+    (12, "float step and threshold from bit fields", 1000000),
 ])
 def test_closed_form_matches_loop(lib, which, name, trials):
     for seed in (1, 2, 3):
