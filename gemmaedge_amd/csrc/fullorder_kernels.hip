@@ -224,10 +224,16 @@ struct HistShared {
 };
 
 // Count of bin `bin` after streaming: the LDS field plus 32768 per spill.
-__device__ __forceinline__ uint32_t bin_count(const HistShared& sh, uint32_t bin, uint32_t nspill) {
-    uint32_t c = (sh.hist[bin_word(bin)] >> bin_shift(bin)) & 0xFFFFu;
+__device__ __forceinline__ uint32_t bin_field(const HistShared& sh, uint32_t bin) {
+    return (sh.hist[bin_word(bin)] >> bin_shift(bin)) & 0xFFFFu;
+}
+__device__ __forceinline__ uint32_t bin_spilled(const HistShared& sh, uint32_t bin, uint32_t nspill) {
+    uint32_t c = 0;
     for (uint32_t i = 0; i < nspill; ++i) c += sh.spill[i] == bin ? 32768u : 0u;
     return c;
+}
+__device__ __forceinline__ uint32_t bin_count(const HistShared& sh, uint32_t bin, uint32_t nspill) {
+    return bin_field(sh, bin) + (nspill ? bin_spilled(sh, bin, nspill) : 0u);
 }
 
 // Counts two bf16 tokens (one 32-bit word) without branches: a token with
@@ -470,14 +476,22 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
     const uint32_t wtop = 65535u - 4096u * static_cast<uint32_t>(wave);
     uint32_t wcount = 0;
     uint32_t nan_local = 0;
-    for (int j = 0; j < 64; ++j) {
-        const uint32_t bin = wtop - 64u * j - lane;
-        const uint32_t c = bin_count(sh, bin, nspill);
-        const bool nz = c != 0 && !bin_is_nan(bin);
-        if (c && bin_is_nan(bin)) nan_local += c;
-        const uint64_t m = __ballot(nz);
-        if (lane == 0) sh.mask[wave * 64 + j] = m;
-        wcount += static_cast<uint32_t>(__popcll(m));
+    for (int j0 = 0; j0 < 64; j0 += 8) {  // eight independent LDS reads per round
+        uint32_t c[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) c[u] = bin_field(sh, wtop - 64u * (j0 + u) - lane);
+        if (nspill) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) c[u] += bin_spilled(sh, wtop - 64u * (j0 + u) - lane, nspill);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const bool isn = bin_is_nan(wtop - 64u * (j0 + u) - lane);
+            if (c[u] && isn) nan_local += c[u];
+            const uint64_t m = __ballot(c[u] != 0u && !isn);
+            if (lane == 0) sh.mask[wave * 64 + j0 + u] = m;
+            wcount += static_cast<uint32_t>(__popcll(m));
+        }
     }
     if (lane == 0) sh.scan[wave] = wcount;
     if (nan_local) atomicAdd(&sh.counters[2], nan_local);
@@ -489,12 +503,9 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
         if (w < wave) wbefore += x;
         nbins_total += x;
     }
-    if (lane == 0) {
-        uint32_t run = wbefore;
-        for (int j = 0; j < 64; ++j) {
-            sh.off[wave * 64 + j] = run;
-            run += static_cast<uint32_t>(__popcll(sh.mask[wave * 64 + j]));
-        }
+    {  // group offsets: lane j takes group 64 * wave + j
+        const uint32_t cj = static_cast<uint32_t>(__popcll(sh.mask[wave * 64 + lane]));
+        sh.off[wave * 64 + lane] = wbefore + wave_incl_u32(cj) - cj;
     }
     __syncthreads();
 
@@ -504,14 +515,23 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
     // place among the penalised items.
     uint32_t* stage_bin = reinterpret_cast<uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
     uint32_t* stage_cnt = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
-    for (int j = 0; j < 64; ++j) {
-        const int g = wave * 64 + j;
-        const uint64_t m = sh.mask[g];
-        if (!((m >> lane) & 1u)) continue;
-        const uint32_t bin = wtop - 64u * j - lane;
-        const uint32_t r = sh.off[g] + static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1)));
-        stage_bin[r] = bin;
-        stage_cnt[r] = bin_count(sh, bin, nspill);
+    const uint64_t below_me = (1ull << lane) - 1;
+    for (int j0 = 0; j0 < 64; j0 += 8) {
+        uint64_t m[8];
+        uint32_t o[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            m[u] = sh.mask[wave * 64 + j0 + u];
+            o[u] = sh.off[wave * 64 + j0 + u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (!((m[u] >> lane) & 1u)) continue;
+            const uint32_t bin = wtop - 64u * (j0 + u) - lane;
+            const uint32_t r = o[u] + static_cast<uint32_t>(__popcll(m[u] & below_me));
+            stage_bin[r] = bin;
+            stage_cnt[r] = bin_count(sh, bin, nspill);
+        }
     }
     __syncthreads();
     for (uint32_t r = tid; r < nbins_total; r += kThreads) {
@@ -687,58 +707,72 @@ __device__ bool wave_chain(const View& iv, int G, ChainPos& cp, uint32_t L, doub
 }
 
 // The same walk for a float accumulator, in 32-bit integer arithmetic: the
-// accumulator is carried as its float bits, each lane's increment comes from
+// accumulator is carried as its float bits, each item's increment comes from
 // the bit fields of its addend (chain_math.h step_bits), increments are capped
 // at 2^24 (more than any binade holds, so the cap never hides an exit) and
-// scanned as u32 with DPP. Addends are floats, read as bits from the view.
+// scanned as u32 with DPP. Each lane takes kPerLane consecutive items, so one
+// step covers 64 * kPerLane items.
 template <bool kDesc, typename View>
 __device__ bool wave_chain_f32(const View& iv, int G, ChainPos& cp, uint32_t L, double& s, double thr) {
+    constexpr int kPerLane = 4;
+    constexpr uint32_t kCap = 0x1000000u;
     const int lane = __lane_id();
     const uint32_t tb = f2u(static_cast<float>(thr));
     uint32_t sb = f2u(static_cast<float>(s));
     while (cp.elem < L && cp.item < G) {
-        const int i = cp.item + lane;
-        uint32_t nt = 0, lo_e = 0, ab = 0;
-        if (i < G) {
-            const uint32_t st = iv.start(i);
-            const uint32_t en = iv.start(i + 1);
-            lo_e = max(st, cp.elem);
-            const uint32_t hi_e = min(en, L);
-            nt = hi_e > lo_e ? hi_e - lo_e : 0u;
-            ab = f2u(iv.addend(i));
-        }
+        const int i0 = cp.item + lane * kPerLane;
+        uint32_t bound[kPerLane + 1];
+#pragma unroll
+        for (int j = 0; j <= kPerLane; ++j) bound[j] = iv.start(min(i0 + j, G));
+        uint32_t ab[kPerLane];
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) ab[j] = i0 + j < G ? f2u(iv.addend(i0 + j)) : 0u;
         const chain::StepBits bb = chain::binade_bits(sb);
-        uint32_t D;
-        bool tie, big;
-        chain::step_bits(ab, bb.uexp, D, tie, big);
-        uint32_t tot = 0;
-        if (nt && !big) {
-            const uint32_t lo32 = nt * D;
-            tot = (__umulhi(nt, D) != 0u || lo32 > 0x1000000u) ? 0x1000000u : lo32;
-        }
-        const uint32_t incl = wave_incl_u32(tot);  // <= 2^30
-        bool ev = false;
-        if (nt) {
-            if (kDesc) {
-                ev = big || tie || bb.m < bb.lo + incl;
-            } else {
-                const uint32_t tm = chain::threshold_bits(tb, bb.uexp);
-                ev = big || tie || bb.m + incl > chain::kHiF || bb.m + incl >= tm;
+        const uint32_t tm = kDesc ? 0u : chain::threshold_bits(tb, bb.uexp);
+        uint32_t nt[kPerLane], lo_e[kPerLane], pre_in[kPerLane + 1];
+        bool evj[kPerLane];
+        pre_in[0] = 0;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            lo_e[j] = max(bound[j], cp.elem);
+            const uint32_t hi_e = min(bound[j + 1], L);
+            nt[j] = hi_e > lo_e[j] ? hi_e - lo_e[j] : 0u;
+            uint32_t D;
+            bool tie, big;
+            chain::step_bits(ab[j], bb.uexp, D, tie, big);
+            uint32_t tot = 0;
+            if (nt[j] && !big) {
+                const uint32_t lo32 = nt[j] * D;
+                tot = (__umulhi(nt[j], D) != 0u || lo32 > kCap) ? kCap : lo32;
             }
+            pre_in[j + 1] = pre_in[j] + tot;  // <= 4 * 2^24
+            evj[j] = nt[j] && (big || tie);
         }
-        const uint64_t evmask = __ballot(ev);
+        const uint32_t lane_tot = min(pre_in[kPerLane], kCap);
+        const uint32_t excl = wave_incl_u32(lane_tot) - lane_tot;  // <= 2^30
+        int jf = kPerLane;
+#pragma unroll
+        for (int j = kPerLane - 1; j >= 0; --j) {
+            const uint32_t after = excl + pre_in[j + 1];
+            bool e = evj[j];
+            if (nt[j]) e = e || (kDesc ? bb.m < bb.lo + after : (bb.m + after > chain::kHiF || bb.m + after >= tm));
+            if (e) jf = j;
+        }
+        const uint64_t evmask = __ballot(jf < kPerLane);
         const int f = evmask ? static_cast<int>(__builtin_ctzll(evmask)) : 64;
-        const uint32_t before = f ? rl32(incl, f - 1) : 0u;
-        const uint32_t m2 = kDesc ? bb.m - before : bb.m + before;
-        // back to float bits: the low region's bits are m itself; a normal
-        // binade keeps its exponent field (m stays in [2^23, 2^24))
-        sb = (sb >> 23) <= 1u ? m2 : ((sb & 0x7F800000u) | (m2 & 0x7FFFFFu));
         if (f == 64) {
-            const int next = cp.item + 64;
+            const uint32_t total = rl32(excl + lane_tot, 63);
+            const uint32_t m2 = kDesc ? bb.m - total : bb.m + total;
+            sb = (sb >> 23) <= 1u ? m2 : ((sb & 0x7F800000u) | (m2 & 0x7FFFFFu));
+            const int next = cp.item + 64 * kPerLane;
             const uint32_t tile_end = iv.start(next < G ? next : G);
-            if (tile_end >= L) {  // the last element lies in this tile
-                const uint64_t lm = __ballot(nt && lo_e + nt == L);
-                cp.item += static_cast<int>(__builtin_ctzll(lm));
+            if (tile_end >= L) {  // the last element lies in this step
+                int where = -1;
+#pragma unroll
+                for (int j = 0; j < kPerLane; ++j)
+                    if (nt[j] && lo_e[j] + nt[j] == L) where = i0 + j;
+                const uint64_t lm = __ballot(where >= 0);
+                cp.item = static_cast<int>(rl32(static_cast<uint32_t>(where), static_cast<int>(__builtin_ctzll(lm))));
                 cp.elem = L;
                 s = static_cast<double>(u2f(sb));
                 return false;
@@ -747,15 +781,30 @@ __device__ bool wave_chain_f32(const View& iv, int G, ChainPos& cp, uint32_t L, 
             cp.item = next;
             continue;
         }
-        cp.elem = rl32(lo_e, f);
-        const uint32_t nf = rl32(nt, f);
-        const double af = static_cast<double>(u2f(rl32(ab, f)));
+        // lanes before f, and items of lane f before its event item, in one step
+        const int jfu = static_cast<int>(rl32(static_cast<uint32_t>(jf), f));
+        uint32_t before_in = 0, lo_f = 0, n_f = 0, a_f = 0;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            if (j == jfu) {
+                before_in = pre_in[j];
+                lo_f = lo_e[j];
+                n_f = nt[j];
+                a_f = ab[j];
+            }
+        }
+        const uint32_t before = rl32(excl + before_in, f);
+        const uint32_t m2 = kDesc ? bb.m - before : bb.m + before;
+        sb = (sb >> 23) <= 1u ? m2 : ((sb & 0x7F800000u) | (m2 & 0x7FFFFFu));
+        cp.item = cp.item + f * kPerLane + jfu;
+        cp.elem = rl32(lo_f, f);
+        const uint32_t nf = rl32(n_f, f);
+        const double af = static_cast<double>(u2f(rl32(a_f, f)));
         double sd = static_cast<double>(u2f(sb));
         bool evt = false;
         const uint64_t used = kDesc ? chain::desc_run_f32(sd, af, nf, evt)
                                     : chain::asc_run_f32(sd, af, nf, thr, evt);
         sb = f2u(static_cast<float>(sd));
-        cp.item += f;
         if (evt) {
             cp.elem += static_cast<uint32_t>(kDesc ? used : used - 1);
             s = sd;
