@@ -23,9 +23,7 @@ struct ge_sampler {
     int max_vocab;
     int max_history;
     uint32_t* tickets;
-    uint32_t* chunk_count;
-    uint64_t* cand;
-    int64_t cand_stride;
+    uint64_t* slots;
     // Full-order path (bf16 rows with k > kMaxTopK); allocated when max_vocab > kMaxTopK.
     uint64_t* fo_items;
     float* fo_aux;
@@ -121,15 +119,13 @@ int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, 
     s->max_rows = max_rows;
     s->max_vocab = max_vocab;
     s->max_history = max_history;
-    s->cand_stride = (static_cast<int64_t>(max_vocab) + kMaxChunkLen - 1) / kMaxChunkLen * kMaxChunkLen;
     const size_t rows = static_cast<size_t>(max_rows);
     hipError_t e = hipSuccess;
     auto alloc = [&](void** p, size_t bytes) {
         if (e == hipSuccess) e = hipMalloc(p, bytes);
     };
     alloc(reinterpret_cast<void**>(&s->tickets), rows * sizeof(uint32_t));
-    alloc(reinterpret_cast<void**>(&s->chunk_count), rows * ge::kMaxChunks * sizeof(uint32_t));
-    alloc(reinterpret_cast<void**>(&s->cand), rows * static_cast<size_t>(s->cand_stride) * sizeof(uint64_t));
+    alloc(reinterpret_cast<void**>(&s->slots), rows * ge::kSlotWords * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMemset(s->tickets, 0, rows * sizeof(uint32_t));
     if (max_vocab > ge::kMaxTopK) {
         s->fo_items_stride = ge::fo_items_stride(max_history);
@@ -158,8 +154,7 @@ void ge_sampler_destroy(ge_sampler* s) {
     if (!s) return;
     DeviceGuard guard(s->device);
     (void)hipFree(s->tickets);
-    (void)hipFree(s->chunk_count);
-    (void)hipFree(s->cand);
+    (void)hipFree(s->slots);
     (void)hipFree(s->fo_items);
     (void)hipFree(s->fo_aux);
     (void)hipFree(s->fo_pre);
@@ -193,7 +188,6 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
 
     // Rows with k > kMaxTopK (top-k disabled or large) take the full-order
     // kernels, which this build has for bf16 logits.
-    int gpt = 16;
     bool run_select = true;
     bool run_full = false;
     if (!x.row_params) {
@@ -207,7 +201,6 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
             run_select = false;
             run_full = true;
         }
-        gpt = k <= 64 ? 1 : (k <= 256 ? 4 : 16);
     } else {
         run_full = x.dtype == GE_DTYPE_BF16 && x.vocab > ge::kMaxTopK;
     }
@@ -243,9 +236,7 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     a.probs = x.probs_out;
     a.flags = x.flags_out;
     a.tickets = s->tickets;
-    a.chunk_count = s->chunk_count;
-    a.cand = s->cand;
-    a.cand_stride = s->cand_stride;
+    a.slots = s->slots;
     a.cpr = cpr;
     a.chunk_len = chunk_len;
     a.vec_ok = vec_ok ? 1 : 0;
@@ -263,7 +254,7 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     if (!guard.ok) return fail(GE_ERR_DEVICE, "hipSetDevice(%d) failed", s->device);
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (run_select) {
-        const hipError_t e = ge::launch_select(a, st, ept, gpt);
+        const hipError_t e = ge::launch_select(a, st, ept);
         if (e != hipSuccess) return hip_fail(e, "launch");
     }
     if (run_full) {

@@ -11,9 +11,9 @@ namespace ge {
 
 constexpr int kBlock = 256;        // threads per workgroup (4 wave64)
 constexpr int kMaxTopK = 1024;     // largest k of the selection path
-constexpr int kSurvivorCap = 2048; // LDS survivors of the merge stage
 constexpr int kMaxChunks = 256;    // chunks (workgroups) per row
 constexpr int kMaxEpt = 64;        // elements per thread in the streaming pass
+constexpr int kSlotWords = 2048;   // per-row words of the chunk lists (all chunks together)
 
 // Device-side view of one ge_sample call plus the handle's workspace.
 struct DevArgs {
@@ -36,9 +36,7 @@ struct DevArgs {
 
     // Workspace (allocated by ge_sampler_create, sized for max_rows x max_vocab).
     uint32_t* tickets;            // [max_rows]          zero between calls
-    uint32_t* chunk_count;        // [max_rows * kMaxChunks]
-    uint64_t* cand;               // [max_rows * cand_stride]  composite keys of final values
-    int64_t cand_stride;          // entries per row, >= cpr * chunk_len
+    uint64_t* slots;              // [max_rows * kSlotWords]  per chunk: guarantee + sorted top-m list
 
     // Launch geometry of the streaming pass.
     int32_t cpr;                  // chunks per row
@@ -69,8 +67,8 @@ inline int64_t fo_items_stride(int max_history) {
 }
 
 // Launches the fused select/sample kernel for rows whose k <= kMaxTopK.
-// ept in {16, 64}; gpt in {1, 4, 16}. Returns a hipError_t.
-hipError_t launch_select(const DevArgs& a, hipStream_t stream, int ept, int gpt);
+// ept in {16, 64}. Returns a hipError_t.
+hipError_t launch_select(const DevArgs& a, hipStream_t stream, int ept);
 
 // Launches the two full-order kernels (bf16 rows with k > kMaxTopK; other
 // rows are skipped). Returns a hipError_t.

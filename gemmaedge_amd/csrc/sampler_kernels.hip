@@ -1,34 +1,43 @@
-// gfx950 sampling kernels for the GemmaEdge token sampler.
+// gfx950 selection-path kernel of the GemmaEdge token sampler (rows whose
+// effective top-k is at most kMaxTopK, and greedy rows).
 //
 // One launch samples `rows` rows. Each row is split into `cpr` chunks of
-// kBlock * EPT logits, one workgroup per chunk. A workgroup
-//   1. issues its chunk's 16-byte loads (consecutive threads on consecutive
-//      addresses) and, while they are in flight, builds the chunk's penalty
-//      bitmap in LDS from the row's history;
-//   2. takes the maximum RAW logit of each group of EPT/GPT of its slots
-//      (penalised tokens left out) and finds, with two adaptive 8-bit radix
-//      digits over their order keys, a lower bound tau on the k-th largest of
-//      those maxima: at least k non-penalised logits of the chunk are >= tau,
-//      so softcap(tau) bounds the row's k-th largest final value from below;
-//   3. lowers tau to the first raw key whose softcapped value equals
-//      softcap(tau) (softcap is monotone, so this keeps every logit that could
-//      tie after capping);
-//   4. compacts its candidates into LDS — the non-penalised logits at or above
-//      that floor, and its penalised tokens that could still reach the top-k —
-//      evaluates their final values there (softcap, then the penalty: each
-//      token once, so history duplicates cannot apply it twice), and publishes
-//      them as (final value desc, index asc) composite keys;
-//   5. takes a ticket; the last workgroup of the row merges the chunks' lists
-//      (their union contains the row's top-k with exact final values), selects
-//      and sorts the top-k and runs the reference's softmax / min-p / top-p /
-//      draw in its exact operation order (src/generation.cpp:89-126).
+// kBlock * EPT logits, one workgroup per chunk. Every workgroup publishes the
+// EXACT top-m of its chunk by the sampler's total order (final value
+// descending, index ascending), sorted, together with a guarantee G: every
+// element of the chunk whose composite key is >= G is in the list. m is a
+// speculative count, about k / cpr plus five standard deviations of a
+// binomial spread, so the lists are short (k = 40 over 16 chunks: m = 17).
 //
-// Cross-workgroup data (candidate lists and counts) is written with
-// agent-scope relaxed atomic stores and read with agent-scope relaxed atomic
-// loads. On gfx950 these are plain loads/stores with the sc1 bit, coherent
-// across the XCDs' L2s; each wave waits for its stores (s_waitcnt) before the
-// workgroup barrier that precedes the ticket. This avoids __threadfence(),
-// which on this chip writes back and invalidates the XCD's whole L2.
+// Per chunk:
+//   1. issue the chunk's 16-byte loads (consecutive threads on consecutive
+//      addresses); while they are in flight, mark the row's unique history
+//      ids that fall in the chunk in an LDS bitmap (penalised slots);
+//   2. from the maxima of groups of raw logits (penalised slots left out)
+//      derive tau, a raw order key with at least m non-penalised logits of
+//      the chunk at or above it, and lower tau to the first raw key whose
+//      softcapped value equals softcap(tau) (softcap is monotone, so every
+//      logit that can tie with tau after capping stays);
+//   3. stage the candidates (raw >= that floor, and penalised tokens that can
+//      still reach it) in LDS, evaluate their final values there (softcap,
+//      then the penalty once per token) and keep the top m, sorted by rank.
+//      If the candidates overflow LDS (massive ties) the exact m-th raw key
+//      is found by radix select and ties are broken by taking the lowest
+//      indices of the boundary class in index order;
+//   4. write [G, list] to the row's slot, wait for the stores, take a ticket.
+// The last workgroup of the row merges: with Gmax the largest guarantee,
+// every element whose composite key is >= Gmax is in some list, so if at
+// least k listed entries are >= Gmax they contain the row's top-k. Otherwise
+// (a chunk held more than m of the row's top-k) the chunks whose guarantee is
+// above the k-th largest listed entry are rescanned with m = k. The merge then
+// runs the reference's softmax / min-p / top-p / draw in its exact operation
+// order (src/generation.cpp:89-126).
+//
+// Cross-workgroup data is written with agent-scope relaxed atomic stores and
+// read with agent-scope relaxed atomic loads: on gfx950 these carry the sc1
+// bit and are coherent across the XCDs' L2s. Each wave waits for its stores
+// (s_waitcnt) before the barrier that precedes the ticket; no __threadfence()
+// (which writes back and invalidates the XCD's whole L2).
 //
 // No MFMA: nothing here is a contraction. The bound is HBM bandwidth.
 #include <hip/hip_runtime.h>
@@ -38,14 +47,17 @@
 
 #include "ge_math.h"
 #include "sampler_internal.h"
+#include "wave_ops.h"
 
 #pragma clang fp contract(off)
 
 namespace ge {
 namespace {
 
-constexpr int kBatch = 8;     // independent global loads in flight per thread
-constexpr int kPenCap = 1024; // penalised tokens of one chunk listed in LDS
+constexpr int kStage = 2048;    // LDS staging entries (candidates, union)
+constexpr int kLoadBatch = 8;   // independent global loads in flight per thread
+constexpr uint32_t kKeyPosInf = 0xff800000u;  // order_key(+inf)
+constexpr uint32_t kPenTag = 0x80000000u;     // staged entry: penalised token
 
 template <typename U>
 __device__ __forceinline__ void store_shared(U* p, U v) {
@@ -56,39 +68,12 @@ __device__ __forceinline__ U load_shared(const U* p) {
     return __hip_atomic_load(const_cast<U*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
-    const int lane = __lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t t = __shfl_up(v, d, 64);
-        if (lane >= d) v += t;
-    }
-    return v;
-}
-
-__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, d, 64)));
-    return v;
-}
-
-__device__ __forceinline__ uint32_t wave_min(uint32_t v) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v = min(v, static_cast<uint32_t>(__shfl_xor(v, d, 64)));
-    return v;
-}
-
-__device__ __forceinline__ int wave_min_i(int v) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v = min(v, __shfl_xor(v, d, 64));
-    return v;
-}
-
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
-    return v;
-}
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) { return wave::incl_add(v); }
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) { return wave::max_u32(v); }
+__device__ __forceinline__ uint32_t wave_min(uint32_t v) { return wave::min_u32(v); }
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { return wave::max_u64(v); }
+__device__ __forceinline__ int wave_min_i(int v) { return wave::min_i32(v); }
+__device__ __forceinline__ double wave_sum(double v) { return wave::sum_f64(v); }
 
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
@@ -107,7 +92,6 @@ __device__ __forceinline__ double readlane_d(double v, int i) {
 }
 
 // Lane I of the result is `v` (a wave-uniform value); other lanes keep `old`.
-// One v_writelane_b32 with an immediate lane index.
 template <int I>
 __device__ __forceinline__ uint32_t writelane_u(uint32_t v, uint32_t old) {
     const uint32_t s = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
@@ -133,6 +117,15 @@ __device__ __forceinline__ void static_for(F&& f) {
         f(std::integral_constant<int, J>{});
         static_for<J + 1, N>(f);
     }
+}
+
+// threadIdx.x through a volatile move: values derived from it cannot be
+// hoisted out of an enclosing loop (the merge's rescans run the chunk routine
+// in a loop; hoisted per-thread addresses would stay live across all of it).
+__device__ __forceinline__ int opaque_tid() {
+    int t;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"(static_cast<int>(threadIdx.x)));
+    return t;
 }
 
 __device__ __forceinline__ float load_one(const float* rowp, int i) { return rowp[i]; }
@@ -164,27 +157,35 @@ __device__ __forceinline__ int lsb_exponent(float e) {
     return static_cast<int>(ex) - 150 + __builtin_ctz(man | 0x800000u);
 }
 
-struct Shared {
-    union {
-        uint64_t surv[kSurvivorCap];  // merge: union cache, then survivors (composite keys)
-        struct {
-            uint32_t raw[kSurvivorCap];  // streaming pass: candidate logit bits
-            uint32_t tag[kSurvivorCap];  // streaming pass: token index
-        } stage;
-    };
-    uint32_t pen_idx[kPenCap];  // streaming pass: the chunk's penalised tokens...
-    uint32_t pen_raw[kPenCap];  // ...and their raw logit bits
-    float prob[kMaxTopK];
+// List length each chunk publishes for a row with effective top-k `k`: the
+// mean share k / cpr plus five binomial standard deviations plus 6, capped by
+// k, by the chunk length and by the row's slot capacity (cpr * (m + 1) words
+// <= kSlotWords). The host and every workgroup of the row compute the same m.
+__device__ __forceinline__ uint32_t spec_m(uint32_t k, int cpr, int chunk_len) {
+    if (k <= 1u) return 1u;
+    const float mu = static_cast<float>(k) / static_cast<float>(cpr);
+    uint32_t m = static_cast<uint32_t>(ceilf(mu + 5.0f * sqrtf(mu))) + 6u;
+    m = min(m, k);
+    m = min(m, static_cast<uint32_t>(chunk_len));
+    m = min(m, static_cast<uint32_t>(kSlotWords / cpr - 1));
+    return max(m, 1u);
+}
+
+struct __align__(16) SelShared {
+    uint64_t stage[kStage];      // candidates (staging) / union / sort area; floats of the softmax
+    uint64_t list[kMaxTopK];     // chunk routine output: its top-m, sorted descending
+    uint64_t top[kMaxTopK];      // merge: the row's top-k, sorted descending
+    uint64_t gam[kMaxChunks];    // merge: guarantee of each chunk
     uint32_t hist[256];
-    uint32_t off[kMaxChunks + 1];  // exclusive prefix of the chunks' candidate counts
+    uint64_t u64[4];
     double f64[kBlock / 64];
     int i32[kBlock / 64];
     uint32_t u32[32];
 };
 
 // Exclusive prefix over the workgroup of one value per thread; also returns
-// the total. Uses sh.u32[24..28]; contains barriers (block-uniform).
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t& total, Shared& sh) {
+// the total. Uses sh.u32[24..27]; contains barriers (block-uniform).
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t& total, SelShared& sh) {
     const int lane = __lane_id();
     const int wave = threadIdx.x >> 6;
     const uint32_t incl = wave_incl_scan(v);
@@ -195,6 +196,13 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t& total,
     total = sh.u32[24] + sh.u32[25] + sh.u32[26] + sh.u32[27];
     __syncthreads();
     return before + incl - v;
+}
+
+// Sum over the workgroup; block-uniform result. Uses sh.u32[24..27].
+__device__ __forceinline__ uint32_t block_sum(uint32_t v, SelShared& sh) {
+    uint32_t total;
+    (void)block_excl_scan(v, total, sh);
+    return total;
 }
 
 // Wave 0: hist[256] holds counts per digit; find the digit b (scanning from
@@ -208,7 +216,7 @@ __device__ __forceinline__ void find_bin_desc(const uint32_t* hist, uint32_t k, 
     for (int i = 0; i < 4; ++i) h[i] = hist[b0 - i];
     const uint32_t s = h[0] + h[1] + h[2] + h[3];
     const uint32_t incl = wave_incl_scan(s);
-    const uint32_t total = __shfl(incl, 63, 64);
+    const uint32_t total = wave::readlane(incl, 63);
     if (total < k) {
         if (lane == 0) {
             out[0] = 0;
@@ -232,11 +240,11 @@ __device__ __forceinline__ void find_bin_desc(const uint32_t* hist, uint32_t k, 
 // Lower bound on the k-th largest of the keys that `visit` presents within
 // [lo, hi] (every thread calls visit(f) and f(key) runs once per key it
 // holds). Two radix passes over the 8-bit digits right below the common prefix
-// of lo and hi, so the keys spread over the bins. Returns 0 if fewer than k
-// keys lie in [lo, hi]. Uses sh.hist and sh.u32[20..22]; block-uniform.
+// of lo and hi. Returns 0 if fewer than k keys lie in [lo, hi]. Uses sh.hist
+// and sh.u32[20..22]; block-uniform.
 template <typename Visit>
 __device__ __forceinline__ uint32_t block_kth(uint32_t lo, uint32_t hi, uint32_t k, Visit&& visit,
-                                              Shared& sh) {
+                                              SelShared& sh) {
     const int tid = threadIdx.x;
     if (lo > hi || k == 0) return 0u;
     const uint32_t diff = lo ^ hi;
@@ -274,17 +282,62 @@ __device__ __forceinline__ uint32_t block_kth(uint32_t lo, uint32_t hi, uint32_t
     return bucket + (d2 << shift2);
 }
 
+// The exact k-th largest of the keys (>= 1) that `visit` presents: 8-bit
+// radix digits from the highest bit where lo and hi differ, narrowed until
+// every bit is fixed. Returns 0 if fewer than k keys lie in [lo, hi].
+// Block-uniform; uses sh.hist and sh.u32[20..22].
+template <typename Visit>
+__device__ __forceinline__ uint32_t block_kth_exact(uint32_t lo, uint32_t hi, uint32_t k, Visit&& visit, SelShared& sh) {
+    const int tid = threadIdx.x;
+    if (lo > hi || k == 0) return 0u;
+    const uint32_t diff = lo ^ hi;
+    int hb = diff ? 31 - __clz(static_cast<int>(diff)) : 0;
+    int shift = max(hb - 7, 0);
+    int width = hb - shift + 1;
+    uint32_t fixed = (hb + 1 >= 32) ? 0u : ~((1u << (hb + 1)) - 1u);
+    uint32_t prefix = lo & fixed;
+    uint32_t need = k;
+    for (;;) {
+        for (int i = tid; i < 256; i += kBlock) sh.hist[i] = 0u;
+        __syncthreads();
+        const uint32_t dmask = (1u << width) - 1u;
+        visit([&](uint32_t key) {
+            if (key >= lo && key <= hi && (key & fixed) == prefix)
+                atomicAdd(&sh.hist[(key >> shift) & dmask], 1u);
+        });
+        __syncthreads();
+        if (tid < 64) find_bin_desc(sh.hist, need, &sh.u32[20]);
+        __syncthreads();
+        const uint32_t d = sh.u32[20];
+        const uint32_t above = sh.u32[21];
+        const bool short_set = sh.u32[22] != 0u;
+        __syncthreads();
+        if (short_set) return 0u;
+        need -= above;
+        prefix |= d << shift;
+        fixed |= dmask << shift;
+        if (shift == 0) return prefix;
+        const int ns = max(shift - 8, 0);
+        width = shift - ns;
+        shift = ns;
+    }
+}
+
 // Called by one whole wave; every lane returns the same value: the smallest
 // raw key x <= tau with softcap(x) == softcap(tau). softcap is monotone
 // non-decreasing (glibc tanhf is monotone on all floats), so the keys with
 // equal capped value form an interval. Usually tau-1 already caps lower and
 // one evaluation round decides; otherwise a 64-way search finds the floor.
-__device__ __forceinline__ uint32_t tie_floor(uint32_t tau, float cap) {
-    if (!(cap > 0.0f) || tau <= kKeyNegInf) return tau;
+__device__ __forceinline__ uint32_t tie_floor(uint32_t tau, float cap, float* cap_tau = nullptr) {
+    if (!(cap > 0.0f) || tau <= kKeyNegInf) {
+        if (cap_tau) *cap_tau = softcap(key_value(tau), cap);
+        return tau;
+    }
     const int lane = __lane_id();
     const float s01 = softcap(key_value(tau - static_cast<uint32_t>(lane & 1)), cap);
-    const float target = __shfl(s01, 0, 64);
-    if (__shfl(s01, 1, 64) != target) return tau;
+    const float target = u2f(wave::readlane(f2u(s01), 0));
+    if (cap_tau) *cap_tau = target;
+    if (u2f(wave::readlane(f2u(s01), 1)) != target) return tau;
     uint32_t hi = tau - 1;  // lowest key known to map to target
     uint32_t lo;            // a key known to map below target
     uint64_t step = 1;
@@ -297,13 +350,13 @@ __device__ __forceinline__ uint32_t tie_floor(uint32_t tau, float cap) {
         const uint64_t ne = __ballot(!eq);
         if (ne) {
             const int j = __ffsll(static_cast<unsigned long long>(ne)) - 1;
-            const uint32_t xj = __shfl(x, j, 64);
-            const uint32_t xp = __shfl(x, j > 0 ? j - 1 : 0, 64);
+            const uint32_t xj = wave::readlane(x, j);
+            const uint32_t xp = wave::readlane(x, j > 0 ? j - 1 : 0);
             lo = xj;
             hi = j > 0 ? xp : hi;
             break;
         }
-        hi = __shfl(x, 63, 64);
+        hi = wave::readlane(x, 63);
         if (hi == kKeyNegInf) return kKeyNegInf;
         step *= 64;
     }
@@ -315,15 +368,61 @@ __device__ __forceinline__ uint32_t tie_floor(uint32_t tau, float cap) {
         const bool eq = softcap(key_value(x), cap) == target;
         const uint64_t m = __ballot(eq);  // non-empty: lanes probing hi match
         const int j = __ffsll(static_cast<unsigned long long>(m)) - 1;
-        const uint32_t xj = __shfl(x, j, 64);
-        const uint32_t xp = __shfl(x, j > 0 ? j - 1 : 0, 64);
+        const uint32_t xj = wave::readlane(x, j);
+        const uint32_t xp = wave::readlane(x, j > 0 ? j - 1 : 0);
         lo = j > 0 ? xp : lo;
         hi = xj;
     }
     return hi;
 }
 
-// Descending bitonic sort of s[0, n), n a power of two <= kSurvivorCap, by the
+// Mirror of tie_floor: the largest raw key x >= r with softcap(x) ==
+// softcap(r). One whole wave; every lane returns the same value.
+__device__ __forceinline__ uint32_t tie_ceil(uint32_t r, float cap) {
+    if (!(cap > 0.0f) || r < kKeyNegInf || r >= kKeyPosInf) return r;
+    const int lane = __lane_id();
+    const float s01 = softcap(key_value(r + static_cast<uint32_t>(lane & 1)), cap);
+    const float target = u2f(wave::readlane(f2u(s01), 0));
+    if (u2f(wave::readlane(f2u(s01), 1)) != target) return r;
+    uint32_t lo = r + 1;  // highest key known to map to target
+    uint32_t hi;          // a key known to map above target
+    uint64_t step = 1;
+    for (;;) {
+        const uint64_t off = static_cast<uint64_t>(lane + 1) * step;
+        const uint32_t x = (static_cast<uint64_t>(kKeyPosInf - lo) > off)
+                               ? lo + static_cast<uint32_t>(off)
+                               : kKeyPosInf;
+        const bool eq = softcap(key_value(x), cap) == target;
+        const uint64_t ne = __ballot(!eq);
+        if (ne) {
+            const int j = __ffsll(static_cast<unsigned long long>(ne)) - 1;
+            const uint32_t xj = wave::readlane(x, j);
+            const uint32_t xp = wave::readlane(x, j > 0 ? j - 1 : 0);
+            hi = xj;
+            lo = j > 0 ? xp : lo;
+            break;
+        }
+        lo = wave::readlane(x, 63);
+        if (lo == kKeyPosInf) return kKeyPosInf;
+        step *= 64;
+    }
+    while (hi - lo > 1) {
+        const uint32_t span = hi - lo;
+        const uint32_t s = (span + 63u) / 64u;
+        const uint64_t off = static_cast<uint64_t>(lane + 1) * s;
+        const uint32_t x = off < span ? lo + static_cast<uint32_t>(off) : hi;
+        const bool eq = softcap(key_value(x), cap) == target;
+        const uint64_t nm = __ballot(!eq);  // non-empty: lanes probing hi differ
+        const int j = __ffsll(static_cast<unsigned long long>(nm)) - 1;
+        const uint32_t xj = wave::readlane(x, j);
+        const uint32_t xp = wave::readlane(x, j > 0 ? j - 1 : 0);
+        lo = j > 0 ? xp : lo;
+        hi = xj;
+    }
+    return lo;
+}
+
+// Descending bitonic sort of s[0, n), n a power of two <= kStage, by the
 // whole workgroup through LDS.
 __device__ __forceinline__ void bitonic_desc_block(uint64_t* s, uint32_t n) {
     const int tid = threadIdx.x;
@@ -344,67 +443,530 @@ __device__ __forceinline__ void bitonic_desc_block(uint64_t* s, uint32_t n) {
     }
 }
 
-// Descending bitonic sort of 64 values, one per lane, within one wave.
-__device__ __forceinline__ uint64_t bitonic_desc_wave(uint64_t x) {
-    const uint32_t lane = __lane_id();
-#pragma unroll
-    for (uint32_t size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            const uint64_t y = __shfl_xor(x, static_cast<int>(stride), 64);
-            const bool lower = (lane & stride) == 0;
-            const bool desc = (lane & size) == 0 || size == 64;
-            x = (lower == desc) ? (x > y ? x : y) : (x < y ? x : y);
+// dst[0, min(n, m)) = the largest min(n, m) of the distinct non-zero keys
+// src[0, n), sorted descending. src is clobbered. n <= kStage. Block-uniform.
+__device__ __forceinline__ uint32_t select_top(uint64_t* src, uint32_t n, uint32_t m, uint64_t* dst) {
+    const int tid = threadIdx.x;
+    const uint32_t out = min(n, m);
+    if (n <= static_cast<uint32_t>(kBlock)) {
+        // Rank by counting: every key is distinct, so its rank is the number
+        // of larger keys. Two keys per 16-byte LDS read (src[n] padded).
+        if (tid == 0 && (n & 1u)) src[n] = 0ull;
+        __syncthreads();
+        if (static_cast<uint32_t>(tid) < n) {
+            const uint64_t x = src[tid];
+            uint32_t r = 0;
+            const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(src);
+#pragma unroll 8
+            for (uint32_t j = 0; j < (n + 1) / 2; ++j) {
+                const ulonglong2 q = p2[j];
+                r += q.x > x ? 1u : 0u;
+                r += q.y > x ? 1u : 0u;
+            }
+            if (r < m) dst[r] = x;
         }
+        __syncthreads();
+        return out;
     }
-    return x;
+    uint32_t n2 = 1;
+    while (n2 < n) n2 <<= 1;
+    for (uint32_t i = n + tid; i < n2; i += kBlock) src[i] = 0ull;
+    __syncthreads();
+    bitonic_desc_block(src, n2);
+    for (uint32_t i = tid; i < out; i += kBlock) dst[i] = src[i];
+    __syncthreads();
+    return out;
 }
 
-// Descending bitonic sort of 64 keys, one per lane, within one wave.
-__device__ __forceinline__ uint32_t bitonic_desc_wave_u32(uint32_t x) {
-    const uint32_t lane = __lane_id();
+// The row-level context every workgroup of a row shares.
+struct RowCtx {
+    const void* rowp;   // the row's logits
+    const int32_t* hist;
+    int row;
+    int V;
+    int H;
+    int vec_ok;         // rows are 16-byte aligned
+    bool pen;           // the penalty applies (history non-empty, r != 1)
+    float r;
+    float cap;
+};
+
+// Builds the chunk's penalty bitmap in pbits (one bit per element of
+// [c0, c0 + CHUNK)) from the row's history. Block-uniform (barriers).
+template <int CHUNK>
+__device__ __forceinline__ void build_penalty_bitmap(const RowCtx& rc, int c0, int cend, int tid, uint32_t* pbits) {
+    for (int w = tid; w < CHUNK / 32; w += kBlock) pbits[w] = 0u;
+    __syncthreads();
+    for (int base = 0; base < rc.H; base += kBlock * kLoadBatch) {
+        int t[kLoadBatch];
 #pragma unroll
-    for (uint32_t size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            const uint32_t y = static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), static_cast<int>(stride), 64));
-            const bool lower = (lane & stride) == 0;
-            const bool desc = (lane & size) == 0 || size == 64;
-            x = (lower == desc) ? max(x, y) : min(x, y);
+        for (int u = 0; u < kLoadBatch; ++u) {
+            const int j = base + u * kBlock + tid;
+            t[u] = j < rc.H ? rc.hist[j] : -1;
         }
+#pragma unroll
+        for (int u = 0; u < kLoadBatch; ++u)
+            if (t[u] >= c0 && t[u] < cend) atomicOr(&pbits[(t[u] - c0) >> 5], 1u << ((t[u] - c0) & 31));
     }
-    return x;
+    __syncthreads();
 }
 
-// Visits every entry of the row's candidate union [0, total) in global memory
-// with kBatch agent-coherent loads in flight per thread. off[] (LDS) is the
-// exclusive prefix of the per-chunk counts; entry g lives in the chunk c with
-// off[c] <= g < off[c+1]. f(g, entry) runs for each entry.
-template <typename F>
-__device__ __forceinline__ void walk_union(const uint64_t* cand_row, int chunk_len, const uint32_t* off,
-                                           int cpr, uint32_t total, F&& f) {
-    for (uint32_t base = 0; base < total; base += kBlock * kBatch) {
-        uint64_t e[kBatch];
+// Exact top-m of one chunk, for the rare cases: candidates that overflow LDS
+// in the streaming pass (massive ties, or a bound far below the m-th value)
+// and the merge's rescans. Same contract as chunk_topm. It keeps registers
+// low: runtime loops over one 16-byte group per thread at a time, reloading
+// the chunk from memory (L2 / MALL) in every pass.
+//   1. R = the exact m-th largest non-penalised raw order key (radix select);
+//   2. lo..hi = the raw keys whose softcapped value equals R's (its class);
+//   3. candidates: every non-penalised element above the class, the
+//      m - (that count) lowest-index members of the class (counted in index
+//      order), and every penalised token that can reach the class;
+//   4. final values, top m, sorted.
+template <typename T, int EPT>
+__device__ __forceinline__ uint64_t chunk_slow(const RowCtx& rc, int c0, uint32_t m, uint32_t* pbits,
+                                               SelShared& sh, uint32_t& n_out, bool& ok) {
+    constexpr int W = sizeof(T) == 4 ? 4 : 8;
+    constexpr int NV = EPT / W;
+    constexpr int CHUNK = kBlock * EPT;
+    const int tid = opaque_tid();
+    const int lane = __lane_id();
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const T* rowp = static_cast<const T*>(rc.rowp);
+    const int cend = min(c0 + CHUNK, rc.V);
+    const bool pen_all = !(rc.r >= 1.0f);
+    ok = true;
+    if (rc.pen) build_penalty_bitmap<CHUNK>(rc, c0, cend, tid, pbits);
+    auto is_pen = [&](int e) -> bool {
+        return rc.pen && ((pbits[(e - c0) >> 5] >> ((e - c0) & 31)) & 1u);
+    };
+    // Group v of this thread: elements e0 .. e0 + W - 1, e0 = c0 + (v * kBlock + tid) * W.
+    auto load_group = [&](int v, float (&x)[W]) {
+        const int e0 = c0 + (v * kBlock + tid) * W;
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const uint32_t g = base + u * kBlock + threadIdx.x;
-            e[u] = 0ull;
-            if (g < total) {
-                int lo = 0, hi = cpr;
-                while (hi - lo > 1) {
-                    const int mid = (lo + hi) >> 1;
-                    if (off[mid] <= g) lo = mid;
-                    else hi = mid;
-                }
-                e[u] = load_shared(&cand_row[static_cast<int64_t>(lo) * chunk_len + (g - off[lo])]);
+        for (int j = 0; j < W; ++j) x[j] = e0 + j < cend ? load_one(rowp, e0 + j) : NAN;
+    };
+    auto visit_np = [&](auto&& f) {
+#pragma unroll 1
+        for (int v = 0; v < NV; ++v) {
+            float x[W];
+            load_group(v, x);
+            const int e0 = c0 + (v * kBlock + tid) * W;
+#pragma unroll
+            for (int j = 0; j < W; ++j)
+                if (e0 + j < cend && !is_pen(e0 + j)) f(order_key(x[j]));
+        }
+    };
+    const uint32_t R = block_kth_exact(1u, 0xffffffffu, m, visit_np, sh);
+    uint32_t lo = 0u, hi = 0xffffffffu;  // R == 0: fewer than m, take them all
+    if (R != 0u) {
+        if (wave == 0) {
+            const uint32_t l = tie_floor(R, rc.cap);
+            const uint32_t h = tie_ceil(R, rc.cap);
+            if (lane == 0) {
+                sh.u32[4] = l;
+                sh.u32[5] = h;
             }
         }
+        __syncthreads();
+        lo = sh.u32[4];
+        hi = sh.u32[5];
+    }
+    uint32_t above = 0;
+    if (R != 0u) {
+        visit_np([&](uint32_t key) { above += key > hi ? 1u : 0u; });
+        above = block_sum(above, sh);
+    }
+    const uint32_t q = R != 0u ? m - above : 0xffffffffu;  // class members to take
+    // Stage in index order: per group, the class ranks and the candidates'
+    // positions are exclusive scans over the threads.
+    uint32_t cls_before = 0, n_c = 0;
+#pragma unroll 1
+    for (int v = 0; v < NV; ++v) {
+        float x[W];
+        load_group(v, x);
+        const int e0 = c0 + (v * kBlock + tid) * W;
+        uint32_t cls = 0, pen = 0, valid = 0;
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const uint32_t g = base + u * kBlock + threadIdx.x;
-            if (g < total) f(g, e[u]);
+        for (int j = 0; j < W; ++j) {
+            const uint32_t key = order_key(x[j]);
+            const bool in = e0 + j < cend;
+            const bool pj = in && is_pen(e0 + j);
+            valid |= static_cast<uint32_t>(in) << j;
+            pen |= static_cast<uint32_t>(pj) << j;
+            cls |= static_cast<uint32_t>(in && !pj && key >= lo && key <= hi) << j;
+        }
+        uint32_t cls_total;
+        const uint32_t cbase = cls_before + block_excl_scan(static_cast<uint32_t>(__popc(cls)), cls_total, sh);
+        cls_before += cls_total;
+        uint32_t cand = 0;
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+            const uint32_t key = order_key(x[j]);
+            bool c;
+            if ((pen >> j) & 1u) {
+                c = pen_all || key >= lo;
+            } else if ((cls >> j) & 1u) {
+                c = cbase + static_cast<uint32_t>(__popc(cls & ((1u << j) - 1u))) < q;
+            } else {
+                c = ((valid >> j) & 1u) && key > hi;
+            }
+            cand |= static_cast<uint32_t>(c) << j;
+        }
+        uint32_t cand_total;
+        const uint32_t pos = n_c + block_excl_scan(static_cast<uint32_t>(__popc(cand)), cand_total, sh);
+        if (n_c + cand_total > static_cast<uint32_t>(kStage)) {
+            ok = false;
+            n_out = 0;
+            return ~0ull;
+        }
+        uint32_t o = pos;
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+            if ((cand >> j) & 1u) {
+                const uint32_t tag = static_cast<uint32_t>(e0 + j) | (((pen >> j) & 1u) ? kPenTag : 0u);
+                sh.stage[o++] = (static_cast<uint64_t>(tag) << 32) | f2u(x[j]);
+            }
+        }
+        n_c += cand_total;
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < n_c; i += kBlock) {
+        const uint64_t x = sh.stage[i];
+        const uint32_t tag = static_cast<uint32_t>(x >> 32);
+        float f = softcap(u2f(static_cast<uint32_t>(x)), rc.cap);
+        if (tag & kPenTag) f = penalize(f, rc.r);
+        sh.stage[i] = composite(order_key(f), tag & ~kPenTag);
+    }
+    __syncthreads();
+    n_out = select_top(sh.stage, n_c, m, sh.list);
+    // Every element left out is below the m-th listed key (or the chunk
+    // listed everything).
+    return n_out == m ? sh.list[m - 1] : 0ull;
+}
+
+// The t-th largest (1 <= t <= 64) of the wave's 64 keys, wave-uniform. For
+// small t, t rounds of "maximum, then retire one lane holding it"; else a
+// bit-by-bit ballot search.
+__device__ __forceinline__ uint32_t wave_kth(uint32_t key, uint32_t t) {
+    if (t > 8u) return wave::kth_largest(key, t);
+    const int lane = __lane_id();
+    uint32_t mx = 0u;
+    for (uint32_t i = 0; i < t; ++i) {
+        mx = wave::max_u32(key);
+        const uint64_t eq = __ballot(key == mx);
+        if (lane == __ffsll(static_cast<unsigned long long>(eq)) - 1) key = 0u;
+    }
+    return mx;
+}
+
+// Rank of x among the staged keys: per-wave segments sh.stage[w * kSeg, +cnt[w]).
+constexpr int kSeg = kStage / (kBlock / 64);
+
+// Exact top-m of one chunk (elements [c0, min(c0 + CHUNK, V))) by composite
+// final key, sorted descending into sh.list[0, n_out). Returns the chunk's
+// guarantee: every element of the chunk whose composite key is >= it is in
+// the list. ok = false if the candidates could not be staged (more than
+// kStage penalised ties). Block-uniform; every thread returns the same values.
+//
+// Why the guarantee holds whatever bound tau is used: a non-penalised element
+// whose final value reaches softcap(tau) has raw >= floor (softcap is
+// monotone), so it is a candidate; a penalised one with r >= 1 ends at or
+// below its softcapped raw value, so it also needs raw >= floor; with r < 1
+// every penalised token is a candidate. tau only decides how strong the
+// guarantee is (and how many candidates there are).
+template <typename T, int EPT>
+__device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_t m, uint32_t* pbits,
+                                               SelShared& sh, uint32_t& n_out, bool& ok) {
+    constexpr int W = sizeof(T) == 4 ? 4 : 8;  // elements per 16-byte load
+    constexpr int NV = EPT / W;                 // 16-byte loads per thread
+    constexpr int NW = EPT * sizeof(T) / 4;     // 32-bit words per thread
+    constexpr int CHUNK = kBlock * EPT;
+    constexpr int NG = EPT / 4;                 // groups of 4 slots per thread
+    static_assert(EPT % W == 0 && EPT <= 64 && EPT % 4 == 0, "bad tiling");
+
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const int wave = tid >> 6;
+    const T* rowp = static_cast<const T*>(rc.rowp);
+    const int cend = min(c0 + CHUNK, rc.V);
+    const float cap = rc.cap;
+    const float r = rc.r;
+    ok = true;
+
+    // Slot s of this thread is element c0 + ((s / W) * kBlock + tid) * W + s % W.
+    auto elem = [&](int s) { return c0 + ((s / W) * kBlock + tid) * W + (s % W); };
+    constexpr uint32_t kHole = 0x7fc00000u;  // NaN placed in out-of-range slots
+
+    // 1. The first kBlock * kLoadBatch history ids, then the chunk's 16-byte
+    //    loads; both round trips overlap (loads return in issue order).
+    int hid[kLoadBatch];
+    if (rc.pen) {
+#pragma unroll
+        for (int u = 0; u < kLoadBatch; ++u) {
+            const int j = u * kBlock + tid;
+            hid[u] = j < rc.H ? rc.hist[j] : -1;
         }
     }
+    uint32_t d[NW];
+    uint64_t vmask = ~0ull;  // in-range slots
+    if (rc.vec_ok && c0 + CHUNK <= rc.V) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const uint4 q = *reinterpret_cast<const uint4*>(rowp + c0 + (v * kBlock + tid) * W);
+            d[4 * v + 0] = q.x;
+            d[4 * v + 1] = q.y;
+            d[4 * v + 2] = q.z;
+            d[4 * v + 3] = q.w;
+        }
+        if constexpr (EPT < 64) vmask = (1ull << EPT) - 1ull;
+    } else {
+        vmask = 0ull;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int n_in = min(max(cend - (c0 + (v * kBlock + tid) * W), 0), W);
+            vmask |= static_cast<uint64_t>((1u << n_in) - 1u) << (v * W);
+        }
+#pragma unroll
+        for (int s = 0; s < EPT; ++s) {
+            const int e = elem(s);
+            const uint32_t bits = e < cend ? f2u(load_one(rowp, e)) : kHole;
+            if constexpr (W == 4) {
+                d[s] = bits;
+            } else if (s % 2 == 0) {
+                d[s / 2] = bits >> 16;
+            } else {
+                d[s / 2] |= bits & 0xffff0000u;
+            }
+        }
+    }
+    auto value = [&](int s) -> float {
+        if constexpr (W == 4) return u2f(d[s]);
+        else return u2f((s % 2 == 0) ? (d[s / 2] << 16) : (d[s / 2] & 0xffff0000u));
+    };
+    // bf16: makes the packed words opaque so that the unpacked floats of one
+    // phase are recomputed in the next instead of being held in registers.
+    auto fence_words = [&]() {
+        if constexpr (W == 8) {
+#pragma unroll
+            for (int i = 0; i < NW; ++i) asm volatile("" : "+v"(d[i]));
+        }
+    };
+    if (rc.pen)
+        for (int w = tid; w < CHUNK / 32; w += kBlock) pbits[w] = 0u;
+
+    // 2. The bound. Maxima of groups of 4 raw values (fmaxf ignores the NaN
+    //    of out-of-range slots; penalised slots take part, see above).
+    float gm[NG];
+    float lmf = NAN;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        float x = value(g * 4);
+#pragma unroll
+        for (int j = 1; j < 4; ++j) x = fmaxf(x, value(g * 4 + j));
+        gm[g] = x;
+        lmf = fmaxf(lmf, x);
+    }
+    fence_words();
+    const uint32_t lkey = order_key(lmf);
+    uint32_t tau;
+    if (m <= 64u) {
+        // Each wave: the ceil(m/4)-th largest of its 64 lane maxima; the
+        // smallest of the four leaves >= m elements at or above it.
+        const uint32_t tw = wave_kth(lkey, (m + 3u) / 4u);
+        if (lane == 0) sh.u32[8 + wave] = tw;
+        __syncthreads();  // also orders the bitmap clear before its fill
+        tau = min(min(sh.u32[8], sh.u32[9]), min(sh.u32[10], sh.u32[11]));
+    } else {
+        uint32_t gmn = 0xffffffffu;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) gmn = min(gmn, order_key(gm[g]));
+        const uint32_t gmx = wave_max(lkey);
+        gmn = wave_min(gmn);
+        if (lane == 0) {
+            sh.u32[8 + wave] = gmx;
+            sh.u32[12 + wave] = gmn;
+        }
+        __syncthreads();
+        const uint32_t bmax = max(max(sh.u32[8], sh.u32[9]), max(sh.u32[10], sh.u32[11]));
+        const uint32_t bmin = min(min(sh.u32[12], sh.u32[13]), min(sh.u32[14], sh.u32[15]));
+        tau = block_kth(bmin, bmax, m,
+                        [&](auto&& f) {
+#pragma unroll
+                            for (int g = 0; g < NG; ++g) f(order_key(gm[g]));
+                        },
+                        sh);
+    }
+
+    // 3. Wave 0: the tie floor, and the guarantee floor g_floor (every element
+    //    whose final key reaches it is staged). Alongside, every lane caps its
+    //    own maximum (most candidates are lane maxima, so their final values
+    //    are ready when they are staged), and every wave marks the penalised
+    //    tokens in the bitmap from the ids loaded at the start.
+    const float lcap = softcap(lmf, cap);
+    if (wave == 0) {
+        float ct;
+        const uint32_t thr0 = max(tie_floor(tau, cap, &ct), kKeyNaN);
+        if (lane == 0) {
+            sh.u32[2] = thr0;
+            sh.u32[3] = thr0 <= kKeyNaN ? 0u : order_key(ct);
+        }
+    }
+    if (rc.pen) {
+        for (int base = 0; base < rc.H; base += kBlock * kLoadBatch) {
+            if (base > 0) {
+#pragma unroll
+                for (int u = 0; u < kLoadBatch; ++u) {
+                    const int j = base + u * kBlock + tid;
+                    hid[u] = j < rc.H ? rc.hist[j] : -1;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kLoadBatch; ++u)
+                if (hid[u] >= c0 && hid[u] < cend)
+                    atomicOr(&pbits[(hid[u] - c0) >> 5], 1u << ((hid[u] - c0) & 31));
+        }
+    }
+    __syncthreads();
+    const uint32_t thr = sh.u32[2];
+    const uint32_t g_floor = sh.u32[3];
+    const bool allpass = thr <= kKeyNaN;
+    const float floor_v = key_value(max(thr, kKeyNegInf));  // raw >= floor_v <=> key >= thr
+    const bool pen_all = rc.pen && !(r >= 1.0f);
+    if (allpass && cend - c0 > kStage) {
+        // No pruning possible (fewer than m real logits in some wave): the
+        // exact routine.
+        return chunk_slow<T, EPT>(rc, c0, m, pbits, sh, n_out, ok);
+    }
+
+    // 4. Stage the candidates from ballots into this wave's segment. Entry:
+    //    (index | kKnown if the value is already final-before-penalty) << 32
+    //    | value bits. A group of 4 slots is examined only if its maximum
+    //    reaches the floor; with r < 1 every penalised token is a candidate.
+    constexpr uint32_t kKnown = 0x80000000u;
+    const int ebase = c0 + tid * W;
+    uint32_t woff = 0;  // wave-uniform
+    uint64_t* seg = sh.stage + wave * kSeg;
+    auto is_pen = [&](int e) -> bool { return ((pbits[(e - c0) >> 5] >> ((e - c0) & 31)) & 1u) != 0u; };
+    auto put = [&](bool c, int s) {
+        const uint64_t mk = __ballot(c);
+        if (mk) {
+            const uint32_t o = woff + lanes_below(mk);
+            if (c && o < static_cast<uint32_t>(kSeg)) {
+                const int e = ebase + (s / W) * kBlock * W + s % W;
+                const float x = value(s);
+                const bool known = f2u(x) == f2u(lmf);
+                seg[o] = (static_cast<uint64_t>(static_cast<uint32_t>(e) | (known ? kKnown : 0u)) << 32) |
+                         f2u(known ? lcap : x);
+            }
+            woff += static_cast<uint32_t>(__popcll(mk));
+        }
+    };
+    if (allpass) {
+#pragma unroll
+        for (int s = 0; s < EPT; ++s) put(((vmask >> s) & 1ull) != 0ull, s);
+    } else if (!pen_all) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            if (__ballot(gm[g] >= floor_v) == 0ull) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) put(value(4 * g + j) >= floor_v, 4 * g + j);
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < EPT; ++s) {
+            const int e = ebase + (s / W) * kBlock * W + s % W;
+            put(value(s) >= floor_v || (((vmask >> s) & 1ull) && is_pen(e)), s);
+        }
+    }
+    fence_words();
+    // Pad an odd segment with an empty key (the rank reads keys in pairs).
+    if (lane == 0) {
+        sh.u32[24 + wave] = woff;
+        if ((woff & 1u) && woff < static_cast<uint32_t>(kSeg)) seg[woff] = 0ull;
+    }
+    __syncthreads();
+    uint32_t cnt[kBlock / 64];
+    uint32_t n_c = 0;
+    bool seg_over = false;
+#pragma unroll
+    for (int w = 0; w < kBlock / 64; ++w) {
+        cnt[w] = sh.u32[24 + w];
+        n_c += cnt[w];
+        seg_over |= cnt[w] >= static_cast<uint32_t>(kSeg);
+    }
+    if (seg_over) {
+        // Massive ties or a loose bound: the exact routine.
+        return chunk_slow<T, EPT>(rc, c0, m, pbits, sh, n_out, ok);
+    }
+    // 5. Final values of this wave's candidates: softcap where not already
+    //    known, then the penalty once per token.
+    for (uint32_t i = lane; i < cnt[wave]; i += 64) {
+        const uint64_t x = seg[i];
+        const uint32_t hi = static_cast<uint32_t>(x >> 32);
+        const uint32_t e = hi & ~kKnown;
+        float f = u2f(static_cast<uint32_t>(x));
+        if (!(hi & kKnown)) f = softcap(f, cap);
+        if (rc.pen && is_pen(static_cast<int>(e))) f = penalize(f, r);
+        seg[i] = composite(order_key(f), e);
+    }
+    __syncthreads();
+    // 6. Top m, sorted. Up to kBlock candidates: rank by counting over the
+    //    segments (keys in pairs); more: gather them and sort.
+    if (n_c <= static_cast<uint32_t>(kBlock)) {
+        if (static_cast<uint32_t>(tid) < n_c) {
+            int w = 0;
+            uint32_t i = static_cast<uint32_t>(tid);
+            while (i >= cnt[w]) {
+                i -= cnt[w];
+                ++w;
+            }
+            const uint64_t x = sh.stage[w * kSeg + i];
+            uint32_t rk = 0;
+#pragma unroll
+            for (int v = 0; v < kBlock / 64; ++v) {
+                const ulonglong2* sv = reinterpret_cast<const ulonglong2*>(sh.stage + v * kSeg);
+#pragma unroll 4
+                for (uint32_t j = 0; j < (cnt[v] + 1) / 2; ++j) {
+                    const ulonglong2 q = sv[j];
+                    rk += q.x > x ? 1u : 0u;
+                    rk += q.y > x ? 1u : 0u;
+                }
+            }
+            if (rk < m) sh.list[rk] = x;
+        }
+        __syncthreads();
+        n_out = min(n_c, m);
+    } else {
+        uint64_t tmp[kStage / kBlock];
+#pragma unroll
+        for (int q = 0; q < kStage / kBlock; ++q) {
+            uint32_t i = static_cast<uint32_t>(q * kBlock + tid);
+            tmp[q] = 0ull;
+            if (i < n_c) {
+                int w = 0;
+                while (i >= cnt[w]) {
+                    i -= cnt[w];
+                    ++w;
+                }
+                tmp[q] = sh.stage[w * kSeg + i];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kStage / kBlock; ++q) {
+            const uint32_t i = static_cast<uint32_t>(q * kBlock + tid);
+            if (i < n_c) sh.stage[i] = tmp[q];
+        }
+        __syncthreads();
+        n_out = select_top(sh.stage, n_c, m, sh.list);
+    }
+    // The guarantee: the larger of the floor's and the m-th listed key.
+    uint64_t gamma = static_cast<uint64_t>(g_floor) << 32;
+    if (n_out == m) {
+        const uint64_t last = sh.list[m - 1];
+        gamma = last > gamma ? last : gamma;
+    }
+    return gamma;
 }
 
 __device__ __forceinline__ void write_row(const DevArgs& a, int row, int32_t token, float prob,
@@ -422,17 +984,16 @@ __device__ __forceinline__ void write_row(const DevArgs& a, int row, int32_t tok
 }
 
 // generation.cpp:103-126 on probabilities sorted by value desc / index asc,
-// evaluated by one whole wave. seg_prob(g) returns this lane's probability of
-// entry g * 64 + lane (0 past keff). The reference's cumulative sums are
-// sequential fp32 (and, for the boundary distances, double) chains: every lane
-// computes the same chain and lane j keeps step j of each 64-entry segment, so
-// each stop test is one ballot rather than a branch per step.
+// evaluated by one whole wave, for any values (NaN included). seg_prob(g)
+// returns this lane's probability of entry g * 64 + lane (0 past keff). Every
+// lane computes the same sequential fp32 (and, for the boundary distances,
+// double) chain; lane j keeps step j of each 64-entry segment, so each stop
+// test is one ballot.
 template <typename P>
 __device__ __forceinline__ void scan_and_walk(P&& seg_prob, uint32_t keff, const ge_sample_params& p,
                                               float u, uint32_t& pos_out, bool& near_out) {
     const int lane = __lane_id();
     const float minimum = readlane_f(seg_prob(0u), 0) * p.min_p;
-    // min-p / top-p cut (generation.cpp:103-115).
     float cum = 0.0f;
     float mass = 0.0f;
     uint32_t keep = keff;
@@ -463,11 +1024,8 @@ __device__ __forceinline__ void scan_and_walk(P&& seg_prob, uint32_t keff, const
             stopped = true;
         }
     }
-    // The reference's `mass` loop (generation.cpp:117-118) adds the same probs
-    // in the same order from 0, so it equals the cumulative sum at the cut.
     if (!stopped) mass = cum;  // entries past keff add exact zeros
     const float choice0 = u * mass + 0.0f;  // uniform_real_distribution(0, mass)
-    // Subtract walk (generation.cpp:120-126) with the CDF boundaries around it.
     float choice = choice0;
     double dc = 0.0;
     uint32_t pos = keep - 1;
@@ -508,6 +1066,106 @@ __device__ __forceinline__ void scan_and_walk(P&& seg_prob, uint32_t keff, const
     near_out = near;
 }
 
+// The same chains when no probability is NaN. Then the probabilities are
+// non-increasing (expf is monotone and the values are sorted), so the min-p
+// cut is one parallel search and the cumulative / choice chains are
+// monotone: every lane runs the sequential fp32 adds in registers, 16 steps
+// per block, reading the probabilities as broadcast LDS loads, and only the
+// block holding the stop is examined step by step.
+__device__ __forceinline__ void scan_and_walk_fast(const float* prob, uint32_t keff, const ge_sample_params& p,
+                                                   float u, uint32_t& pos_out, bool& near_out) {
+    constexpr int B = 16;
+    const int lane = __lane_id();
+    const float minimum = prob[0] * p.min_p;
+    // min-p: first j >= 1 with p_j < minimum (checked before adding p_j).
+    uint32_t limit = keff;
+    for (uint32_t base = 0; base < keff; base += 64) {
+        const uint32_t j = base + static_cast<uint32_t>(lane);
+        const bool c = j >= 1 && j < keff && prob[j < keff ? j : 0] < minimum;
+        const uint64_t h = __ballot(c);
+        if (h) {
+            limit = base + static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(h)) - 1);
+            break;
+        }
+    }
+    // top-p: first j >= 1, j < limit, with cum_j >= top_p.
+    float cum = 0.0f;
+    float mass = 0.0f;
+    uint32_t keep = limit;
+    bool stopped = false;
+    for (uint32_t j0 = 0; j0 < limit && !stopped; j0 += B) {
+        float c[B];
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const uint32_t j = j0 + i;
+            const float pj = j < limit ? prob[j] : 0.0f;
+            cum = cum + pj;
+            c[i] = cum;
+        }
+        int hit = B;
+#pragma unroll
+        for (int i = B - 1; i >= 0; --i) {
+            const uint32_t j = j0 + i;
+            if (j >= 1 && j < limit && c[i] >= p.top_p) hit = i;
+        }
+        if (hit < B) {
+            keep = j0 + hit + 1;
+#pragma unroll
+            for (int i = 0; i < B; ++i)
+                if (i == hit) mass = c[i];
+            stopped = true;
+        }
+    }
+    if (!stopped) mass = cum;  // min-p cut or all keff kept
+    // Draw: uniform_real_distribution(0, mass), then the subtract walk.
+    const float choice0 = u * mass + 0.0f;
+    float choice = choice0;
+    double dc = 0.0;
+    uint32_t pos = keep - 1;
+    double c_before = 0.0, c_at = 0.0;
+    for (uint32_t j0 = 0; j0 < keep; j0 += B) {
+        float ch[B];
+        double dd[B];
+        const double dbefore = dc;
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const uint32_t j = j0 + i;
+            const float pj = j < keep ? prob[j] : 0.0f;
+            choice = choice - pj;
+            dc = dc + static_cast<double>(pj);
+            ch[i] = choice;
+            dd[i] = dc;
+        }
+        int hit = B;
+#pragma unroll
+        for (int i = B - 1; i >= 0; --i) {
+            const uint32_t j = j0 + i;
+            if (j < keep && ch[i] <= 0.0f) hit = i;
+        }
+        int at = -1;
+        if (hit < B) {
+            pos = j0 + hit;
+            at = hit;
+        } else if (j0 + B >= keep) {
+            at = static_cast<int>(keep - 1 - j0);  // fallthrough return, generation.cpp:126
+        }
+        if (at >= 0) {
+#pragma unroll
+            for (int i = 0; i < B; ++i) {
+                if (i == at) c_at = dd[i];
+                if (i == at - 1) c_before = dd[i];
+            }
+            if (at == 0) c_before = dbefore;
+            break;
+        }
+    }
+    bool near = false;
+    if (pos > 0 && fabs(static_cast<double>(choice0) - c_before) < 1e-6) near = true;
+    if (pos + 1 < keep && fabs(static_cast<double>(choice0) - c_at) < 1e-6) near = true;
+    pos_out = pos;
+    near_out = near;
+}
+
 // std::max_element (generation.cpp:66-70) keeps index 0 when its value is NaN
 // (NaN < x is false), so greedy returns 0 then. Token 0's final value is NaN
 // iff its raw value is, unless the penalty itself is NaN and 0 is in history.
@@ -521,160 +1179,153 @@ __device__ __forceinline__ bool final0_is_nan(const T* rowp, float cap, bool pen
     return false;
 }
 
+// sh.top[0, nt) := the largest k distinct keys of sh.top[0, nt) and
+// sh.list[0, nl), sorted descending. Returns the new nt. Block-uniform.
+__device__ __forceinline__ uint32_t absorb_list(SelShared& sh, uint32_t nt, uint32_t nl, uint32_t k) {
+    const int tid = threadIdx.x;
+    const uint32_t n = nt + nl;
+    for (uint32_t i = tid; i < nt; i += kBlock) sh.stage[i] = sh.top[i];
+    for (uint32_t i = tid; i < nl; i += kBlock) sh.stage[nt + i] = sh.list[i];
+    uint32_t n2 = 1;
+    while (n2 < n) n2 <<= 1;
+    for (uint32_t i = n + tid; i < n2; i += kBlock) sh.stage[i] = 0ull;
+    __syncthreads();
+    bitonic_desc_block(sh.stage, n2);
+    // Drop duplicates (a key present in both lists) and zeros; keep k.
+    uint32_t kept_total = 0;
+    for (uint32_t base = 0; base < n; base += kBlock) {
+        const uint32_t i = base + tid;
+        const uint64_t x = i < n ? sh.stage[i] : 0ull;
+        const bool keep = i < n && x != 0ull && (i == 0 || sh.stage[i - 1] != x);
+        uint32_t total;
+        const uint32_t pos = kept_total + block_excl_scan(keep ? 1u : 0u, total, sh);
+        if (keep && pos < k) sh.top[pos] = x;
+        kept_total += total;
+    }
+    __syncthreads();
+    return min(kept_total, k);
+}
+
+// Merge, first part (last workgroup of the row): one round trip for every
+// chunk's guarantee and list (sh.gam[c] = guarantee of chunk c). If at least
+// k listed entries are >= the largest guarantee, their top-k is the row's:
+// sh.top[0, keff) holds it and the function returns true. Otherwise sh.top
+// holds the top of everything listed (nt entries) and the chunks whose
+// guarantee is above its k-th entry need a rescan; returns false.
+__device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, int row, uint32_t k,
+                                              uint32_t m, uint32_t& nt) {
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    constexpr int kPer = kSlotWords / kBlock;
+    const uint32_t sl = m + 1;
+    const uint32_t words = static_cast<uint32_t>(a.cpr) * sl;  // <= kSlotWords
+    const uint64_t* slot_row = a.slots + static_cast<int64_t>(row) * kSlotWords;
+
+    uint64_t w[kPer];
+    uint32_t wp[kPer];  // position in the chunk's slot: 0 = guarantee
+    {
+        uint32_t c = static_cast<uint32_t>(tid) / sl, q = static_cast<uint32_t>(tid) % sl;
+        const uint32_t dc = kBlock / sl, dq = kBlock % sl;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const uint32_t g = static_cast<uint32_t>(i * kBlock + tid);
+            w[i] = g < words ? load_shared(&slot_row[g]) : 0ull;
+            wp[i] = g < words ? q : 1u;  // past the end: an empty entry
+            if (g < words && q == 0u) sh.gam[c] = w[i];
+            c += dc;
+            q += dq;
+            if (q >= sl) {
+                q -= sl;
+                ++c;
+            }
+        }
+    }
+    if (tid == 0) sh.u64[0] = 0ull;
+    __syncthreads();
+    uint64_t gmax = 0ull;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (wp[i] == 0u) gmax = w[i] > gmax ? w[i] : gmax;
+    gmax = wave_max_u64(gmax);
+    if (lane == 0) atomicMax(reinterpret_cast<unsigned long long*>(&sh.u64[0]),
+                             static_cast<unsigned long long>(gmax));
+    __syncthreads();
+    const uint64_t gam_max = sh.u64[0];
+
+    // Entries at or above the largest guarantee.
+    uint32_t nsel;
+    {
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) cnt += (wp[i] != 0u && w[i] != 0ull && w[i] >= gam_max) ? 1u : 0u;
+        uint32_t pos = block_excl_scan(cnt, nsel, sh);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+            if (wp[i] != 0u && w[i] != 0ull && w[i] >= gam_max) sh.stage[pos++] = w[i];
+    }
+    __syncthreads();
+    if (nsel >= k) {
+        nt = select_top(sh.stage, nsel, k, sh.top);
+        return true;
+    }
+    // Everything listed.
+    uint32_t nall;
+    {
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) cnt += (wp[i] != 0u && w[i] != 0ull) ? 1u : 0u;
+        uint32_t pos = block_excl_scan(cnt, nall, sh);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+            if (wp[i] != 0u && w[i] != 0ull) sh.stage[pos++] = w[i];
+    }
+    __syncthreads();
+    nt = select_top(sh.stage, nall, k, sh.top);
+    return false;
+}
+
+// Next chunk at or after c whose guarantee is above the running k-th key
+// (0 while fewer than k are known); -1 if none. Block-uniform.
+__device__ __forceinline__ int next_rescan(const SelShared& sh, int c, int cpr, uint32_t nt, uint32_t k) {
+    const uint64_t ku = nt >= k ? sh.top[k - 1] : 0ull;
+    for (; c < cpr; ++c)
+        if (sh.gam[c] > ku) return c;
+    return -1;
+}
+
+// Merge, second part: softmax / min-p / top-p / draw over sh.top[0, keff).
 template <typename T>
-__device__ __forceinline__ void merge_row(const DevArgs& a, Shared& sh, int row,
-                                          const ge_sample_params& p, bool greedy, uint32_t k,
-                                          const T* rowp, const int32_t* hist, int H, bool pen,
-                                          int chunk_len) {
+__device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, const RowCtx& rc,
+                                             const ge_sample_params& p, bool greedy, uint32_t keff) {
     const int tid = threadIdx.x;
     const int lane = __lane_id();
     const int wave = tid >> 6;
-    const uint64_t* cand_row = a.cand + static_cast<int64_t>(row) * a.cand_stride;
-
-    // Chunk counts -> exclusive prefix in LDS.
-    const uint32_t cnt = tid < a.cpr ? load_shared(&a.chunk_count[row * kMaxChunks + tid]) : 0u;
-    uint32_t total;
-    const uint32_t excl = block_excl_scan(cnt, total, sh);
-    if (tid < a.cpr) sh.off[tid] = excl;
-    if (tid == 0) {
-        sh.off[a.cpr] = total;
-        sh.u32[16] = 0u;           // max final key
-        sh.u32[17] = 0xffffffffu;  // min final key
-        sh.u32[3] = 0u;            // survivors
-    }
-    __syncthreads();
-    const bool cached = total <= static_cast<uint32_t>(kSurvivorCap);
-
-    // One pass over the union (composite keys of final values): cache it in
-    // LDS when it fits, and the range of its final keys.
-    uint32_t kmax = 0, kmin = 0xffffffffu;
-    walk_union(cand_row, chunk_len, sh.off, a.cpr, total, [&](uint32_t g, uint64_t e) {
-        const uint32_t key = composite_key(e);
-        kmax = max(kmax, key);
-        kmin = min(kmin, key);
-        if (cached) sh.surv[g] = e;
-    });
-    kmax = wave_max(kmax);
-    kmin = wave_min(kmin);
-    if (lane == 0) {
-        atomicMax(&sh.u32[16], kmax);
-        atomicMin(&sh.u32[17], kmin);
-    }
-    __syncthreads();
-
-    // The union holds the row's top-k (by final value, then index); the k-th
-    // largest final key bounds the survivors.
-    auto visit_union = [&](auto&& f) {
-        if (cached) {
-            for (uint32_t g = tid; g < total; g += kBlock) f(composite_key(sh.surv[g]));
-        } else {
-            walk_union(cand_row, chunk_len, sh.off, a.cpr, total,
-                       [&](uint32_t, uint64_t e) { f(composite_key(e)); });
-        }
-    };
-    const uint32_t kfloor = total > k ? block_kth(sh.u32[17], sh.u32[16], k, visit_union, sh) : 0u;
-
-    if (cached) {
-        // Compact the survivors to the front of the cache (read first: the
-        // survivor list overwrites it).
-        constexpr int kPer = kSurvivorCap / kBlock;
-        uint64_t e[kPer];
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const uint32_t g = u * kBlock + tid;
-            e[u] = g < total ? sh.surv[g] : 0ull;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const uint32_t g = u * kBlock + tid;
-            if (g < total && composite_key(e[u]) >= kfloor) sh.surv[atomicAdd(&sh.u32[3], 1u)] = e[u];
-        }
-    } else {
-        walk_union(cand_row, chunk_len, sh.off, a.cpr, total, [&](uint32_t, uint64_t e) {
-            if (composite_key(e) >= kfloor) {
-                const uint32_t pos = atomicAdd(&sh.u32[3], 1u);
-                if (pos < kSurvivorCap) sh.surv[pos] = e;
-            }
-        });
-    }
-    __syncthreads();
-    const uint32_t nsurv = sh.u32[3];
-
-    if (nsurv == 0 || nsurv > kSurvivorCap) {
-        // More survivors than LDS holds (massive exact ties) or none at all.
+    const int row = rc.row;
+    if (keff == 0u) {
         if (tid == 0) write_row(a, row, -1, 0.0f, GE_FLAG_UNSUPPORTED);
         return;
     }
-    const uint32_t keff = min(k, nsurv);
-    const float u = greedy ? 0.0f : a.uniforms[row];
-    const float r = p.repetition_penalty;
-
-    if (nsurv <= 64) {
-        // One wave: sort in registers, softmax and the sequential scans with
-        // lane-resident probabilities (no barriers).
-        if (wave != 0) return;
-        const uint64_t c = bitonic_desc_wave(lane < static_cast<int>(nsurv) ? sh.surv[lane] : 0ull);
-        if (greedy) {
-            int32_t token = static_cast<int32_t>(composite_index(__shfl(c, 0, 64)));
-            if (lane == 0) {
-                if (final0_is_nan(rowp, p.softcap, pen, r, hist, H)) token = 0;
-                write_row(a, row, token, 1.0f, 0);
-            }
-            return;
-        }
-        // generation.cpp:89-101 — p_i = expf((v_i - max) * (1/T)); double denominator.
-        const float maximum = key_value(composite_key(__shfl(c, 0, 64)));
-        const float inv_temp = 1.0f / p.temperature;
-        const bool live = lane < static_cast<int>(keff);
-        const float e = live ? expf_glibc((key_value(composite_key(c)) - maximum) * inv_temp) : 0.0f;
-        const bool bad = live && (!(e >= 0.0f) || __builtin_isinf(e));
-        const int lsb = (live && e > 0.0f && !bad) ? lsb_exponent(e) : INT_MAX;
-        const double s = wave_sum(static_cast<double>(e));
-        const int m = wave_min_i(lsb);
-        const int ex = static_cast<int>((d2u(s) >> 52) & 0x7ffu) - 1023;
-        double den;
-        if (!__any(bad) && s > 0.0 && !__builtin_isinf(s) && m >= ex - 51) {
-            den = s;  // certified exact, as in the workgroup path below
-        } else {
-            den = 0.0;
-            for (uint32_t i = 0; i < keff; ++i) den += static_cast<double>(readlane_f(e, static_cast<int>(i)));
-        }
-        const float inv_denom = static_cast<float>(1.0 / den);
-        const float pr = e * inv_denom;
-        uint32_t pos;
-        bool near;
-        scan_and_walk([&](uint32_t) { return pr; }, keff, p, u, pos, near);
-        const int32_t token = static_cast<int32_t>(composite_index(__shfl(c, static_cast<int>(pos), 64)));
-        const float prob = readlane_f(pr, static_cast<int>(pos));
-        if (lane == 0) write_row(a, row, token, prob, near ? GE_FLAG_NEAR_BOUNDARY : 0);
-        return;
-    }
-
-    uint32_t n2 = 1;
-    while (n2 < nsurv) n2 <<= 1;
-    for (uint32_t i = nsurv + tid; i < n2; i += kBlock) sh.surv[i] = 0ull;
-    __syncthreads();
-    bitonic_desc_block(sh.surv, n2);
-
     if (greedy) {
         if (tid == 0) {
-            int32_t token = static_cast<int32_t>(composite_index(sh.surv[0]));
-            if (final0_is_nan(rowp, p.softcap, pen, r, hist, H)) token = 0;
+            int32_t token = static_cast<int32_t>(composite_index(sh.top[0]));
+            const T* rowp = static_cast<const T*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
+            if (final0_is_nan(rowp, rc.cap, rc.pen, rc.r, rc.hist, rc.H)) token = 0;
             write_row(a, row, token, 1.0f, 0);
         }
         return;
     }
+
     // generation.cpp:89-101 — p_i = expf((v_i - max) * (1/T)); double denominator.
-    const float maximum = key_value(composite_key(sh.surv[0]));
+    float* prob = reinterpret_cast<float*>(sh.stage);
+    const float maximum = key_value(composite_key(sh.top[0]));
     const float inv_temp = 1.0f / p.temperature;
     double lsum = 0.0;
     int lmin = INT_MAX;
     int bad = 0;
     for (uint32_t i = tid; i < keff; i += kBlock) {
-        const float v = key_value(composite_key(sh.surv[i]));
+        const float v = key_value(composite_key(sh.top[i]));
         const float e = expf_glibc((v - maximum) * inv_temp);
-        sh.prob[i] = e;
+        prob[i] = e;
         lsum += static_cast<double>(e);
         if (!(e >= 0.0f) || __builtin_isinf(e)) bad = 1;
         else if (e > 0.0f) lmin = min(lmin, lsb_exponent(e));
@@ -689,62 +1340,76 @@ __device__ __forceinline__ void merge_row(const DevArgs& a, Shared& sh, int row,
     __syncthreads();
     if (tid == 0) {
         double s = 0.0;
-        int m = INT_MAX;
+        int mn = INT_MAX;
         bool b = false;
-        for (int w = 0; w < kBlock / 64; ++w) {
-            s += sh.f64[w];
-            if (sh.i32[w] == INT_MIN) b = true;
-            else m = min(m, sh.i32[w]);
+        for (int wv = 0; wv < kBlock / 64; ++wv) {
+            s += sh.f64[wv];
+            if (sh.i32[wv] == INT_MIN) b = true;
+            else mn = min(mn, sh.i32[wv]);
         }
-        // Certified exact: every term is a multiple of 2^m and every partial
+        // Certified exact: every term is a multiple of 2^mn and every partial
         // sum is below 2^(E+2), so 53 bits hold each partial sum exactly when
-        // m >= E - 51; then any summation order equals the reference's
+        // mn >= E - 51; then any summation order equals the reference's
         // sequential one. Otherwise replay it sequentially.
         double den;
         int ex = 0;
         if (!b && s > 0.0 && !__builtin_isinf(s)) ex = static_cast<int>((d2u(s) >> 52) & 0x7ffu) - 1023;
-        if (!b && s > 0.0 && !__builtin_isinf(s) && m >= ex - 51) {
+        if (!b && s > 0.0 && !__builtin_isinf(s) && mn >= ex - 51) {
             den = s;
         } else {
             den = 0.0;
-            for (uint32_t i = 0; i < keff; ++i) den += static_cast<double>(sh.prob[i]);
+            for (uint32_t i = 0; i < keff; ++i) den += static_cast<double>(prob[i]);
         }
         sh.f64[0] = den;
     }
     __syncthreads();
     const float inv_denom = static_cast<float>(1.0 / sh.f64[0]);
-    for (uint32_t i = tid; i < keff; i += kBlock) sh.prob[i] = sh.prob[i] * inv_denom;
+    int nan_p = 0;
+    for (uint32_t i = tid; i < keff; i += kBlock) {
+        const float pr = prob[i] * inv_denom;
+        prob[i] = pr;
+        if (__builtin_isnan(pr)) nan_p = 1;
+    }
+    nan_p = __any(nan_p);
+    if (lane == 0) sh.i32[wave] = nan_p;
     __syncthreads();
+    const bool any_nan = (sh.i32[0] | sh.i32[1] | sh.i32[2] | sh.i32[3]) != 0;
     if (wave == 0) {
+        const float u = a.uniforms[row];
         uint32_t pos;
         bool near;
-        scan_and_walk(
-            [&](uint32_t g) {
-                const uint32_t i = g * 64 + static_cast<uint32_t>(lane);
-                return i < keff ? sh.prob[i] : 0.0f;
-            },
-            keff, p, u, pos, near);
+        if (!any_nan) {
+            scan_and_walk_fast(prob, keff, p, u, pos, near);
+        } else {
+            scan_and_walk(
+                [&](uint32_t g) {
+                    const uint32_t i = g * 64 + static_cast<uint32_t>(lane);
+                    return i < keff ? prob[i] : 0.0f;
+                },
+                keff, p, u, pos, near);
+        }
         if (lane == 0)
-            write_row(a, row, static_cast<int32_t>(composite_index(sh.surv[pos])), sh.prob[pos],
+            write_row(a, row, static_cast<int32_t>(composite_index(sh.top[pos])), prob[pos],
                       near ? GE_FLAG_NEAR_BOUNDARY : 0);
     }
 }
 
-template <typename T, int EPT, int GPT>
-__global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
-    constexpr int W = sizeof(T) == 4 ? 4 : 8;  // elements per 16-byte load
-    constexpr int NV = EPT / W;                 // 16-byte loads per thread
-    constexpr int NW = EPT * sizeof(T) / 4;     // 32-bit words per thread
-    constexpr int CHUNK = kBlock * EPT;
-    constexpr int GSZ = EPT / GPT;
-    static_assert(EPT % W == 0 && EPT % GPT == 0 && EPT <= 64, "bad tiling");
+// A rescan of chunk c with m = k for the merge's fallback.
+template <typename T, int EPT>
+__device__ __forceinline__ uint32_t rescan_chunk(const RowCtx& rc, int c, uint32_t k, uint32_t* pbits,
+                                                 SelShared& sh, bool& ok) {
+    uint32_t n_out;
+    (void)chunk_slow<T, EPT>(rc, c * (kBlock * EPT), k, pbits, sh, n_out, ok);
+    return n_out;
+}
 
+template <typename T, int EPT>
+__global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
+    constexpr int CHUNK = kBlock * EPT;
     __shared__ uint32_t s_pbits[CHUNK / 32];
-    __shared__ Shared sh;
+    __shared__ SelShared sh;
 
     const int tid = threadIdx.x;
-    const int lane = __lane_id();
-    const int wave = tid >> 6;
     const int row = blockIdx.x / a.cpr;
     const int chunk = blockIdx.x - row * a.cpr;
     const int V = a.vocab;
@@ -764,249 +1429,28 @@ __global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
         }
         return;
     }
-    const T* rowp = static_cast<const T*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
-    const int32_t* hist;
-    int H;
-    row_history(a, row, hist, H);
-    const float r = p.repetition_penalty;
-    const bool pen = H > 0 && !(r == 1.0f);
-    const float cap = p.softcap;
-    const int c0 = chunk * CHUNK;
-    const int cend = min(c0 + CHUNK, V);
+    RowCtx rc;
+    rc.rowp = static_cast<const T*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
+    row_history(a, row, rc.hist, rc.H);
+    rc.row = row;
+    rc.V = V;
+    rc.vec_ok = a.vec_ok;
+    rc.r = p.repetition_penalty;
+    rc.pen = rc.H > 0 && !(rc.r == 1.0f);
+    rc.cap = p.softcap;
+    const uint32_t m = spec_m(k, a.cpr, CHUNK);
 
-    // Slot s of this thread is element c0 + ((s / W) * kBlock + tid) * W + s % W.
-    auto elem = [&](int s) { return c0 + ((s / W) * kBlock + tid) * W + (s % W); };
-    constexpr uint32_t kHole = 0x7fc00000u;  // NaN placed in penalised / out-of-range slots
+    uint32_t n_out;
+    bool ok;
+    const uint64_t gamma = chunk_topm<T, EPT>(rc, chunk * CHUNK, m, s_pbits, sh, n_out, ok);
 
-    // 1. Issue the chunk's loads first so their latency overlaps the bitmap build.
-    uint32_t d[NW];
-    if (a.vec_ok && c0 + CHUNK <= V) {
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const uint4 q = *reinterpret_cast<const uint4*>(rowp + c0 + (v * kBlock + tid) * W);
-            d[4 * v + 0] = q.x;
-            d[4 * v + 1] = q.y;
-            d[4 * v + 2] = q.z;
-            d[4 * v + 3] = q.w;
-        }
-    } else {
-#pragma unroll
-        for (int s = 0; s < EPT; ++s) {
-            const int e = elem(s);
-            const uint32_t bits = e < cend ? f2u(load_one(rowp, e)) : kHole;
-            if constexpr (W == 4) {
-                d[s] = bits;
-            } else if (s % 2 == 0) {
-                d[s / 2] = bits >> 16;
-            } else {
-                d[s / 2] |= bits & 0xffff0000u;
-            }
-        }
+    // Publish [guarantee, list padded with zeros], wait for the stores, then
+    // one ticket per workgroup; the last workgroup of the row merges.
+    uint64_t* slot = a.slots + static_cast<int64_t>(row) * kSlotWords + static_cast<int64_t>(chunk) * (m + 1);
+    for (uint32_t i = tid; i <= m; i += kBlock) {
+        const uint64_t v = i == 0 ? gamma : (i - 1 < n_out ? sh.list[i - 1] : 0ull);
+        store_shared(&slot[i], v);
     }
-    auto value = [&](int s) -> float {
-        if constexpr (W == 4) return u2f(d[s]);
-        else return u2f((s % 2 == 0) ? (d[s / 2] << 16) : (d[s / 2] & 0xffff0000u));
-    };
-
-    // 2. Penalty bitmap of this chunk (history loads kBatch-wide); penalised
-    //    slots become holes: fmax and ">= floor" below never select a NaN.
-    if (pen) {
-        for (int w = tid; w < CHUNK / 32; w += kBlock) s_pbits[w] = 0u;
-        if (tid == 0) sh.u32[5] = 0u;
-        __syncthreads();
-        for (int base = 0; base < H; base += kBlock * kBatch) {
-            int t[kBatch];
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int j = base + u * kBlock + tid;
-                t[u] = j < H ? hist[j] : -1;
-            }
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                if (t[u] >= c0 && t[u] < cend)
-                    atomicOr(&s_pbits[(t[u] - c0) >> 5], 1u << ((t[u] - c0) & 31));
-        }
-        __syncthreads();
-        // Each penalised slot is visited once here, so listing it dedupes the
-        // history; the list keeps the raw value for the final evaluation.
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const int li = (v * kBlock + tid) * W;  // W divides 32: one bitmap word
-            const uint32_t bits = (s_pbits[li >> 5] >> (li & 31)) & ((1u << W) - 1u);
-            if (bits) {
-#pragma unroll
-                for (int j = 0; j < W; ++j) {
-                    if ((bits >> j) & 1u) {
-                        const uint32_t pos = atomicAdd(&sh.u32[5], 1u);
-                        if (pos < static_cast<uint32_t>(kPenCap)) {
-                            sh.pen_idx[pos] = static_cast<uint32_t>(elem(v * W + j));
-                            sh.pen_raw[pos] = f2u(value(v * W + j));
-                        }
-                        if constexpr (W == 4) d[4 * v + j] = kHole;
-                        else if (j % 2 == 0) d[4 * v + j / 2] = (d[4 * v + j / 2] & 0xffff0000u) | (kHole >> 16);
-                        else d[4 * v + j / 2] = (d[4 * v + j / 2] & 0xffffu) | (kHole & 0xffff0000u);
-                    }
-                }
-            }
-        }
-    }
-
-    // 3. Group maxima of the raw values (holes ignored) and the chunk bound tau
-    //    over their order keys.
-    uint32_t gkey[GPT];
-    uint32_t gmx = 0, gmn = 0xffffffffu;
-#pragma unroll
-    for (int g = 0; g < GPT; ++g) {
-        float m = value(g * GSZ);
-#pragma unroll
-        for (int j = 1; j < GSZ; ++j) m = fmaxf(m, value(g * GSZ + j));
-        gkey[g] = order_key(m);
-        gmx = max(gmx, gkey[g]);
-        gmn = min(gmn, gkey[g]);
-    }
-    gmx = wave_max(gmx);
-    gmn = wave_min(gmn);
-    if (lane == 0) {
-        sh.u32[8 + wave] = gmx;
-        sh.u32[12 + wave] = gmn;
-    }
-    __syncthreads();
-    const uint32_t bmax = max(max(sh.u32[8], sh.u32[9]), max(sh.u32[10], sh.u32[11]));
-    const uint32_t bmin = min(min(sh.u32[12], sh.u32[13]), min(sh.u32[14], sh.u32[15]));
-    uint32_t tau;
-    if (k == 1) {
-        tau = bmax;
-    } else if (GPT == 1 && k <= 64) {
-        // Each wave: the ceil(k/4)-th largest of its 64 group maxima; the
-        // smallest of the four still leaves >= k maxima at or above it.
-        const uint32_t srt = bitonic_desc_wave_u32(gkey[0]);
-        const uint32_t tw = __shfl(srt, static_cast<int>((k + 3) / 4) - 1, 64);
-        if (lane == 0) sh.u32[16 + wave] = tw;
-        __syncthreads();
-        tau = min(min(sh.u32[16], sh.u32[17]), min(sh.u32[18], sh.u32[19]));
-    } else {
-        tau = block_kth(bmin, bmax, k,
-                        [&](auto&& f) {
-#pragma unroll
-                            for (int g = 0; g < GPT; ++g) f(gkey[g]);
-                        },
-                        sh);
-    }
-
-    // 4. Tie floor. A floor at or below kKeyNaN means "no pruning": fewer than
-    //    k real non-penalised logits are known, so every slot is a candidate
-    //    (NaN logits included, they sort last).
-    if (wave == 0) {
-        const uint32_t t = tie_floor(tau, cap);
-        if (lane == 0) sh.u32[7] = max(t, kKeyNaN);
-    }
-    __syncthreads();
-    const uint32_t thr = sh.u32[7];
-    const bool allpass = thr <= kKeyNaN;
-    const float floor_v = key_value(max(thr, kKeyNegInf));  // raw >= floor_v <=> key >= thr
-    uint64_t cmask = 0;  // non-penalised candidate slots
-    if (!allpass) {
-#pragma unroll
-        for (int s = 0; s < EPT; ++s) cmask |= static_cast<uint64_t>(value(s) >= floor_v) << s;
-    } else {
-#pragma unroll
-        for (int s = 0; s < EPT; ++s) {
-            const int e = elem(s);
-            bool c = e < cend;
-            if (c && pen) c = !((s_pbits[(e - c0) >> 5] >> ((e - c0) & 31)) & 1u);
-            cmask |= static_cast<uint64_t>(c) << s;
-        }
-    }
-
-    // 5. Compact the candidates into LDS (wave ballots, one region per wave),
-    //    evaluate final values there, publish.
-    uint32_t n_chunk;
-    const uint32_t wfirst = block_excl_scan(
-        __shfl(wave_incl_scan(static_cast<uint32_t>(__popcll(cmask))), 63, 64) * (lane == 63 ? 1u : 0u),
-        n_chunk, sh);
-    const uint32_t wave_base = __shfl(wfirst, 63, 64);
-    uint64_t* region = a.cand + static_cast<int64_t>(row) * a.cand_stride + static_cast<int64_t>(c0);
-    for (uint32_t base = 0; base < n_chunk; base += kSurvivorCap) {
-        // Opaque per round: stops the compiler from hoisting 64 slot tests and
-        // element indices out of this (nearly always single-trip) loop, which
-        // would hold them all in registers.
-        uint32_t cm_lo = static_cast<uint32_t>(cmask), cm_hi = static_cast<uint32_t>(cmask >> 32);
-        int ebase = c0 + tid * W;
-        asm volatile("" : "+v"(cm_lo), "+v"(cm_hi), "+v"(ebase));
-        const uint64_t cm = (static_cast<uint64_t>(cm_hi) << 32) | cm_lo;
-        uint32_t wb = wave_base;
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const uint32_t vbits = static_cast<uint32_t>(cm >> (v * W)) & ((1u << W) - 1u);
-            if (__ballot(vbits != 0u) == 0ull) continue;
-#pragma unroll
-            for (int j = 0; j < W; ++j) {
-                const int s = v * W + j;
-                const bool c = (vbits >> j) & 1u;
-                const uint64_t m = __ballot(c);
-                if (m) {
-                    const uint32_t o = wb + lanes_below(m);
-                    if (c && o >= base && o < base + kSurvivorCap) {
-                        sh.stage.raw[o - base] = f2u(value(s));
-                        sh.stage.tag[o - base] = static_cast<uint32_t>(ebase + v * kBlock * W + j);
-                    }
-                    wb += static_cast<uint32_t>(__popcll(m));
-                }
-            }
-        }
-        __syncthreads();
-        const uint32_t n = min(n_chunk - base, static_cast<uint32_t>(kSurvivorCap));
-        for (uint32_t i = tid; i < n; i += kBlock)
-            store_shared(&region[base + i],
-                         composite(order_key(softcap(u2f(sh.stage.raw[i]), cap)), sh.stage.tag[i]));
-        __syncthreads();
-    }
-
-    // Penalised tokens of the chunk, from the LDS list (or, if it overflowed,
-    // by claiming each in-range history id once: the thread whose atomicAnd
-    // clears its bit owns it). With r >= 1 the penalty never raises a value, so
-    // raw values below the floor cannot reach the top-k.
-    if (pen) {
-        if (tid == 0) sh.u32[6] = n_chunk;
-        __syncthreads();
-        const bool prune = r >= 1.0f && !allpass;
-        const uint32_t npen = sh.u32[5];
-        auto emit = [&](uint32_t t, float raw) {
-            if (prune && !(raw >= floor_v)) return;
-            const float f = penalize(softcap(raw, cap), r);
-            store_shared(&region[atomicAdd(&sh.u32[6], 1u)], composite(order_key(f), t));
-        };
-        if (npen <= static_cast<uint32_t>(kPenCap)) {
-            for (uint32_t i = tid; i < npen; i += kBlock) emit(sh.pen_idx[i], u2f(sh.pen_raw[i]));
-        } else {
-            for (int base = 0; base < H; base += kBlock * kBatch) {
-                int t[kBatch];
-#pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    const int j = base + u * kBlock + tid;
-                    t[u] = j < H ? hist[j] : -1;
-                }
-#pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    if (t[u] >= c0 && t[u] < cend) {
-                        const uint32_t bit = 1u << ((t[u] - c0) & 31);
-                        if (!(atomicAnd(&s_pbits[(t[u] - c0) >> 5], ~bit) & bit)) t[u] = -1;
-                    } else {
-                        t[u] = -1;
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < kBatch; ++u)
-                    if (t[u] >= 0) emit(static_cast<uint32_t>(t[u]), load_one(rowp, t[u]));
-            }
-        }
-        __syncthreads();
-        n_chunk = sh.u32[6];
-    }
-
-    // 6. Publish: every wave waits for its stores, then one ticket per
-    //    workgroup; the last workgroup of the row merges.
-    if (tid == 0) store_shared(&a.chunk_count[row * kMaxChunks + chunk], n_chunk);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -1016,27 +1460,38 @@ __global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
     }
     __syncthreads();
     if (sh.u32[0] == 0u) return;
-    merge_row<T>(a, sh, row, p, greedy, k, rowp, hist, H, pen, CHUNK);
+
+    uint32_t nt;
+    if (!merge_collect(a, sh, row, k, m, nt)) {
+        // Fallback: chunks whose guarantee is above the k-th largest listed
+        // key may hold more of the row's top-k than they listed.
+        for (int c = next_rescan(sh, 0, a.cpr, nt, k); c >= 0; c = next_rescan(sh, c + 1, a.cpr, nt, k)) {
+            bool rok;
+            const uint32_t nl = rescan_chunk<T, EPT>(rc, c, k, s_pbits, sh, rok);
+            if (!rok) {
+                if (tid == 0) write_row(a, row, -1, 0.0f, GE_FLAG_UNSUPPORTED);
+                return;
+            }
+            nt = absorb_list(sh, nt, nl, k);
+        }
+    }
+    merge_finish<T>(a, sh, rc, p, greedy, min(nt, k));
 }
 
 template <typename T, int EPT>
-hipError_t launch_t(const DevArgs& a, hipStream_t s, int gpt) {
+hipError_t launch_t(const DevArgs& a, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(a.rows * a.cpr));
     const dim3 block(kBlock);
-    switch (gpt) {
-        case 1: hipLaunchKernelGGL((select_kernel<T, EPT, 1>), grid, block, 0, s, a); break;
-        case 4: hipLaunchKernelGGL((select_kernel<T, EPT, 4>), grid, block, 0, s, a); break;
-        default: hipLaunchKernelGGL((select_kernel<T, EPT, 16>), grid, block, 0, s, a); break;
-    }
+    hipLaunchKernelGGL((select_kernel<T, EPT>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_select(const DevArgs& a, hipStream_t stream, int ept, int gpt) {
+hipError_t launch_select(const DevArgs& a, hipStream_t stream, int ept) {
     if (a.dtype == GE_DTYPE_BF16)
-        return ept == 16 ? launch_t<uint16_t, 16>(a, stream, gpt) : launch_t<uint16_t, 64>(a, stream, gpt);
-    return ept == 16 ? launch_t<float, 16>(a, stream, gpt) : launch_t<float, 64>(a, stream, gpt);
+        return ept == 16 ? launch_t<uint16_t, 16>(a, stream) : launch_t<uint16_t, 64>(a, stream);
+    return ept == 16 ? launch_t<float, 16>(a, stream) : launch_t<float, 64>(a, stream);
 }
 
 }  // namespace ge

@@ -112,14 +112,7 @@ def _random_case(rng, case):
 def test_random_small_cases(sampler):
     rng = np.random.default_rng(1234)
     for case in range(120):
-        w = _random_case(rng, case)
-        # Rows whose survivors exceed the LDS list are reported, not sampled;
-        # skip those here (covered by test_tie_overflow_is_flagged).
-        gpu = run_gpu(sampler, w)
-        if np.any(gpu[2] & 2):
-            continue
-        ora = run_oracle(w)
-        assert_parity(w, gpu, ora, w.name)
+        _check(sampler, _random_case(rng, case))
 
 
 def test_nan_logits(sampler):
@@ -168,10 +161,45 @@ def test_per_row_params(sampler):
     assert np.array_equal(probs.cpu().numpy().view(np.uint32), ora.probs.view(np.uint32))
 
 
-def test_tie_overflow_is_flagged(sampler):
-    # All-equal logits over a large vocabulary leave more exact ties than the
-    # merge list holds; the row must be reported (token -1, flag 2), never wrong.
-    w = small_workload("all-equal", np.zeros(200000, np.float32), dict(temperature=1.0, top_k=64))
-    tokens, probs, flags = run_gpu(sampler, w)
-    ora = run_oracle(w)
-    assert (tokens[0] == ora.tokens[0]) or (tokens[0] == -1 and flags[0] & 2)
+def test_massive_ties_are_exact(sampler):
+    # All-equal logits: every chunk's candidates overflow LDS, so the exact
+    # routine (radix select, lowest indices of the tie class) runs, and the
+    # merge must rescan the low chunks: the top-k are indices 0..k-1.
+    for k in (1, 64, 1024):
+        w = small_workload(f"all-equal-k{k}", np.zeros(200000, np.float32), dict(temperature=1.0, top_k=k))
+        _check(sampler, w)
+    # Masked vocabulary: a few finite logits, the rest -inf (softcap maps
+    # them to -30, a tie class of ~262k tokens that top-k 64 reaches).
+    rng = np.random.default_rng(21)
+    x = np.full((2, W.VOCAB), -np.inf, np.float32)
+    for r in range(2):
+        x[r, rng.choice(W.VOCAB, 10, replace=False)] = rng.standard_normal(10).astype(np.float32) * 3
+    _check(sampler, small_workload("masked", x, dict(temperature=1.0, top_k=64, softcap=30.0)))
+    _check(sampler, small_workload("masked-nocap", x, dict(temperature=0.7, top_k=40, top_p=1.0)))
+    # Ties with a penalty on part of the tie class.
+    hist = np.arange(0, 5000, 3, dtype=np.int32)
+    w = small_workload("ties-penalty", np.ones(100000, np.float32), dict(temperature=1.0, top_k=300,
+                       repetition_penalty=1.3), history=hist, offsets=np.array([0, hist.size], np.int32))
+    _check(sampler, w)
+
+
+@pytest.mark.parametrize("rows", [1, 64])
+def test_clustered_top_k_takes_the_rescan(sampler, rows):
+    # Each chunk lists only about k / chunks + 5 sigma entries; when the row's
+    # top-k sits in one chunk (sorted logits, or one hot region) the merge
+    # rescans that chunk with m = k. Results must still be exact.
+    rng = np.random.default_rng(33 + rows)
+    V = W.VOCAB
+    base = rng.standard_normal((rows, V)).astype(np.float32)
+    desc = -np.sort(base, axis=1)                     # descending: top-k in chunk 0
+    asc = np.sort(base, axis=1)                       # ascending: top-k in the last chunk
+    hot = base.copy()
+    hot[:, 70000:72000] += 6.0                        # one hot region
+    for name, x in (("desc", desc), ("asc", asc), ("hot", hot)):
+        for k, T, p in ((40, 0.7, 0.9), (64, 1.0, 0.95), (1024, 1.0, 0.99)):
+            hist = rng.integers(0, V, size=rows * 64).astype(np.int32)
+            offs = (np.arange(rows + 1) * 64).astype(np.int32)
+            w = small_workload(f"{name}-k{k}-r{rows}", np.ascontiguousarray(x),
+                               dict(temperature=T, top_k=k, top_p=p, softcap=30.0, repetition_penalty=1.15),
+                               history=hist, offsets=offs, uniforms=W.mt_uniforms(k + rows, rows))
+            _check(sampler, w)
