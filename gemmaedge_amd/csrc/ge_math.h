@@ -166,7 +166,10 @@ __host__ __device__ inline uint64_t exp2_table(uint32_t i) {
 }
 
 // ARM optimized-routines expf (glibc e_expf.c, FMA build).
-__host__ __device__ inline float expf_glibc(float x) {
+// `tab(i)` returns table entry i: the constant table, or a copy of it that a
+// kernel staged in LDS (same bits).
+template <typename Tab>
+__host__ __device__ inline float expf_glibc_tab(float x, Tab&& tab) {
     const double kInvLn2N = 0x1.71547652b82fep+5;  // 32 / ln2
     const double kShift = 0x1.8p+52;
     const double C0 = 0x1.c6af84b912394p-20;       // poly / N^3, N^2, N
@@ -185,7 +188,7 @@ __host__ __device__ inline float expf_glibc(float x) {
     const uint64_t ki = d2u(kd);
     kd -= kShift;
     const double r = fma(kInvLn2N, xd, -kd);
-    uint64_t t = exp2_table(static_cast<uint32_t>(ki % 32));
+    uint64_t t = tab(static_cast<uint32_t>(ki % 32));
     t += ki << 47;
     const double s = u2d(t);
     const double z = fma(C0, r, C1);
@@ -194,6 +197,10 @@ __host__ __device__ inline float expf_glibc(float x) {
     y = fma(z, r2, y);
     y = y * s;
     return static_cast<float>(y);
+}
+
+__host__ __device__ inline float expf_glibc(float x) {
+    return expf_glibc_tab(x, [](uint32_t i) { return exp2_table(i); });
 }
 
 // Final-logit softcap, src/generation.cpp:431-437: c * tanh(l / c) when c > 0.

@@ -74,6 +74,7 @@ __device__ __forceinline__ uint32_t wave_min(uint32_t v) { return wave::min_u32(
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { return wave::max_u64(v); }
 __device__ __forceinline__ int wave_min_i(int v) { return wave::min_i32(v); }
 __device__ __forceinline__ double wave_sum(double v) { return wave::sum_f64(v); }
+__device__ __forceinline__ double wave_incl_f64(double v) { return wave::incl_f64(v); }
 
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
@@ -88,25 +89,6 @@ __device__ __forceinline__ double readlane_d(double v, int i) {
     const uint64_t b = d2u(v);
     const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(b), i);
     const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(b >> 32), i);
-    return u2d((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-// Lane I of the result is `v` (a wave-uniform value); other lanes keep `old`.
-template <int I>
-__device__ __forceinline__ uint32_t writelane_u(uint32_t v, uint32_t old) {
-    const uint32_t s = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
-    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(old) : "s"(s), "i"(I));
-    return old;
-}
-template <int I>
-__device__ __forceinline__ float writelane_f(float v, float old) {
-    return u2f(writelane_u<I>(f2u(v), f2u(old)));
-}
-template <int I>
-__device__ __forceinline__ double writelane_d(double v, double old) {
-    const uint64_t b = d2u(v), o = d2u(old);
-    const uint32_t lo = writelane_u<I>(static_cast<uint32_t>(b), static_cast<uint32_t>(o));
-    const uint32_t hi = writelane_u<I>(static_cast<uint32_t>(b >> 32), static_cast<uint32_t>(o >> 32));
     return u2d((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
@@ -158,13 +140,13 @@ __device__ __forceinline__ int lsb_exponent(float e) {
 }
 
 // List length each chunk publishes for a row with effective top-k `k`: the
-// mean share k / cpr plus five binomial standard deviations plus 6, capped by
+// mean share k / cpr plus four binomial standard deviations plus 4, capped by
 // k, by the chunk length and by the row's slot capacity (cpr * (m + 1) words
 // <= kSlotWords). The host and every workgroup of the row compute the same m.
 __device__ __forceinline__ uint32_t spec_m(uint32_t k, int cpr, int chunk_len) {
     if (k <= 1u) return 1u;
     const float mu = static_cast<float>(k) / static_cast<float>(cpr);
-    uint32_t m = static_cast<uint32_t>(ceilf(mu + 5.0f * sqrtf(mu))) + 6u;
+    uint32_t m = static_cast<uint32_t>(ceilf(mu + 4.0f * sqrtf(mu))) + 4u;
     m = min(m, k);
     m = min(m, static_cast<uint32_t>(chunk_len));
     m = min(m, static_cast<uint32_t>(kSlotWords / cpr - 1));
@@ -176,6 +158,7 @@ struct __align__(16) SelShared {
     uint64_t list[kMaxTopK];     // chunk routine output: its top-m, sorted descending
     uint64_t top[kMaxTopK];      // merge: the row's top-k, sorted descending
     uint64_t gam[kMaxChunks];    // merge: guarantee of each chunk
+    uint64_t exp_tab[32];        // merge: the expf table (2^(i/32)), staged from constant memory
     uint32_t hist[256];
     uint64_t u64[4];
     double f64[kBlock / 64];
@@ -328,16 +311,12 @@ __device__ __forceinline__ uint32_t block_kth_exact(uint32_t lo, uint32_t hi, ui
 // non-decreasing (glibc tanhf is monotone on all floats), so the keys with
 // equal capped value form an interval. Usually tau-1 already caps lower and
 // one evaluation round decides; otherwise a 64-way search finds the floor.
-__device__ __forceinline__ uint32_t tie_floor(uint32_t tau, float cap, float* cap_tau = nullptr) {
-    if (!(cap > 0.0f) || tau <= kKeyNegInf) {
-        if (cap_tau) *cap_tau = softcap(key_value(tau), cap);
-        return tau;
-    }
+// tie_floor with its first evaluation supplied: target = softcap(tau),
+// below = softcap(tau - 1) (both wave-uniform).
+__device__ __forceinline__ uint32_t tie_floor_given(uint32_t tau, float cap, float target, float below) {
+    if (!(cap > 0.0f) || tau <= kKeyNegInf) return tau;
+    if (below != target) return tau;
     const int lane = __lane_id();
-    const float s01 = softcap(key_value(tau - static_cast<uint32_t>(lane & 1)), cap);
-    const float target = u2f(wave::readlane(f2u(s01), 0));
-    if (cap_tau) *cap_tau = target;
-    if (u2f(wave::readlane(f2u(s01), 1)) != target) return tau;
     uint32_t hi = tau - 1;  // lowest key known to map to target
     uint32_t lo;            // a key known to map below target
     uint64_t step = 1;
@@ -374,6 +353,13 @@ __device__ __forceinline__ uint32_t tie_floor(uint32_t tau, float cap, float* ca
         hi = xj;
     }
     return hi;
+}
+
+__device__ __forceinline__ uint32_t tie_floor(uint32_t tau, float cap) {
+    if (!(cap > 0.0f) || tau <= kKeyNegInf) return tau;
+    const int lane = __lane_id();
+    const float s01 = softcap(key_value(tau - static_cast<uint32_t>(lane & 1)), cap);
+    return tie_floor_given(tau, cap, u2f(wave::readlane(f2u(s01), 0)), u2f(wave::readlane(f2u(s01), 1)));
 }
 
 // Mirror of tie_floor: the largest raw key x >= r with softcap(x) ==
@@ -659,8 +645,69 @@ __device__ __forceinline__ uint32_t wave_kth(uint32_t key, uint32_t t) {
     return mx;
 }
 
-// Rank of x among the staged keys: per-wave segments sh.stage[w * kSeg, +cnt[w]).
+// Per-wave staging segments: wave w stages its keys in
+// sh.stage[w * kSeg, w * kSeg + cnt[w]), padded with a zero key to an even
+// count (the rank reads keys in pairs).
 constexpr int kSeg = kStage / (kBlock / 64);
+// sh.u32 words holding the segment counts. Not shared with any other helper's
+// scratch: block_excl_scan (24..27) can run right after the counts are read.
+constexpr int kSegCount = 28;
+
+// dst[0, min(n, m)) = the largest of the n <= kBlock distinct non-zero keys in
+// the segments, sorted descending (rank by counting, keys in pairs).
+// Block-uniform (one barrier at the end).
+__device__ __forceinline__ void seg_rank_top(const uint64_t* stage, const uint32_t (&cnt)[kBlock / 64],
+                                             uint32_t n, uint32_t m, uint64_t* dst) {
+    const int tid = threadIdx.x;
+    if (static_cast<uint32_t>(tid) < n) {
+        int w = 0;
+        uint32_t i = static_cast<uint32_t>(tid);
+        while (i >= cnt[w]) {
+            i -= cnt[w];
+            ++w;
+        }
+        const uint64_t x = stage[w * kSeg + i];
+        uint32_t rk = 0;
+#pragma unroll
+        for (int v = 0; v < kBlock / 64; ++v) {
+            const ulonglong2* sv = reinterpret_cast<const ulonglong2*>(stage + v * kSeg);
+#pragma unroll 4
+            for (uint32_t j = 0; j < (cnt[v] + 1) / 2; ++j) {
+                const ulonglong2 q = sv[j];
+                rk += q.x > x ? 1u : 0u;
+                rk += q.y > x ? 1u : 0u;
+            }
+        }
+        if (rk < m) dst[rk] = x;
+    }
+    __syncthreads();
+}
+
+// Moves the n keys of the segments to stage[0, n) (n <= kStage). Block-uniform.
+__device__ __forceinline__ void seg_gather(uint64_t* stage, const uint32_t (&cnt)[kBlock / 64], uint32_t n) {
+    const int tid = threadIdx.x;
+    uint64_t tmp[kStage / kBlock];
+#pragma unroll
+    for (int q = 0; q < kStage / kBlock; ++q) {
+        uint32_t i = static_cast<uint32_t>(q * kBlock + tid);
+        tmp[q] = 0ull;
+        if (i < n) {
+            int w = 0;
+            while (i >= cnt[w]) {
+                i -= cnt[w];
+                ++w;
+            }
+            tmp[q] = stage[w * kSeg + i];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kStage / kBlock; ++q) {
+        const uint32_t i = static_cast<uint32_t>(q * kBlock + tid);
+        if (i < n) stage[i] = tmp[q];
+    }
+    __syncthreads();
+}
 
 // Exact top-m of one chunk (elements [c0, min(c0 + CHUNK, V))) by composite
 // final key, sorted descending into sh.list[0, n_out). Returns the chunk's
@@ -802,13 +849,19 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     //    own maximum (most candidates are lane maxima, so their final values
     //    are ready when they are staged), and every wave marks the penalised
     //    tokens in the bitmap from the ids loaded at the start.
-    const float lcap = softcap(lmf, cap);
+    //    One softcap evaluation per lane: lanes 0 and 1 of wave 0 take
+    //    tau and tau - 1 (the tie floor's first probe), every other lane its
+    //    own maximum.
+    const bool probe = wave == 0 && lane < 2;
+    const float sc = softcap(probe ? key_value(tau - static_cast<uint32_t>(lane)) : lmf, cap);
+    const float lcap = sc;  // meaningful where !probe
     if (wave == 0) {
-        float ct;
-        const uint32_t thr0 = max(tie_floor(tau, cap, &ct), kKeyNaN);
+        const float ct = u2f(wave::readlane(f2u(sc), 0));
+        const float cb = u2f(wave::readlane(f2u(sc), 1));
+        const uint32_t thr0 = max(tie_floor_given(tau, cap, ct, cb), kKeyNaN);
         if (lane == 0) {
             sh.u32[2] = thr0;
-            sh.u32[3] = thr0 <= kKeyNaN ? 0u : order_key(ct);
+            sh.u32[3] = thr0 <= kKeyNaN ? 0u : order_key(cap > 0.0f ? ct : key_value(tau));
         }
     }
     if (rc.pen) {
@@ -854,7 +907,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             if (c && o < static_cast<uint32_t>(kSeg)) {
                 const int e = ebase + (s / W) * kBlock * W + s % W;
                 const float x = value(s);
-                const bool known = f2u(x) == f2u(lmf);
+                const bool known = !probe && f2u(x) == f2u(lmf);
                 seg[o] = (static_cast<uint64_t>(static_cast<uint32_t>(e) | (known ? kKnown : 0u)) << 32) |
                          f2u(known ? lcap : x);
             }
@@ -881,7 +934,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     fence_words();
     // Pad an odd segment with an empty key (the rank reads keys in pairs).
     if (lane == 0) {
-        sh.u32[24 + wave] = woff;
+        sh.u32[kSegCount + wave] = woff;
         if ((woff & 1u) && woff < static_cast<uint32_t>(kSeg)) seg[woff] = 0ull;
     }
     __syncthreads();
@@ -890,7 +943,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     bool seg_over = false;
 #pragma unroll
     for (int w = 0; w < kBlock / 64; ++w) {
-        cnt[w] = sh.u32[24 + w];
+        cnt[w] = sh.u32[kSegCount + w];
         n_c += cnt[w];
         seg_over |= cnt[w] >= static_cast<uint32_t>(kSeg);
     }
@@ -911,53 +964,12 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     }
     __syncthreads();
     // 6. Top m, sorted. Up to kBlock candidates: rank by counting over the
-    //    segments (keys in pairs); more: gather them and sort.
+    //    segments; more: gather them and sort.
     if (n_c <= static_cast<uint32_t>(kBlock)) {
-        if (static_cast<uint32_t>(tid) < n_c) {
-            int w = 0;
-            uint32_t i = static_cast<uint32_t>(tid);
-            while (i >= cnt[w]) {
-                i -= cnt[w];
-                ++w;
-            }
-            const uint64_t x = sh.stage[w * kSeg + i];
-            uint32_t rk = 0;
-#pragma unroll
-            for (int v = 0; v < kBlock / 64; ++v) {
-                const ulonglong2* sv = reinterpret_cast<const ulonglong2*>(sh.stage + v * kSeg);
-#pragma unroll 4
-                for (uint32_t j = 0; j < (cnt[v] + 1) / 2; ++j) {
-                    const ulonglong2 q = sv[j];
-                    rk += q.x > x ? 1u : 0u;
-                    rk += q.y > x ? 1u : 0u;
-                }
-            }
-            if (rk < m) sh.list[rk] = x;
-        }
-        __syncthreads();
+        seg_rank_top(sh.stage, cnt, n_c, m, sh.list);
         n_out = min(n_c, m);
     } else {
-        uint64_t tmp[kStage / kBlock];
-#pragma unroll
-        for (int q = 0; q < kStage / kBlock; ++q) {
-            uint32_t i = static_cast<uint32_t>(q * kBlock + tid);
-            tmp[q] = 0ull;
-            if (i < n_c) {
-                int w = 0;
-                while (i >= cnt[w]) {
-                    i -= cnt[w];
-                    ++w;
-                }
-                tmp[q] = sh.stage[w * kSeg + i];
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < kStage / kBlock; ++q) {
-            const uint32_t i = static_cast<uint32_t>(q * kBlock + tid);
-            if (i < n_c) sh.stage[i] = tmp[q];
-        }
-        __syncthreads();
+        seg_gather(sh.stage, cnt, n_c);
         n_out = select_top(sh.stage, n_c, m, sh.list);
     }
     // The guarantee: the larger of the floor's and the m-th listed key.
@@ -987,8 +999,8 @@ __device__ __forceinline__ void write_row(const DevArgs& a, int row, int32_t tok
 // evaluated by one whole wave, for any values (NaN included). seg_prob(g)
 // returns this lane's probability of entry g * 64 + lane (0 past keff). Every
 // lane computes the same sequential fp32 (and, for the boundary distances,
-// double) chain; lane j keeps step j of each 64-entry segment, so each stop
-// test is one ballot.
+// double) chain; lane j keeps step j of each 64-entry segment (a select), so
+// each stop test is one ballot.
 template <typename P>
 __device__ __forceinline__ void scan_and_walk(P&& seg_prob, uint32_t keff, const ge_sample_params& p,
                                               float u, uint32_t& pos_out, bool& near_out) {
@@ -1003,10 +1015,12 @@ __device__ __forceinline__ void scan_and_walk(P&& seg_prob, uint32_t keff, const
         const float pl = seg_prob(g);
         const float before = cum;
         float cl = 0.0f;
-        static_for<0, 64>([&](auto J) {
-            cum = cum + readlane_f(pl, J);
-            cl = writelane_f<J>(cum, cl);
-        });
+        for (int q = 0; q < 64; q += 16) {
+            static_for<0, 16>([&](auto J) {
+                cum = cum + readlane_f(pl, q + J);
+                cl = lane == q + J ? cum : cl;
+            });
+        }
         const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
         const bool valid = idx < keff && idx > 0;
         const uint64_t mh = __ballot(valid && pl < minimum);     // checked before adding
@@ -1037,13 +1051,15 @@ __device__ __forceinline__ void scan_and_walk(P&& seg_prob, uint32_t keff, const
         const double dbefore = dc;
         float chl = 0.0f;
         double dl = 0.0;
-        static_for<0, 64>([&](auto J) {
-            const float pj = readlane_f(pl, J);
-            choice = choice - pj;
-            dc = dc + static_cast<double>(pj);
-            chl = writelane_f<J>(choice, chl);
-            dl = writelane_d<J>(dc, dl);
-        });
+        for (int q = 0; q < 64; q += 16) {
+            static_for<0, 16>([&](auto J) {
+                const float pj = readlane_f(pl, q + J);
+                choice = choice - pj;
+                dc = dc + static_cast<double>(pj);
+                chl = lane == q + J ? choice : chl;
+                dl = lane == q + J ? dc : dl;
+            });
+        }
         const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
         const uint64_t hit = __ballot(idx < keep && chl <= 0.0f);
         int j = -1;
@@ -1069,94 +1085,117 @@ __device__ __forceinline__ void scan_and_walk(P&& seg_prob, uint32_t keff, const
 // The same chains when no probability is NaN. Then the probabilities are
 // non-increasing (expf is monotone and the values are sorted), so the min-p
 // cut is one parallel search and the cumulative / choice chains are
-// monotone: every lane runs the sequential fp32 adds in registers, 16 steps
-// per block, reading the probabilities as broadcast LDS loads, and only the
-// block holding the stop is examined step by step.
-__device__ __forceinline__ void scan_and_walk_fast(const float* prob, uint32_t keff, const ge_sample_params& p,
+// monotone. Every lane runs the reference's sequential fp32 adds, 64 steps per
+// segment, with the step's probability broadcast from the lane holding it
+// (v_readlane, off the add chain); lane i keeps the sum after step i (a
+// v_cndmask, also off the chain), so one ballot finds the stop in a segment.
+// seg_prob(g) returns this lane's probability of entry g * 64 + lane (any
+// finite value past keff; those entries are masked here).
+template <typename P>
+__device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, uint32_t keff, const ge_sample_params& p,
                                                    float u, uint32_t& pos_out, bool& near_out) {
-    constexpr int B = 16;
     const int lane = __lane_id();
-    const float minimum = prob[0] * p.min_p;
-    // min-p: first j >= 1 with p_j < minimum (checked before adding p_j).
+    const float p0 = readlane_f(seg_prob(0u), 0);
+    const float minimum = p0 * p.min_p;
+    // min-p: first j >= 1 with p_j < minimum (checked before adding p_j);
+    // none when minimum <= 0 (probabilities are >= 0).
     uint32_t limit = keff;
-    for (uint32_t base = 0; base < keff; base += 64) {
-        const uint32_t j = base + static_cast<uint32_t>(lane);
-        const bool c = j >= 1 && j < keff && prob[j < keff ? j : 0] < minimum;
-        const uint64_t h = __ballot(c);
-        if (h) {
-            limit = base + static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(h)) - 1);
-            break;
+    if (minimum > 0.0f) {
+        for (uint32_t g = 0; g * 64 < keff; ++g) {
+            const uint32_t j = g * 64 + static_cast<uint32_t>(lane);
+            const uint64_t h = __ballot(j >= 1 && j < keff && seg_prob(g) < minimum);
+            if (h) {
+                limit = g * 64 + static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(h)) - 1);
+                break;
+            }
         }
     }
-    // top-p: first j >= 1, j < limit, with cum_j >= top_p.
+    // top-p: first j >= 1, j < limit, with cum_j >= top_p. Steps run in
+    // sub-blocks of 16; the scan leaves the segment after the sub-block that
+    // holds the stop.
     float cum = 0.0f;
     float mass = 0.0f;
     uint32_t keep = limit;
     bool stopped = false;
-    for (uint32_t j0 = 0; j0 < limit && !stopped; j0 += B) {
-        float c[B];
-#pragma unroll
-        for (int i = 0; i < B; ++i) {
-            const uint32_t j = j0 + i;
-            const float pj = j < limit ? prob[j] : 0.0f;
-            cum = cum + pj;
-            c[i] = cum;
-        }
-        int hit = B;
-#pragma unroll
-        for (int i = B - 1; i >= 0; --i) {
-            const uint32_t j = j0 + i;
-            if (j >= 1 && j < limit && c[i] >= p.top_p) hit = i;
-        }
-        if (hit < B) {
-            keep = j0 + hit + 1;
-#pragma unroll
-            for (int i = 0; i < B; ++i)
-                if (i == hit) mass = c[i];
-            stopped = true;
+    for (uint32_t g = 0; g * 64 < limit && !stopped; ++g) {
+        const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
+        const float pl = idx < limit ? seg_prob(g) : 0.0f;
+        float cl = 0.0f;
+        for (int q = 0; q < 64 && !stopped; q += 16) {
+            static_for<0, 16>([&](auto J) {
+                cum = cum + readlane_f(pl, q + J);
+                cl = lane == q + J ? cum : cl;
+            });
+            const uint64_t th = __ballot(lane < q + 16 && idx >= 1 && idx < limit && cl >= p.top_p);
+            if (th) {
+                const int jt = __ffsll(static_cast<unsigned long long>(th)) - 1;
+                keep = g * 64 + static_cast<uint32_t>(jt) + 1;
+                mass = readlane_f(cl, jt);
+                stopped = true;
+            }
         }
     }
     if (!stopped) mass = cum;  // min-p cut or all keff kept
-    // Draw: uniform_real_distribution(0, mass), then the subtract walk.
+    // Draw: uniform_real_distribution(0, mass), then the subtract walk with
+    // the double CDF boundaries around the pick.
     const float choice0 = u * mass + 0.0f;
     float choice = choice0;
-    double dc = 0.0;
-    uint32_t pos = keep - 1;
-    double c_before = 0.0, c_at = 0.0;
-    for (uint32_t j0 = 0; j0 < keep; j0 += B) {
-        float ch[B];
-        double dd[B];
-        const double dbefore = dc;
-#pragma unroll
-        for (int i = 0; i < B; ++i) {
-            const uint32_t j = j0 + i;
-            const float pj = j < keep ? prob[j] : 0.0f;
-            choice = choice - pj;
-            dc = dc + static_cast<double>(pj);
-            ch[i] = choice;
-            dd[i] = dc;
-        }
-        int hit = B;
-#pragma unroll
-        for (int i = B - 1; i >= 0; --i) {
-            const uint32_t j = j0 + i;
-            if (j < keep && ch[i] <= 0.0f) hit = i;
-        }
-        int at = -1;
-        if (hit < B) {
-            pos = j0 + hit;
-            at = hit;
-        } else if (j0 + B >= keep) {
-            at = static_cast<int>(keep - 1 - j0);  // fallthrough return, generation.cpp:126
-        }
-        if (at >= 0) {
-#pragma unroll
-            for (int i = 0; i < B; ++i) {
-                if (i == at) c_at = dd[i];
-                if (i == at - 1) c_before = dd[i];
+    uint32_t pos = keep - 1;  // fallthrough return, generation.cpp:126
+    bool found = false;
+    for (uint32_t g = 0; g * 64 < keep && !found; ++g) {
+        const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
+        const float pl = idx < keep ? seg_prob(g) : 0.0f;
+        float chl = 0.0f;
+        for (int q = 0; q < 64 && !found; q += 16) {
+            static_for<0, 16>([&](auto J) {
+                choice = choice - readlane_f(pl, q + J);
+                chl = lane == q + J ? choice : chl;
+            });
+            const uint64_t hit = __ballot(lane < q + 16 && idx < keep && chl <= 0.0f);
+            if (hit) {
+                pos = g * 64 + static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(hit)) - 1);
+                found = true;
             }
-            if (at == 0) c_before = dbefore;
-            break;
+        }
+    }
+    // The reference's boundary sums: c_at = sum_{i <= pos} (double)p_i in
+    // order, c_before the same up to pos - 1. A wave prefix sum gives them
+    // exactly when every term is a multiple of 2^L with L >= -52 (all partial
+    // sums are below 2, so 53 bits hold them in any order); else replay.
+    double c_before = 0.0, c_at = 0.0;
+    {
+        const uint32_t gp = pos / 64;
+        double base = 0.0;
+        int lmin = INT_MAX;
+        for (uint32_t g = 0; g <= gp; ++g) {
+            const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
+            const float pl = idx <= pos ? seg_prob(g) : 0.0f;
+            if (pl > 0.0f) lmin = min(lmin, lsb_exponent(pl));
+        }
+        lmin = wave_min_i(lmin);
+        if (lmin >= -52) {
+            for (uint32_t g = 0; g <= gp; ++g) {
+                const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
+                const float pl = idx <= pos ? seg_prob(g) : 0.0f;
+                const double incl = base + wave_incl_f64(static_cast<double>(pl));
+                if (g == gp) {
+                    const int at = static_cast<int>(pos - g * 64);
+                    c_at = readlane_d(incl, at);
+                    c_before = at > 0 ? readlane_d(incl, at - 1) : base;
+                }
+                base = readlane_d(incl, 63);
+            }
+        } else {
+            double dc = 0.0;
+            for (uint32_t g = 0; g <= gp; ++g) {
+                const float pl = seg_prob(g);
+                const int last = g == gp ? static_cast<int>(pos - g * 64) : 63;
+                for (int i = 0; i <= last; ++i) {
+                    c_before = dc;
+                    dc = dc + static_cast<double>(readlane_f(pl, i));
+                }
+            }
+            c_at = dc;
         }
     }
     bool near = false;
@@ -1166,18 +1205,6 @@ __device__ __forceinline__ void scan_and_walk_fast(const float* prob, uint32_t k
     near_out = near;
 }
 
-// std::max_element (generation.cpp:66-70) keeps index 0 when its value is NaN
-// (NaN < x is false), so greedy returns 0 then. Token 0's final value is NaN
-// iff its raw value is, unless the penalty itself is NaN and 0 is in history.
-template <typename T>
-__device__ __forceinline__ bool final0_is_nan(const T* rowp, float cap, bool pen, float r,
-                                              const int32_t* hist, int H) {
-    if (__builtin_isnan(softcap(load_one(rowp, 0), cap))) return true;
-    if (!pen || !__builtin_isnan(r)) return false;
-    for (int j = 0; j < H; ++j)
-        if (hist[j] == 0) return true;
-    return false;
-}
 
 // sh.top[0, nt) := the largest k distinct keys of sh.top[0, nt) and
 // sh.list[0, nl), sorted descending. Returns the new nt. Block-uniform.
@@ -1216,6 +1243,7 @@ __device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, i
                                               uint32_t m, uint32_t& nt) {
     const int tid = threadIdx.x;
     const int lane = __lane_id();
+    if (tid < 32) sh.exp_tab[tid] = exp2_table(static_cast<uint32_t>(tid));  // in flight with the slots
     constexpr int kPer = kSlotWords / kBlock;
     const uint32_t sl = m + 1;
     const uint32_t words = static_cast<uint32_t>(a.cpr) * sl;  // <= kSlotWords
@@ -1252,19 +1280,80 @@ __device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, i
     __syncthreads();
     const uint64_t gam_max = sh.u64[0];
 
-    // Entries at or above the largest guarantee.
-    uint32_t nsel;
+    // Entries at or above the largest guarantee, staged in per-wave segments.
+    uint32_t nsel = 0;
     {
-        uint32_t cnt = 0;
+        const int wave = tid >> 6;
+        uint64_t* seg = sh.stage + wave * kSeg;
+        uint32_t woff = 0;  // <= kPer * 64 = kSeg
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) cnt += (wp[i] != 0u && w[i] != 0ull && w[i] >= gam_max) ? 1u : 0u;
-        uint32_t pos = block_excl_scan(cnt, nsel, sh);
-#pragma unroll
-        for (int i = 0; i < kPer; ++i)
-            if (wp[i] != 0u && w[i] != 0ull && w[i] >= gam_max) sh.stage[pos++] = w[i];
+        for (int i = 0; i < kPer; ++i) {
+            const bool c = wp[i] != 0u && w[i] != 0ull && w[i] >= gam_max;
+            const uint64_t mk = __ballot(c);
+            if (c) seg[woff + lanes_below(mk)] = w[i];
+            woff += static_cast<uint32_t>(__popcll(mk));
+        }
+        if (lane == 0) {
+            sh.u32[kSegCount + wave] = woff;
+            if ((woff & 1u) && woff < static_cast<uint32_t>(kSeg)) seg[woff] = 0ull;
+        }
     }
     __syncthreads();
+    uint32_t cnt[kBlock / 64];
+#pragma unroll
+    for (int v = 0; v < kBlock / 64; ++v) {
+        cnt[v] = sh.u32[kSegCount + v];
+        nsel += cnt[v];
+    }
+    if (nsel >= k && nsel <= static_cast<uint32_t>(kBlock)) {
+        seg_rank_top(sh.stage, cnt, nsel, k, sh.top);
+        nt = k;
+        return true;
+    }
     if (nsel >= k) {
+        seg_gather(sh.stage, cnt, nsel);
+        {
+            // Cut to the entries whose value key reaches a lower bound on the
+            // k-th largest one (two radix digits), so the sort sees fewer.
+            constexpr int kPerS = kStage / kBlock;
+            uint64_t e[kPerS];
+#pragma unroll
+            for (int q = 0; q < kPerS; ++q) {
+                const uint32_t i = static_cast<uint32_t>(q * kBlock + tid);
+                e[q] = i < nsel ? sh.stage[i] : 0ull;
+            }
+            uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+            for (int q = 0; q < kPerS; ++q)
+                if (e[q] != 0ull) {
+                    kmin = min(kmin, composite_key(e[q]));
+                    kmax = max(kmax, composite_key(e[q]));
+                }
+            kmin = wave_min(kmin);
+            kmax = wave_max(kmax);
+            if (lane == 0) {
+                sh.u32[8 + (tid >> 6)] = kmax;
+                sh.u32[12 + (tid >> 6)] = kmin;
+            }
+            __syncthreads();
+            const uint32_t bmax = max(max(sh.u32[8], sh.u32[9]), max(sh.u32[10], sh.u32[11]));
+            const uint32_t bmin = min(min(sh.u32[12], sh.u32[13]), min(sh.u32[14], sh.u32[15]));
+            const uint32_t kk = block_kth(bmin, bmax, k,
+                                          [&](auto&& f) {
+#pragma unroll
+                                              for (int q = 0; q < kPerS; ++q)
+                                                  if (e[q] != 0ull) f(composite_key(e[q]));
+                                          },
+                                          sh);
+            uint32_t cnt2 = 0;
+#pragma unroll
+            for (int q = 0; q < kPerS; ++q) cnt2 += (e[q] != 0ull && composite_key(e[q]) >= kk) ? 1u : 0u;
+            uint32_t pos = block_excl_scan(cnt2, nsel, sh);
+#pragma unroll
+            for (int q = 0; q < kPerS; ++q)
+                if (e[q] != 0ull && composite_key(e[q]) >= kk) sh.stage[pos++] = e[q];
+            __syncthreads();
+        }
         nt = select_top(sh.stage, nsel, k, sh.top);
         return true;
     }
@@ -1296,7 +1385,8 @@ __device__ __forceinline__ int next_rescan(const SelShared& sh, int c, int cpr, 
 // Merge, second part: softmax / min-p / top-p / draw over sh.top[0, keff).
 template <typename T>
 __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, const RowCtx& rc,
-                                             const ge_sample_params& p, bool greedy, uint32_t keff) {
+                                             const ge_sample_params& p, bool greedy, uint32_t keff,
+                                             float u, float x0) {
     const int tid = threadIdx.x;
     const int lane = __lane_id();
     const int wave = tid >> 6;
@@ -1307,91 +1397,121 @@ __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, co
     }
     if (greedy) {
         if (tid == 0) {
+            // std::max_element (generation.cpp:66-70) keeps index 0 when its
+            // value is NaN (NaN < x is false). Token 0's final value is NaN
+            // iff its raw value is, unless the penalty itself is NaN and 0
+            // is in the history.
             int32_t token = static_cast<int32_t>(composite_index(sh.top[0]));
-            const T* rowp = static_cast<const T*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
-            if (final0_is_nan(rowp, rc.cap, rc.pen, rc.r, rc.hist, rc.H)) token = 0;
+            bool nan0 = __builtin_isnan(softcap(x0, rc.cap));
+            if (!nan0 && rc.pen && __builtin_isnan(rc.r))
+                for (int j = 0; j < rc.H && !nan0; ++j) nan0 = rc.hist[j] == 0;
+            if (nan0) token = 0;
             write_row(a, row, token, 1.0f, 0);
         }
         return;
     }
 
     // generation.cpp:89-101 — p_i = expf((v_i - max) * (1/T)); double denominator.
-    float* prob = reinterpret_cast<float*>(sh.stage);
     const float maximum = key_value(composite_key(sh.top[0]));
     const float inv_temp = 1.0f / p.temperature;
-    double lsum = 0.0;
-    int lmin = INT_MAX;
-    int bad = 0;
-    for (uint32_t i = tid; i < keff; i += kBlock) {
-        const float v = key_value(composite_key(sh.top[i]));
-        const float e = expf_glibc((v - maximum) * inv_temp);
-        prob[i] = e;
-        lsum += static_cast<double>(e);
-        if (!(e >= 0.0f) || __builtin_isinf(e)) bad = 1;
-        else if (e > 0.0f) lmin = min(lmin, lsb_exponent(e));
-    }
-    lsum = wave_sum(lsum);
-    lmin = wave_min_i(lmin);
-    bad = __any(bad);
-    if (lane == 0) {
-        sh.f64[wave] = lsum;
-        sh.i32[wave] = bad ? INT_MIN : lmin;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        double s = 0.0;
-        int mn = INT_MAX;
-        bool b = false;
-        for (int wv = 0; wv < kBlock / 64; ++wv) {
-            s += sh.f64[wv];
-            if (sh.i32[wv] == INT_MIN) b = true;
-            else mn = min(mn, sh.i32[wv]);
-        }
-        // Certified exact: every term is a multiple of 2^mn and every partial
-        // sum is below 2^(E+2), so 53 bits hold each partial sum exactly when
-        // mn >= E - 51; then any summation order equals the reference's
-        // sequential one. Otherwise replay it sequentially.
+    auto expf_lds = [&](float x) { return expf_glibc_tab(x, [&](uint32_t i) { return sh.exp_tab[i]; }); };
+    const bool one_wave = keff <= 64u;
+    float* prob = reinterpret_cast<float*>(sh.stage);
+    float pr_reg = 0.0f;  // one-wave path: this lane's probability
+    bool any_nan;
+    if (one_wave) {
+        // One wave, probabilities in registers, no barriers.
+        if (wave != 0) return;
+        const bool live = lane < static_cast<int>(keff);
+        const uint64_t c = live ? sh.top[lane] : 0ull;
+        const float e = live ? expf_lds((key_value(composite_key(c)) - maximum) * inv_temp) : 0.0f;
+        const bool bad = live && (!(e >= 0.0f) || __builtin_isinf(e));
+        const int lsb = (live && e > 0.0f && !bad) ? lsb_exponent(e) : INT_MAX;
+        const double s = wave_sum(static_cast<double>(e));
+        const int mn = wave_min_i(lsb);
+        const int ex = static_cast<int>((d2u(s) >> 52) & 0x7ffu) - 1023;
         double den;
-        int ex = 0;
-        if (!b && s > 0.0 && !__builtin_isinf(s)) ex = static_cast<int>((d2u(s) >> 52) & 0x7ffu) - 1023;
-        if (!b && s > 0.0 && !__builtin_isinf(s) && mn >= ex - 51) {
+        // Certified exact (see below): any order equals the sequential sum.
+        if (!__any(bad) && s > 0.0 && !__builtin_isinf(s) && mn >= ex - 51) {
             den = s;
         } else {
             den = 0.0;
-            for (uint32_t i = 0; i < keff; ++i) den += static_cast<double>(prob[i]);
+            for (uint32_t i = 0; i < keff; ++i) den += static_cast<double>(readlane_f(e, static_cast<int>(i)));
         }
-        sh.f64[0] = den;
-    }
-    __syncthreads();
-    const float inv_denom = static_cast<float>(1.0 / sh.f64[0]);
-    int nan_p = 0;
-    for (uint32_t i = tid; i < keff; i += kBlock) {
-        const float pr = prob[i] * inv_denom;
-        prob[i] = pr;
-        if (__builtin_isnan(pr)) nan_p = 1;
-    }
-    nan_p = __any(nan_p);
-    if (lane == 0) sh.i32[wave] = nan_p;
-    __syncthreads();
-    const bool any_nan = (sh.i32[0] | sh.i32[1] | sh.i32[2] | sh.i32[3]) != 0;
-    if (wave == 0) {
-        const float u = a.uniforms[row];
-        uint32_t pos;
-        bool near;
-        if (!any_nan) {
-            scan_and_walk_fast(prob, keff, p, u, pos, near);
-        } else {
-            scan_and_walk(
-                [&](uint32_t g) {
-                    const uint32_t i = g * 64 + static_cast<uint32_t>(lane);
-                    return i < keff ? prob[i] : 0.0f;
-                },
-                keff, p, u, pos, near);
+        const float inv_denom = static_cast<float>(1.0 / den);
+        pr_reg = e * inv_denom;
+        any_nan = __any(live && __builtin_isnan(pr_reg));
+    } else {
+        double lsum = 0.0;
+        int lmin = INT_MAX;
+        int bad = 0;
+        for (uint32_t i = tid; i < keff; i += kBlock) {
+            const float v = key_value(composite_key(sh.top[i]));
+            const float e = expf_lds((v - maximum) * inv_temp);
+            prob[i] = e;
+            lsum += static_cast<double>(e);
+            if (!(e >= 0.0f) || __builtin_isinf(e)) bad = 1;
+            else if (e > 0.0f) lmin = min(lmin, lsb_exponent(e));
         }
-        if (lane == 0)
-            write_row(a, row, static_cast<int32_t>(composite_index(sh.top[pos])), prob[pos],
-                      near ? GE_FLAG_NEAR_BOUNDARY : 0);
+        lsum = wave_sum(lsum);
+        lmin = wave_min_i(lmin);
+        bad = __any(bad);
+        if (lane == 0) {
+            sh.f64[wave] = lsum;
+            sh.i32[wave] = bad ? INT_MIN : lmin;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            double s = 0.0;
+            int mn = INT_MAX;
+            bool b = false;
+            for (int wv = 0; wv < kBlock / 64; ++wv) {
+                s += sh.f64[wv];
+                if (sh.i32[wv] == INT_MIN) b = true;
+                else mn = min(mn, sh.i32[wv]);
+            }
+            // Certified exact: every term is a multiple of 2^mn and every
+            // partial sum is below 2^(E+2), so 53 bits hold each partial sum
+            // exactly when mn >= E - 51; then any summation order equals the
+            // reference's sequential one. Otherwise replay it sequentially.
+            double den;
+            int ex = 0;
+            if (!b && s > 0.0 && !__builtin_isinf(s)) ex = static_cast<int>((d2u(s) >> 52) & 0x7ffu) - 1023;
+            if (!b && s > 0.0 && !__builtin_isinf(s) && mn >= ex - 51) {
+                den = s;
+            } else {
+                den = 0.0;
+                for (uint32_t i = 0; i < keff; ++i) den += static_cast<double>(prob[i]);
+            }
+            sh.f64[0] = den;
+        }
+        __syncthreads();
+        const float inv_denom = static_cast<float>(1.0 / sh.f64[0]);
+        int nan_p = 0;
+        for (uint32_t i = tid; i < keff; i += kBlock) {
+            const float pr = prob[i] * inv_denom;
+            prob[i] = pr;
+            if (__builtin_isnan(pr)) nan_p = 1;
+        }
+        nan_p = __any(nan_p);
+        if (lane == 0) sh.i32[wave] = nan_p;
+        __syncthreads();
+        any_nan = (sh.i32[0] | sh.i32[1] | sh.i32[2] | sh.i32[3]) != 0;
+        if (wave != 0) return;
     }
+    // Wave 0: generation.cpp:103-126.
+    auto seg_prob = [&](uint32_t g) {
+        if (one_wave) return g == 0 ? pr_reg : 0.0f;
+        const uint32_t i = g * 64 + static_cast<uint32_t>(lane);
+        return i < keff ? prob[i] : 0.0f;
+    };
+    uint32_t pos;
+    bool near;
+    if (!any_nan) scan_and_walk_fast(seg_prob, keff, p, u, pos, near);
+    else scan_and_walk(seg_prob, keff, p, u, pos, near);
+    const float ppos = one_wave ? readlane_f(pr_reg, static_cast<int>(pos)) : prob[pos];
+    if (lane == 0)
+        write_row(a, row, static_cast<int32_t>(composite_index(sh.top[pos])), ppos, near ? GE_FLAG_NEAR_BOUNDARY : 0);
 }
 
 // A rescan of chunk c with m = k for the merge's fallback.
@@ -1461,6 +1581,10 @@ __global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
     __syncthreads();
     if (sh.u32[0] == 0u) return;
 
+    // Row inputs of the merge's last steps, loaded now so their latency
+    // overlaps the collection.
+    const float u = greedy ? 0.0f : a.uniforms[row];
+    const float x0 = greedy ? load_one(static_cast<const T*>(rc.rowp), 0) : 0.0f;
     uint32_t nt;
     if (!merge_collect(a, sh, row, k, m, nt)) {
         // Fallback: chunks whose guarantee is above the k-th largest listed
@@ -1475,7 +1599,7 @@ __global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
             nt = absorb_list(sh, nt, nl, k);
         }
     }
-    merge_finish<T>(a, sh, rc, p, greedy, min(nt, k));
+    merge_finish<T>(a, sh, rc, p, greedy, min(nt, k), u, x0);
 }
 
 template <typename T, int EPT>

@@ -97,6 +97,21 @@ __device__ __forceinline__ double sum_f64(double v) {
     return readlane_f64(v, 63);
 }
 
+// Inclusive prefix sum (lane i: v_0 + ... + v_i) in the scan's association
+// order; callers use it only where every order gives the same sums.
+__device__ __forceinline__ double incl_f64(double v) {
+    auto sh = [](double x, auto ctl) -> double {
+        return __builtin_bit_cast(double, ctl(__builtin_bit_cast(uint64_t, x)));
+    };
+    v += sh(v, [](uint64_t x) { return dpp64<kRowShr1, 0xf>(x, 0); });
+    v += sh(v, [](uint64_t x) { return dpp64<kRowShr2, 0xf>(x, 0); });
+    v += sh(v, [](uint64_t x) { return dpp64<kRowShr4, 0xf>(x, 0); });
+    v += sh(v, [](uint64_t x) { return dpp64<kRowShr8, 0xf>(x, 0); });
+    v += sh(v, [](uint64_t x) { return dpp64<kRowBcast15, 0xa>(x, 0); });
+    v += sh(v, [](uint64_t x) { return dpp64<kRowBcast31, 0xc>(x, 0); });
+    return v;
+}
+
 // The t-th largest (1 <= t <= 64) of the 64 lanes' keys, wave-uniform:
 // the largest x with at least t lanes holding a key >= x, found bit by bit
 // with ballots (one compare per bit; the count is a scalar popcount).
