@@ -1110,9 +1110,10 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, uint32_t keff, 
             }
         }
     }
-    // top-p: first j >= 1, j < limit, with cum_j >= top_p. Steps run in
-    // sub-blocks of 16; the scan leaves the segment after the sub-block that
-    // holds the stop.
+    // top-p: first j >= 1, j < limit, with cum_j >= top_p. The chain runs in
+    // sub-blocks of 16 plain adds; cum is non-decreasing, so the stop lies in
+    // the first sub-block that ends at or above top_p, which is then replayed
+    // step by step from its starting value (same adds, same bits).
     float cum = 0.0f;
     float mass = 0.0f;
     uint32_t keep = limit;
@@ -1120,24 +1121,27 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, uint32_t keff, 
     for (uint32_t g = 0; g * 64 < limit && !stopped; ++g) {
         const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
         const float pl = idx < limit ? seg_prob(g) : 0.0f;
-        float cl = 0.0f;
         for (int q = 0; q < 64 && !stopped; q += 16) {
-            static_for<0, 16>([&](auto J) {
-                cum = cum + readlane_f(pl, q + J);
-                cl = lane == q + J ? cum : cl;
-            });
-            const uint64_t th = __ballot(lane < q + 16 && idx >= 1 && idx < limit && cl >= p.top_p);
-            if (th) {
-                const int jt = __ffsll(static_cast<unsigned long long>(th)) - 1;
-                keep = g * 64 + static_cast<uint32_t>(jt) + 1;
-                mass = readlane_f(cl, jt);
-                stopped = true;
+            const float before = cum;
+            static_for<0, 16>([&](auto J) { cum = cum + readlane_f(pl, q + J); });
+            if (cum >= p.top_p) {
+                float c = before;
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t j = g * 64 + static_cast<uint32_t>(q + i);
+                    c = c + readlane_f(pl, q + i);
+                    if (j >= 1 && j < limit && c >= p.top_p) {
+                        keep = j + 1;
+                        mass = c;
+                        stopped = true;
+                        break;
+                    }
+                }
             }
         }
     }
     if (!stopped) mass = cum;  // min-p cut or all keff kept
-    // Draw: uniform_real_distribution(0, mass), then the subtract walk with
-    // the double CDF boundaries around the pick.
+    // Draw: uniform_real_distribution(0, mass), then the subtract walk
+    // (choice is non-increasing: the same sub-block search).
     const float choice0 = u * mass + 0.0f;
     float choice = choice0;
     uint32_t pos = keep - 1;  // fallthrough return, generation.cpp:126
@@ -1145,16 +1149,20 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, uint32_t keff, 
     for (uint32_t g = 0; g * 64 < keep && !found; ++g) {
         const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
         const float pl = idx < keep ? seg_prob(g) : 0.0f;
-        float chl = 0.0f;
         for (int q = 0; q < 64 && !found; q += 16) {
-            static_for<0, 16>([&](auto J) {
-                choice = choice - readlane_f(pl, q + J);
-                chl = lane == q + J ? choice : chl;
-            });
-            const uint64_t hit = __ballot(lane < q + 16 && idx < keep && chl <= 0.0f);
-            if (hit) {
-                pos = g * 64 + static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(hit)) - 1);
-                found = true;
+            const float before = choice;
+            static_for<0, 16>([&](auto J) { choice = choice - readlane_f(pl, q + J); });
+            if (choice <= 0.0f) {
+                float c = before;
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t j = g * 64 + static_cast<uint32_t>(q + i);
+                    c = c - readlane_f(pl, q + i);
+                    if (j < keep && c <= 0.0f) {
+                        pos = j;
+                        found = true;
+                        break;
+                    }
+                }
             }
         }
     }
