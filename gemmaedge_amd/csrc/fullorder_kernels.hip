@@ -34,6 +34,7 @@
 // lowest-index tie rule used everywhere in this library.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 
 #include "chain_math.h"
@@ -570,6 +571,228 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
     }
 }
 
+// ---- kernel 1, f32 rows: every token's final key, sorted --------------------
+//
+// An f32 row can hold V distinct values, so its items come from a sort of
+// the final keys of all its tokens (softcap, then the penalty on marked ids),
+// complemented so that ascending order is the reference's descending one.
+// One 1024-thread workgroup per row runs a stable LSD radix sort, 8 bits per
+// pass, ping-ponging between two per-row buffers in global memory (the decide
+// kernel's aux and pre arrays, unused until then). Each wave owns a fixed
+// portion of the positions and scatters it in order through per-(portion,
+// digit) cursors, so equal digits keep their order without synchronisation
+// inside a pass; the ranks among the 64 lanes of one step come from ballots
+// over the digit's bits. The counts of the next pass are taken while this
+// one scatters. Runs of equal keys then become the items (value, count).
+
+constexpr int kDigits = 256;
+constexpr int kSortUnroll = 4;  // 64-token steps in flight per wave
+
+struct SortShared {
+    uint32_t cnt[2][kWaves][kDigits];  // per (portion, digit): counts, then cursors
+    uint32_t excl[kDigits];
+    uint32_t scan[kWaves];
+};
+
+// Buffer reads of the sort read from L2 (agent-scope loads skip the CU's L1),
+// so a line the L1 kept from an earlier pass is never used after another wave
+// of the workgroup rewrote it; the writers wait for their stores before each
+// barrier.
+__device__ __forceinline__ uint32_t ld_l2(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stores_done_barrier() {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+}
+
+// Lanes among `act` whose 8-bit digit equals this lane's.
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t act) {
+    uint64_t m = act;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const bool bit = ((d >> b) & 1u) != 0u;
+        const uint64_t bb = __ballot(bit);
+        m &= bit ? bb : ~bb;
+    }
+    return m;
+}
+
+__global__ __launch_bounds__(kThreads) void fo_sort_f32_kernel(DevArgs a) {
+    __shared__ SortShared sh;
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const int wave = tid >> 6;
+    const int row = blockIdx.x;
+    const int V = a.vocab;
+    const ge_sample_params p = params_of(a, row);
+    uint32_t k;
+    if (!full_order_row(p, V, k)) return;
+
+    const float* rowp = static_cast<const float*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
+    const int32_t* hist;
+    int H;
+    history_of(a, row, hist, H);
+    const float r = p.repetition_penalty;
+    const float cap = p.softcap;
+    const bool pen = H > 0 && !(r == 1.0f);
+    uint32_t* bitmap = a.fo_bitmap + static_cast<int64_t>(row) * a.fo_bitmap_words;
+    uint64_t* items = a.fo_items + static_cast<int64_t>(row) * a.fo_items_stride;
+    uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * 4;
+    uint32_t* buf0 = reinterpret_cast<uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
+    uint32_t* buf1 = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
+
+    // 1. Unique in-range history ids; the decide kernel clears the bits.
+    if (pen) {
+        for (int i = tid; i < H; i += kThreads) {
+            const int32_t id = hist[i];
+            if (id >= 0 && id < V) atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+        }
+    }
+    for (int i = tid; i < 2 * kWaves * kDigits; i += kThreads) (&sh.cnt[0][0][0])[i] = 0u;
+    stores_done_barrier();
+
+    // Wave w owns positions [w P, (w + 1) P), P a power of two.
+    int lgP = 6;
+    while ((static_cast<int64_t>(kWaves) << lgP) < V) ++lgP;
+    const int wlo = min(wave << lgP, V);
+    const int whi = min(wlo + (1 << lgP), V);
+    const uint64_t below = (1ull << lane) - 1ull;
+
+    // 2. Final keys (generation.cpp:431-437 softcap, then the penalty) and
+    //    the counts of the first digit.
+    {
+        uint32_t* c0 = sh.cnt[0][wave];
+        for (int base = wlo; base < whi; base += 64 * kSortUnroll) {
+            float x[kSortUnroll];
+            uint32_t bw[kSortUnroll];
+#pragma unroll
+            for (int u = 0; u < kSortUnroll; ++u) {
+                const int i = base + 64 * u + lane;
+                x[u] = i < whi ? rowp[i] : 0.0f;
+                bw[u] = (pen && i < whi) ? ld_l2(bitmap + (i >> 5)) : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < kSortUnroll; ++u) {
+                const int i = base + 64 * u + lane;
+                if (i < whi) {
+                    float f = softcap(x[u], cap);
+                    if ((bw[u] >> (i & 31)) & 1u) f = penalize(f, r);
+                    const uint32_t s = ~order_key(f);
+                    buf0[i] = s;
+                    atomicAdd(&c0[s & 255u], 1u);
+                }
+            }
+        }
+    }
+
+    // 3. Four stable passes, least significant digit first.
+    uint32_t* src = buf0;
+    uint32_t* dst = buf1;
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 8 * pass;
+        uint32_t (*C)[kDigits] = sh.cnt[pass & 1];
+        uint32_t (*N)[kDigits] = sh.cnt[(pass + 1) & 1];
+        stores_done_barrier();  // counts complete, the previous pass's stores done
+        if (tid < kDigits) {
+            uint32_t t = 0;
+            for (int w = 0; w < kWaves; ++w) t += C[w][tid];
+            const uint32_t incl = wave_incl_u32(t);
+            if (lane == 63) sh.scan[wave] = incl;
+            sh.excl[tid] = incl - t;
+        }
+        __syncthreads();
+        if (tid < kDigits) {
+            uint32_t run = sh.excl[tid];
+            for (int w = 0; w < wave; ++w) run += sh.scan[w];
+            for (int w = 0; w < kWaves; ++w) {
+                const uint32_t c = C[w][tid];
+                C[w][tid] = run;
+                run += c;
+            }
+        }
+        for (int i = tid; i < kWaves * kDigits; i += kThreads) (&N[0][0])[i] = 0u;
+        __syncthreads();
+        uint32_t* cur = C[wave];
+        for (int base = wlo; base < whi; base += 64 * kSortUnroll) {
+            uint32_t key[kSortUnroll];
+#pragma unroll
+            for (int u = 0; u < kSortUnroll; ++u) {
+                const int i = base + 64 * u + lane;
+                key[u] = i < whi ? ld_l2(src + i) : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < kSortUnroll; ++u) {
+                const bool act = base + 64 * u + lane < whi;
+                const uint64_t am = __ballot(act);
+                if (am == 0ull) break;
+                const uint32_t d = (key[u] >> shift) & 255u;
+                const uint64_t mm = match_digit(d, am);
+                if (act) {
+                    // Lanes of one digit read the same cursor, then all
+                    // write the same advanced value (in program order, so
+                    // the next step reads it).
+                    const uint32_t c = cur[d];
+                    const uint32_t dest = c + static_cast<uint32_t>(__popcll(mm & below));
+                    dst[dest] = key[u];
+                    cur[d] = c + static_cast<uint32_t>(__popcll(mm));
+                    if (pass < 3) atomicAdd(&N[dest >> lgP][(key[u] >> (shift + 8)) & 255u], 1u);
+                }
+            }
+        }
+        uint32_t* t = src;
+        src = dst;
+        dst = t;
+    }
+    stores_done_barrier();
+
+    // 4. Items: runs of equal keys in the sorted order (src); their starts
+    //    go to the other buffer.
+    const uint32_t* s = src;
+    uint32_t* istart = dst;
+    uint32_t nb = 0;
+    for (int base = wlo; base < whi; base += 64) {
+        const int i = base + lane;
+        const bool act = i < whi;
+        const uint32_t cv = act ? ld_l2(s + i) : 0u;
+        const uint32_t pv = (act && i > 0) ? ld_l2(s + i - 1) : ~cv;
+        nb += static_cast<uint32_t>(__popcll(__ballot(act && cv != pv)));
+    }
+    if (lane == 0) sh.scan[wave] = nb;
+    __syncthreads();
+    uint32_t j = 0, G = 0;
+    for (int w = 0; w < kWaves; ++w) {
+        const uint32_t x = sh.scan[w];
+        if (w < wave) j += x;
+        G += x;
+    }
+    for (int base = wlo; base < whi; base += 64) {
+        const int i = base + lane;
+        const bool act = i < whi;
+        const uint32_t cv = act ? ld_l2(s + i) : 0u;
+        const uint32_t pv = (act && i > 0) ? ld_l2(s + i - 1) : ~cv;
+        const bool bnd = act && cv != pv;
+        const uint64_t m = __ballot(bnd);
+        if (bnd) istart[j + static_cast<uint32_t>(__popcll(m & below))] = static_cast<uint32_t>(i);
+        j += static_cast<uint32_t>(__popcll(m));
+    }
+    if (tid == 0) istart[G] = static_cast<uint32_t>(V);
+    stores_done_barrier();
+    for (uint32_t q = tid; q < G; q += kThreads) {
+        const uint32_t st = ld_l2(istart + q);
+        const uint32_t key = ~ld_l2(s + st);
+        const uint32_t val = key == kKeyNaN ? 0x7fc00000u : f2u(key_value(key));
+        items[q] = (static_cast<uint64_t>(val) << 32) | (ld_l2(istart + q + 1) - st);
+    }
+    if (tid == 0) {
+        const bool last_nan = ~ld_l2(s + V - 1) == kKeyNaN;
+        meta[kMetaItems] = G;
+        meta[kMetaExtras] = 0;
+        meta[kMetaNan] = last_nan ? static_cast<uint32_t>(V) - ld_l2(istart + G - 1) : 0u;
+        meta[kMetaStatus] = kStatusOk;
+    }
+}
+
 // ---- kernel 2: probabilities, exact chains, token ----------------------------
 
 struct ChainPos {
@@ -857,7 +1080,7 @@ struct DecideShared {
     uint32_t scan[kDWaves];
     double den;
     uint32_t pos, group_rank, group_total, forward, gx_count;
-    uint32_t blo, bhi, nan_group, near;
+    uint32_t blo, bhi, nan_group, near, gkey;
     int32_t token;
     int item;
 };
@@ -905,7 +1128,9 @@ __device__ uint32_t wave_partition_point(uint32_t lo, uint32_t hi, Pred pred) {
     return lo;
 }
 
+template <typename T>
 __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
+    constexpr bool kF32 = sizeof(T) == 4;
     __shared__ DecideShared sh;
     const int tid = threadIdx.x;
     const int lane = __lane_id();
@@ -1152,12 +1377,19 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         const uint32_t first = iv.start(is);
         const uint32_t total = iv.start(ie + 1) - first;
         const uint32_t rank = pos - first;
-        // bins [blo, bhi] whose final value has this key (empty when blo > bhi)
+        // Raw keys [blo, bhi] (bf16 bins, or f32 order keys) whose
+        // unpenalised final value has this key (empty when blo > bhi).
         uint32_t blo = 1, bhi = 0;
         const bool nan_group = key == kKeyNaN;
         if (!nan_group) {
-            blo = wave_partition_point(kLowBin, kHighBin + 1, [&](uint32_t b) { return bin_key(b, cap) < key; });
-            bhi = wave_partition_point(blo, kHighBin + 1, [&](uint32_t b) { return bin_key(b, cap) <= key; }) - 1;
+            if constexpr (kF32) {
+                auto fk = [&](uint32_t b) { return order_key(softcap(key_value(b), cap)); };
+                blo = wave_partition_point(kKeyNegInf, kKeyPosInf + 1, [&](uint32_t b) { return fk(b) < key; });
+                bhi = wave_partition_point(blo, kKeyPosInf + 1, [&](uint32_t b) { return fk(b) <= key; }) - 1;
+            } else {
+                blo = wave_partition_point(kLowBin, kHighBin + 1, [&](uint32_t b) { return bin_key(b, cap) < key; });
+                bhi = wave_partition_point(blo, kHighBin + 1, [&](uint32_t b) { return bin_key(b, cap) <= key; }) - 1;
+            }
         }
         // penalised tokens with this key: a run of the sorted extras
         uint32_t xs = 0, xe = 0;
@@ -1174,6 +1406,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             sh.blo = blo;
             sh.bhi = bhi;
             sh.nan_group = nan_group ? 1u : 0u;
+            sh.gkey = key;
             sh.gx_count = xe - xs;
             sh.forward = (rank <= (total - 1) / 2) ? 1u : 0u;
             sh.token = -1;
@@ -1191,22 +1424,26 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     // Locate the token: the rank-th lowest index of the group (or the
     // (total-1-rank)-th highest), in batches of 8192 tokens from that end;
     // each thread covers 16 consecutive tokens of a batch, and the next
-    // batch's loads are in flight while this one is scanned.
+    // batch's loads are in flight while this one is scanned. A token is in
+    // the group when its raw key is in [blo, bhi] and it is not penalised;
+    // penalised tokens of the group are the extras run (bf16) or are
+    // evaluated where the bitmap marks them (f32).
     {
         constexpr int kPer = 16;
         constexpr int kBatch = kDThreads * kPer;
+        constexpr int kW = kPer * static_cast<int>(sizeof(T)) / 4;  // 32-bit words per 16 tokens
+        constexpr int kPerVec = 16 / static_cast<int>(sizeof(T));   // tokens per 16-byte load
         const bool fwd = sh.forward != 0;
         uint32_t want = fwd ? sh.group_rank : sh.group_total - 1 - sh.group_rank;
         const uint32_t blo = sh.blo, bhi = sh.bhi;
         const bool nan_group = sh.nan_group != 0;
+        const uint32_t gkey = sh.gkey;
         const uint32_t gx = sh.gx_count;
-        const uint16_t* rowp = static_cast<const uint16_t*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
+        const T* rowp = static_cast<const T*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
         const bool vec = a.vec_ok != 0;
-        auto bin_match = [&](uint32_t bits16) {
-            const uint32_t bin = bin_of(bits16);
-            return nan_group ? bin_is_nan(bin) : (bin >= blo && bin <= bhi);
-        };
-        // penalised ids of the group in [lo, hi)
+        const float cap = p.softcap;
+        const float rpen = p.repetition_penalty;
+        // penalised ids of the group in [lo, hi) (bf16 extras)
         auto gx_in = [&](uint32_t lo, uint32_t hi) -> uint32_t {
             if (gx == 0) return 0;
             uint32_t a0 = 0, a1 = gx;
@@ -1215,26 +1452,62 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             while (b0 < b1) { const uint32_t m = (b0 + b1) >> 1; if (sh.gx_ids[m] < hi) b0 = m + 1; else b1 = m; }
             return b0 - a0;
         };
-        auto load16 = [&](int lo, uint32_t* w8, uint32_t& valid) {
+        auto load16 = [&](int lo, uint32_t* w, uint32_t& valid) {
             valid = 0;
             if (vec && lo + kPer <= V) {
-                const uint4 q1 = *reinterpret_cast<const uint4*>(rowp + lo);
-                const uint4 q2 = *reinterpret_cast<const uint4*>(rowp + lo + 8);
-                w8[0] = q1.x; w8[1] = q1.y; w8[2] = q1.z; w8[3] = q1.w;
-                w8[4] = q2.x; w8[5] = q2.y; w8[6] = q2.z; w8[7] = q2.w;
+#pragma unroll
+                for (int q = 0; q < kW / 4; ++q) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(rowp + lo + q * kPerVec);
+                    w[4 * q + 0] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+                }
                 valid = 0xFFFFu;
             } else {
-                for (int h = 0; h < 8; ++h) w8[h] = 0;
+                for (int h = 0; h < kW; ++h) w[h] = 0;
                 for (int h = 0; h < kPer; ++h) {
                     if (lo + h < V) {
-                        w8[h >> 1] |= static_cast<uint32_t>(rowp[lo + h]) << ((h & 1) * 16);
+                        if constexpr (kF32) w[h] = f2u(rowp[lo + h]);
+                        else w[h >> 1] |= static_cast<uint32_t>(rowp[lo + h]) << ((h & 1) * 16);
                         valid |= 1u << h;
                     }
                 }
             }
         };
+        // Group members among the 16 tokens at lo (bf16: not counting the
+        // penalised ones, which the extras run supplies).
+        auto match16 = [&](int lo, const uint32_t* w, uint32_t valid) -> uint32_t {
+            uint32_t mm = 0;
+            // 16 tokens at a multiple of 16 lie in one bitmap word
+            const uint32_t pw = (pen && valid) ? (bitmap[lo >> 5] >> (lo & 31)) & valid : 0u;
+            if constexpr (kF32) {
+#pragma unroll
+                for (int h = 0; h < kPer; ++h) {
+                    const float x = u2f(w[h]);
+                    const uint32_t rk = order_key(x);
+                    const bool m = nan_group ? (x != x) : (!((pw >> h) & 1u) && rk >= blo && rk <= bhi);
+                    if (((valid >> h) & 1u) && m) mm |= 1u << h;
+                }
+                if (!nan_group) {
+                    for (uint32_t b = pw; b; b &= b - 1u) {
+                        const int h = __builtin_ctz(b);
+                        const float f = penalize(softcap(rowp[lo + h], cap), rpen);
+                        if (order_key(f) == gkey) mm |= 1u << h;
+                    }
+                }
+            } else {
+                auto bin_match = [&](uint32_t bits16) {
+                    const uint32_t bin = bin_of(bits16);
+                    return nan_group ? bin_is_nan(bin) : (bin >= blo && bin <= bhi);
+                };
+#pragma unroll
+                for (int h = 0; h < kPer; ++h) {
+                    if (((valid >> h) & 1u) && bin_match((w[h >> 1] >> ((h & 1) * 16)) & 0xFFFFu)) mm |= 1u << h;
+                }
+                mm &= ~pw;
+            }
+            return mm;
+        };
         const int nb = (V + kBatch - 1) / kBatch;
-        uint32_t cur[8], nxt[8];
+        uint32_t cur[kW], nxt[kW];
         uint32_t cvalid = 0, nvalid = 0;
         {
             const int batch = fwd ? 0 : nb - 1;
@@ -1247,18 +1520,10 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                 const int nbatch = fwd ? bi + 1 : nb - 2 - bi;
                 load16(nbatch * kBatch + tid * kPer, nxt, nvalid);
             }
-            uint32_t mm = 0;  // matching non-penalised tokens
-            for (int h = 0; h < kPer; ++h) {
-                if (((cvalid >> h) & 1u) && bin_match((cur[h >> 1] >> ((h & 1) * 16)) & 0xFFFFu)) mm |= 1u << h;
-            }
-            if (mm && pen) {
-                // 16 tokens at a multiple of 16 lie in one bitmap word
-                const uint32_t word = bitmap[lo >> 5] >> (lo & 31);
-                mm &= ~word;
-            }
+            const uint32_t mm = match16(lo, cur, cvalid);
             const uint32_t hi = static_cast<uint32_t>(min(lo + kPer, V));
-            const uint32_t cnt = static_cast<uint32_t>(__popc(mm)) +
-                                 (lo < V ? gx_in(static_cast<uint32_t>(lo), hi) : 0u);
+            uint32_t cnt = static_cast<uint32_t>(__popc(mm));
+            if constexpr (!kF32) cnt += lo < V ? gx_in(static_cast<uint32_t>(lo), hi) : 0u;
             uint32_t tot;
             const uint32_t ex_fwd = dblock_excl_scan(cnt, sh.scan, tot);
             const uint32_t ex = fwd ? ex_fwd : tot - ex_fwd - cnt;
@@ -1271,7 +1536,9 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                         if (!((cvalid >> h) & 1u)) continue;
                         const uint32_t idx = static_cast<uint32_t>(lo + h);
                         uint32_t here = (mm >> h) & 1u;
-                        if (!here && gx) here = gx_in(idx, idx + 1);
+                        if constexpr (!kF32) {
+                            if (!here && gx) here = gx_in(idx, idx + 1);
+                        }
                         if (here) {
                             if (r2 == 0) found = static_cast<int>(idx);
                             else --r2;
@@ -1282,7 +1549,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                 break;
             }
             want -= tot;
-            for (int h = 0; h < 8; ++h) cur[h] = nxt[h];
+            for (int h = 0; h < kW; ++h) cur[h] = nxt[h];
             cvalid = nvalid;
         }
     }
@@ -1290,15 +1557,51 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     finish(sh.token, aux[sh.item], sh.near ? GE_FLAG_NEAR_BOUNDARY : 0);
 }
 
+// The per-row pointers of rows [r0, r0 + n) of a call, as a call of its own
+// that uses workspace rows [0, n).
+DevArgs slice_rows(const DevArgs& a, int r0, int n) {
+    DevArgs s = a;
+    const size_t esize = a.dtype == GE_DTYPE_BF16 ? 2 : 4;
+    s.logits = static_cast<const char*>(a.logits) + esize * static_cast<size_t>(a.row_stride) * static_cast<size_t>(r0);
+    s.rows = n;
+    if (a.row_params) s.row_params = a.row_params + r0;
+    if (a.history_offsets) s.history_offsets = a.history_offsets + r0;
+    if (a.ring) s.ring = a.ring + static_cast<int64_t>(r0) * a.ring_capacity;
+    if (a.ring_len) s.ring_len = a.ring_len + r0;
+    if (a.uniforms) s.uniforms = a.uniforms + r0;
+    s.tokens = a.tokens + r0;
+    if (a.probs) s.probs = a.probs + r0;
+    if (a.flags) s.flags = a.flags + r0;
+    return s;
+}
+
 }  // namespace
 
 hipError_t launch_full_order(const DevArgs& a, hipStream_t stream) {
     if (!a.fo_items) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(fo_hist_kernel, dim3(a.rows), dim3(kThreads), 0, stream, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(fo_decide_kernel, dim3(a.rows), dim3(kDThreads), 0, stream, a);
-    return hipGetLastError();
+    if (a.dtype == GE_DTYPE_BF16) {
+        hipLaunchKernelGGL(fo_hist_kernel, dim3(a.rows), dim3(kThreads), 0, stream, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(fo_decide_kernel<uint16_t>, dim3(a.rows), dim3(kDThreads), 0, stream, a);
+        return hipGetLastError();
+    }
+    // f32 rows need up to V items each: as many rows per launch pair as the
+    // workspace holds at that stride (at least one, by construction).
+    const int64_t stride = fo_items_stride_f32(a.vocab);
+    const int per = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.fo_capacity / stride, a.rows)));
+    if (a.fo_capacity < stride) return hipErrorInvalidValue;
+    for (int r0 = 0; r0 < a.rows; r0 += per) {
+        DevArgs s = slice_rows(a, r0, std::min(per, a.rows - r0));
+        s.fo_items_stride = stride;
+        hipLaunchKernelGGL(fo_sort_f32_kernel, dim3(s.rows), dim3(kThreads), 0, stream, s);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(fo_decide_kernel<float>, dim3(s.rows), dim3(kDThreads), 0, stream, s);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace ge

@@ -216,6 +216,7 @@ __host__ __device__ inline float penalize(float v, float r) { return v > 0.0f ? 
 constexpr uint32_t kKeyNone = 0u;
 constexpr uint32_t kKeyNaN = 1u;
 constexpr uint32_t kKeyNegInf = 0x007fffffu;
+constexpr uint32_t kKeyPosInf = 0xff800000u;
 
 __host__ __device__ inline uint32_t order_key(float f) {
     uint32_t b = f2u(f);

@@ -7,6 +7,7 @@
 // process-wide lock (src/cuda_backend.cu:513): a handle belongs to one stream.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdint>
@@ -32,6 +33,7 @@ struct ge_sampler {
     uint32_t* fo_bitmap;
     uint32_t* fo_meta;
     int64_t fo_items_stride;
+    int64_t fo_capacity;
     int32_t fo_extras_cap;
     int64_t fo_bitmap_words;
 };
@@ -131,7 +133,9 @@ int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, 
         s->fo_items_stride = ge::fo_items_stride(max_history);
         s->fo_extras_cap = max_history < ge::kFoExtrasCap ? (max_history > 0 ? max_history : 1) : ge::kFoExtrasCap;
         s->fo_bitmap_words = (static_cast<int64_t>(max_vocab) + 31) / 32;
-        const size_t items = rows * static_cast<size_t>(s->fo_items_stride);
+        const size_t items = std::max(rows * static_cast<size_t>(s->fo_items_stride),
+                                      static_cast<size_t>(ge::fo_items_stride_f32(max_vocab)));
+        s->fo_capacity = static_cast<int64_t>(items);
         const size_t words = rows * static_cast<size_t>(s->fo_bitmap_words);
         alloc(reinterpret_cast<void**>(&s->fo_items), items * sizeof(uint64_t));
         alloc(reinterpret_cast<void**>(&s->fo_aux), items * sizeof(float));
@@ -187,7 +191,7 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     if (maybe_sampling && !x.uniforms) return fail(GE_ERR_INVALID_ARG, "uniforms required when sampling");
 
     // Rows with k > kMaxTopK (top-k disabled or large) take the full-order
-    // kernels, which this build has for bf16 logits.
+    // kernels.
     bool run_select = true;
     bool run_full = false;
     if (!x.row_params) {
@@ -195,14 +199,11 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
         const uint32_t v = static_cast<uint32_t>(x.vocab);
         const uint32_t k = p.temperature <= 0.0f ? 1u : (p.top_k ? (p.top_k < v ? p.top_k : v) : v);
         if (k > static_cast<uint32_t>(ge::kMaxTopK)) {
-            if (x.dtype != GE_DTYPE_BF16)
-                return fail(GE_ERR_UNSUPPORTED, "effective top_k %u above %d needs bf16 logits in this build",
-                            k, ge::kMaxTopK);
             run_select = false;
             run_full = true;
         }
     } else {
-        run_full = x.dtype == GE_DTYPE_BF16 && x.vocab > ge::kMaxTopK;
+        run_full = x.vocab > ge::kMaxTopK;
     }
     if (run_full && !s->fo_items) return fail(GE_ERR_CAPACITY, "handle has no full-order workspace");
 
@@ -249,6 +250,7 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     a.fo_items_stride = s->fo_items_stride;
     a.fo_extras_cap = s->fo_extras_cap;
     a.fo_bitmap_words = s->fo_bitmap_words;
+    a.fo_capacity = s->fo_capacity;
 
     DeviceGuard guard(s->device);
     if (!guard.ok) return fail(GE_ERR_DEVICE, "hipSetDevice(%d) failed", s->device);

@@ -43,8 +43,10 @@ struct DevArgs {
     int32_t chunk_len;            // kBlock * ept
     int32_t vec_ok;               // rows are 16-byte aligned
 
-    // Full-order path workspace (bf16 rows whose k exceeds kMaxTopK); NULL when
-    // the handle's max_vocab cannot produce such rows.
+    // Full-order path workspace (rows whose k exceeds kMaxTopK); NULL when the
+    // handle's max_vocab cannot produce such rows. bf16 rows use
+    // fo_items_stride items each; f32 rows fo_items_stride_f32(vocab), in as
+    // many rows per launch as fo_capacity items hold.
     uint64_t* fo_items;           // [max_rows * fo_items_stride]  (value bits << 32) | count
     float* fo_aux;                // [max_rows * fo_items_stride]  per-item probability
     uint32_t* fo_pre;             // [max_rows * fo_items_stride]  elements before the item
@@ -54,6 +56,7 @@ struct DevArgs {
     int64_t fo_items_stride;
     int32_t fo_extras_cap;        // <= kFoExtrasCap
     int64_t fo_bitmap_words;
+    int64_t fo_capacity;          // items (and aux, pre entries) in the workspace
 };
 
 // Full-order path sizes.
@@ -66,12 +69,17 @@ inline int64_t fo_items_stride(int max_history) {
     return (kFoNonNanBins + extras + 2 + 63) / 64 * 64;  // items + NaN item + end boundary
 }
 
+// f32 rows: one item per distinct final value (up to V) and the end
+// boundary; the sort also uses the aux and pre arrays as two V-entry buffers.
+inline int64_t fo_items_stride_f32(int vocab) { return (static_cast<int64_t>(vocab) + 2 + 63) / 64 * 64; }
+
 // Launches the fused select/sample kernel for rows whose k <= kMaxTopK.
 // ept in {16, 64}. Returns a hipError_t.
 hipError_t launch_select(const DevArgs& a, hipStream_t stream, int ept);
 
-// Launches the two full-order kernels (bf16 rows with k > kMaxTopK; other
-// rows are skipped). Returns a hipError_t.
+// Launches the full-order kernels (rows with k > kMaxTopK; other rows are
+// skipped): one pair for bf16, one pair per slice of rows for f32. Returns a
+// hipError_t.
 hipError_t launch_full_order(const DevArgs& a, hipStream_t stream);
 
 }  // namespace ge

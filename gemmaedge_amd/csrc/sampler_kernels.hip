@@ -56,7 +56,6 @@ namespace {
 
 constexpr int kStage = 2048;    // LDS staging entries (candidates, union)
 constexpr int kLoadBatch = 8;   // independent global loads in flight per thread
-constexpr uint32_t kKeyPosInf = 0xff800000u;  // order_key(+inf)
 constexpr uint32_t kPenTag = 0x80000000u;     // staged entry: penalised token
 
 template <typename U>
@@ -1547,9 +1546,9 @@ __global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
                               : (p.top_k ? min(p.top_k, static_cast<uint32_t>(V))
                                          : static_cast<uint32_t>(V));  // generation.cpp:80
     if (k > static_cast<uint32_t>(kMaxTopK)) {
-        // bf16 rows belong to the full-order kernels, which the host launches
+        // The full-order kernels serve these rows; the host launches them
         // whenever the handle has their workspace.
-        if (a.dtype == GE_DTYPE_BF16 && a.fo_items) return;
+        if (a.fo_items) return;
         if (chunk == 0 && tid == 0) {
             a.tokens[row] = -1;
             if (a.probs) a.probs[row] = 0.0f;

@@ -215,15 +215,3 @@ def test_too_many_penalised_tokens_is_flagged(sampler):
     w2 = small_workload("after-many", x, dict(temperature=1.0, top_k=0, repetition_penalty=1.2),
                         history=hist[:100], offsets=np.array([0, 100], np.int32), dtype="bf16")
     _check(sampler, w2)
-
-
-def test_f32_full_order_is_reported_unsupported(sampler):
-    import torch
-
-    from gemmaedge_amd import SamplingConfig
-    from gemmaedge_amd.sampler import SamplerError
-
-    x = torch.zeros((1, 3000), dtype=torch.float32, device="cuda")
-    u = torch.full((1,), 0.5, dtype=torch.float32, device="cuda")
-    with pytest.raises(SamplerError):
-        sampler.sample(x, SamplingConfig(temperature=1.0, top_k=0), uniforms=u)

@@ -1,0 +1,240 @@
+"""GPU parity of the full-order path for f32 rows: top-k disabled or above the
+selection path's limit (src/generation.cpp:80, k = V when top_k is 0). Every
+token's final key is radix-sorted on the device, runs of equal keys become
+items, and the exact-chain kernel replays the reference's sequential sums.
+Checked against the CPU oracle (a full sort and the reference's sequential
+sums): tokens and probabilities bit-identical, near-boundary flags equal."""
+import numpy as np
+import pytest
+
+import ge_oracle as O
+from gemmaedge_amd import workloads as W
+from gpu_util import assert_parity, run_gpu, run_oracle, small_workload
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    import torch
+
+    from gemmaedge_amd import Sampler, available
+
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    assert available(), "no gfx950 device visible to the HIP library"
+    s = Sampler(max_rows=64, max_vocab=W.VOCAB, max_history=20000)
+    yield s
+    s.close()
+
+
+def _check(sampler, w, label=""):
+    print(f"[fullorder-f32] {label or w.name} rows={w.rows} V={w.vocab} {w.params}", flush=True)
+    gpu = run_gpu(sampler, w)
+    ora = run_oracle(w)
+    assert_parity(w, gpu, ora, label)
+    return gpu, ora
+
+
+def test_c4_shape_in_f32(sampler):
+    # C4's distribution and parameters with f32 logits: a nucleus of most of
+    # the row, every probability within a few binades (certified sums).
+    rng = np.random.default_rng(40)
+    x = (rng.standard_normal((8, W.VOCAB)) * 0.1).astype(np.float32)
+    w = small_workload("c4-f32", x, dict(temperature=1.3, top_k=0, top_p=0.9, softcap=30.0),
+                       uniforms=W.mt_uniforms(40, 8))
+    _, ora = _check(sampler, w)
+    assert np.all(ora.results["k"] == W.VOCAB)
+    assert np.all(ora.results["keep"] > 200000)
+
+
+def test_wide_range_rows_replay_the_double_denominator(sampler):
+    # N(0, 3): probabilities span many binades, so the double denominator is
+    # replayed item by item; u near 1 with top_p >= 1 walks deep into the tail.
+    rng = np.random.default_rng(41)
+    x = (rng.standard_normal((6, W.VOCAB)) * 3).astype(np.float32)
+    u = np.array([0.5, 0.999, 0.99999, 0.0, 0.25, float(np.float32(1 - 2**-24))], np.float32)
+    for top_p in (0.9, 1.0, 2.0):
+        w = small_workload(f"wide-p{top_p}", x, dict(temperature=1.0, top_k=0, top_p=top_p, softcap=30.0),
+                           uniforms=u)
+        _check(sampler, w)
+
+
+def test_special_values(sampler):
+    rng = np.random.default_rng(42)
+    V = 5003
+    base = (rng.standard_normal(V) * 0.5).astype(np.float32)
+    rows = []
+    r = base.copy(); r[::97] = np.nan; rows.append(r)                     # NaNs inside the top-k
+    r = base.copy(); r[5] = np.inf; r[9] = -np.inf; rows.append(r)         # +inf max
+    r = base.copy(); r[::3] = 0.0; r[1::3] = -0.0; rows.append(r)          # +-0 ties
+    r = np.zeros(V, np.float32); rows.append(r)                            # one value
+    r = np.full(V, np.nan, np.float32); rows.append(r)                     # all NaN
+    r = base.copy(); r[:] = -np.inf; r[100] = 1.0; rows.append(r)          # -inf tail
+    r = base.copy(); r[::5] = np.float32(1e-45); r[1::5] = -np.float32(1e-45); rows.append(r)  # denormals
+    # NaN payloads whose high 16 bits read as +-inf
+    r = base.copy(); r[7:12] = np.array([0x7f800001, 0xff800001, 0x7fc00000, 0xffffffff, 0x7f800000],
+                                        np.uint32).view(np.float32); rows.append(r)
+    x = np.stack(rows)
+    for T in (1.0, 0.3):
+        for cap in (0.0, 30.0):
+            for k in (0, 2000):
+                w = small_workload(f"special-T{T}-c{cap}-k{k}", x,
+                                   dict(temperature=T, top_k=k, top_p=0.9, softcap=cap),
+                                   uniforms=W.mt_uniforms(int(T * 10 + cap + k), x.shape[0]))
+                _check(sampler, w)
+
+
+def test_degenerate_temperatures(sampler):
+    rng = np.random.default_rng(43)
+    x = rng.standard_normal((3, 3000)).astype(np.float32)
+    for T in (1e-30, float("nan"), float("inf"), 1e30):
+        w = small_workload(f"T{T}", x, dict(temperature=T, top_k=0, top_p=0.9))
+        _check(sampler, w)
+
+
+def test_penalties(sampler):
+    rng = np.random.default_rng(44)
+    V = 8192
+    x = (rng.standard_normal((4, V)) * 2).astype(np.float32)
+    x[0, :50] = 0.0
+    x[1, 10] = np.nan
+    x[2, :] = np.round(x[2, :])  # heavy ties before and after the penalty
+    H = 3000
+    hist = rng.integers(-5, V + 5, size=4 * H).astype(np.int32)  # duplicates and out-of-range ids
+    hist[:50] = np.arange(50)  # row 0: the zeros are penalised
+    hist[H + 7] = 10           # row 1: a NaN token is penalised
+    offs = (np.arange(5) * H).astype(np.int32)
+    for r in (1.3, 0.7, 1.0):
+        for cap in (0.0, 30.0):
+            w = small_workload(f"pen-r{r}-c{cap}", x,
+                               dict(temperature=0.9, top_k=0, top_p=0.95, softcap=cap, repetition_penalty=r),
+                               history=hist, offsets=offs, uniforms=W.mt_uniforms(int(r * 100 + cap), 4))
+            _check(sampler, w)
+
+
+def test_many_penalised_tokens(sampler):
+    # More unique penalised ids than the bf16 path's extras list holds: f32
+    # rows have no such limit.
+    rng = np.random.default_rng(45)
+    V = 40000
+    x = rng.standard_normal((1, V)).astype(np.float32)
+    hist = rng.permutation(V)[:15000].astype(np.int32)
+    w = small_workload("many-penalised", x, dict(temperature=1.0, top_k=0, repetition_penalty=1.2, softcap=30.0),
+                       history=hist, offsets=np.array([0, hist.size], np.int32))
+    _check(sampler, w)
+    # the history bitmap is clear again: the next call with another history is exact
+    w2 = small_workload("after-many", x, dict(temperature=1.0, top_k=0, repetition_penalty=1.2),
+                        history=hist[:100], offsets=np.array([0, 100], np.int32))
+    _check(sampler, w2)
+
+
+def test_k_truncates_inside_a_tie_group(sampler):
+    rng = np.random.default_rng(46)
+    V = 4099  # not a multiple of 4: scalar tail
+    x = rng.integers(-4, 5, size=(5, V)).astype(np.float32)
+    for k in (1025, 1500, 3000, 4098, 4099, 10**6):
+        for min_p in (0.0, 0.3, 0.9, 1.5):
+            w = small_workload(f"k{k}-minp{min_p}", x,
+                               dict(temperature=0.8, top_k=k, top_p=0.9, min_p=min_p),
+                               uniforms=W.mt_uniforms(k % 1000 + int(min_p * 10), 5))
+            _check(sampler, w)
+
+
+def test_top_p_edges(sampler):
+    rng = np.random.default_rng(47)
+    x = (rng.standard_normal((4, 20000)) * 0.2).astype(np.float32)
+    for top_p in (0.0, 0.5, 0.999, 1.0, 2.0, float("nan"), -1.0):
+        w = small_workload(f"p{top_p}", x, dict(temperature=1.3, top_k=0, top_p=top_p, softcap=30.0))
+        _check(sampler, w)
+
+
+def test_unaligned_rows(sampler):
+    import torch
+
+    from gemmaedge_amd import SamplingConfig
+
+    rng = np.random.default_rng(48)
+    x = (rng.standard_normal((3, 5000)) * 0.3).astype(np.float32)
+    flat = torch.from_numpy(np.concatenate([[0], x.ravel()]).astype(np.float32)).cuda()
+    logits = flat[1:].view(3, 5000)  # 4-byte offset: no 16-byte loads
+    uni = W.mt_uniforms(49, 3)
+    cfg = SamplingConfig(temperature=1.0, top_k=0, top_p=0.9, softcap=30.0)
+    tokens, probs, _ = sampler.sample(logits, cfg, uniforms=torch.from_numpy(uni).cuda())
+    torch.cuda.synchronize()
+    ora = O.run(x, O.make_params(temperature=1.0, top_k=0, top_p=0.9, softcap=30.0), uniforms=uni)
+    assert np.array_equal(tokens.cpu().numpy(), ora.tokens)
+    assert np.array_equal(probs.cpu().numpy().view(np.uint32), ora.probs.view(np.uint32))
+
+
+def test_random_cases(sampler):
+    rng = np.random.default_rng(2025)
+    for case in range(60):
+        V = int(rng.choice([1025, 1500, 4096, 4099, 20000, 70001]))
+        rows = int(rng.integers(1, 4))
+        kind = rng.integers(0, 4)
+        if kind == 0:
+            x = rng.standard_normal((rows, V)) * rng.uniform(0.05, 4)
+        elif kind == 1:
+            x = rng.integers(-3, 4, size=(rows, V)).astype(np.float64)
+        elif kind == 2:
+            x = rng.standard_normal((rows, V)) * 200
+        else:
+            x = rng.choice(np.array([0.0, -0.0, 1e-30, 2.0, -1.0]), size=(rows, V))
+        params = dict(temperature=float(rng.choice([0.5, 1.0, 1.7])),
+                      top_k=int(rng.choice([0, 0, 1025, 3000])),
+                      top_p=float(rng.choice([0.0, 0.5, 0.9, 0.95, 1.0, 1.5])),
+                      min_p=float(rng.choice([0.0, 0.0, 0.05, 0.5])),
+                      softcap=float(rng.choice([0.0, 30.0, 5.0])),
+                      repetition_penalty=float(rng.choice([1.0, 1.1, 1.5, 0.8])))
+        H = int(rng.choice([0, 1, 7, 64, 300]))
+        hist = rng.integers(-2, V + 2, size=rows * H).astype(np.int32)
+        offsets = (np.arange(rows + 1) * H).astype(np.int32)
+        w = small_workload(f"fo32-rand{case}", x.astype(np.float32), params, hist, offsets,
+                           W.mt_uniforms(case, rows))
+        _check(sampler, w)
+
+
+def test_per_row_params_mix_paths(sampler):
+    import torch
+
+    from gemmaedge_amd import SamplingConfig
+
+    rng = np.random.default_rng(50)
+    rows, V = 6, 30000
+    x = (rng.standard_normal((rows, V)) * 1.5).astype(np.float32)
+    cfgs = [SamplingConfig(temperature=t, top_k=k, top_p=p, softcap=30.0, repetition_penalty=1.1)
+            for t, k, p in [(0.0, 0, 0.9), (1.0, 0, 0.95), (0.7, 40, 0.9), (1.0, 5000, 0.99),
+                            (1.2, 1024, 1.0), (0.5, 1025, 0.5)]]
+    hist = rng.integers(0, V, size=rows * 32).astype(np.int32)
+    offs = (np.arange(rows + 1) * 32).astype(np.int32)
+    uni = W.mt_uniforms(51, rows)
+    tokens, probs, flags = sampler.sample(
+        torch.from_numpy(x).cuda(), cfgs, uniforms=torch.from_numpy(uni).cuda(),
+        history=torch.from_numpy(hist).cuda(), history_offsets=torch.from_numpy(offs).cuda())
+    torch.cuda.synchronize()
+    params = [O.make_params(temperature=c.temperature, top_k=c.top_k, top_p=c.top_p,
+                            softcap=c.softcap, repetition_penalty=c.repetition_penalty) for c in cfgs]
+    ora = O.run(x, params, history=hist, offsets=offs, uniforms=uni)
+    assert np.array_equal(tokens.cpu().numpy(), ora.tokens)
+    assert np.array_equal(probs.cpu().numpy().view(np.uint32), ora.probs.view(np.uint32))
+    assert np.array_equal(flags.cpu().numpy() & 1, ora.flags)
+
+
+def test_rows_in_several_launches():
+    # A small workspace holds fewer f32 rows than the call has: the rows go
+    # through the kernels in slices, each with its own rows' inputs and outputs.
+    from gemmaedge_amd import Sampler
+
+    rng = np.random.default_rng(52)
+    for max_rows, V, rows in ((4, 70001, 4), (2, W.VOCAB, 2)):
+        s = Sampler(max_rows=max_rows, max_vocab=max(V, 70001), max_history=64)
+        try:
+            x = (rng.standard_normal((rows, V)) * 2).astype(np.float32)
+            hist = rng.integers(0, V, size=rows * 64).astype(np.int32)
+            offs = (np.arange(rows + 1) * 64).astype(np.int32)
+            w = small_workload(f"slices-{max_rows}x{V}", x,
+                               dict(temperature=1.0, top_k=0, top_p=0.95, softcap=30.0, repetition_penalty=1.3),
+                               history=hist, offsets=offs, uniforms=W.mt_uniforms(V + rows, rows))
+            _check(s, w)
+        finally:
+            s.close()
