@@ -4,8 +4,9 @@
 Headline (BASELINE.json metric): rows/s of the sampler at V=262144, batch 64
 (config C2: fp32 N(0,3) + peaks, softcap 30, T 0.7, top-k 40, top-p 0.9,
 penalty 1.15 over 2048-id histories), with the dominant kernel's achieved HBM
-bandwidth against the 8 TB/s peak; batch-1 latency (C1), C3, C4 and the C5
-decode sweep are reported as extra fields.
+bandwidth against the 8 TB/s peak; batch-1 latency (C1), C3, C4, C4's rows in
+f32 (the f32 full-order path) and the C5 decode sweep are reported as extra
+fields.
 
 A "step" is one ge_sample call over the whole batch with every input already
 resident in HBM. The K timed steps are one HIP-graph replay of K captured
@@ -49,8 +50,8 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--extras", default="C1,C3,C4,C5",
-                    help="comma list of extra configs to report (C1,C3,C4,C5) or ''")
+    ap.add_argument("--extras", default="C1,C3,C4,C4f32,C5",
+                    help="comma list of extra configs to report (C1,C3,C4,C4f32,C5) or ''")
     ap.add_argument("--c5-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -344,6 +345,9 @@ def main():
                 extras.update(bench_throughput(torch, sampler, W.c3(), "C3"))
             elif name == "C4":
                 extras.update(bench_throughput(torch, sampler, W.c4(), "C4"))
+            elif name == "C4f32":
+                # not a BASELINE config: C4's rows kept in f32 (the f32 full-order path)
+                extras.update(bench_throughput(torch, sampler, W.c4(f32=True), "C4_f32"))
             elif name == "C5":
                 extras["C5"] = c5_sweep(torch, sampler, W, args.c5_steps)
         except Exception as e:  # report, do not hide
@@ -373,7 +377,7 @@ def main():
                                "top-p 0.9, penalty 1.15, H=2048", "rows": w.rows, "vocab": w.vocab},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(),
-                     "kernel": "select_kernel<float,64,1>", "kernel_us_mean": launch_us,
+                     "kernel": "select_kernel<float,64>", "kernel_us_mean": launch_us,
                      "kernel_us_isolated_p50": float(np.median(d)), "bytes_per_launch": bytes_launch},
         "cpu_baseline": cpu,
         "parity": {"C2": par},

@@ -179,17 +179,19 @@ def c3(seed: int = 3, rows: int = 256, vocab: int = VOCAB) -> Workload:
     return Workload("C3", x, "f32", p, hist, offsets, mt_uniforms(seed, rows), seed)
 
 
-def c4(seed: int = 4, rows: int = 512, vocab: int = VOCAB) -> Workload:
+def c4(seed: int = 4, rows: int = 512, vocab: int = VOCAB, f32: bool = False) -> Workload:
     """Batch 512, bf16 N(0,0.1) (RNE from f32); top-k off, p 0.9, T 1.3, no
-    penalty; softcap 30 (model default)."""
+    penalty; softcap 30 (model default). f32=True keeps the f32 logits (the
+    same rows before rounding): the f32 full-order path."""
     rng = _rng(seed)
     x = (rng.standard_normal((rows, vocab), dtype=np.float32) * np.float32(0.1)).astype(np.float32)
-    bits = f32_to_bf16_bits(x)
     hist = np.zeros(0, np.int32)
     offsets = np.zeros(rows + 1, np.int32)
     p = dict(temperature=1.3, top_k=0, top_p=0.9, min_p=0.0, softcap=30.0,
              repetition_penalty=1.0)
-    return Workload("C4", bits, "bf16", p, hist, offsets, mt_uniforms(seed, rows), seed)
+    if f32:
+        return Workload("C4-f32", x, "f32", p, hist, offsets, mt_uniforms(seed, rows), seed)
+    return Workload("C4", f32_to_bf16_bits(x), "bf16", p, hist, offsets, mt_uniforms(seed, rows), seed)
 
 
 def c5_steps(seed: int = 5, steps: int = 1024, vocab: int = VOCAB) -> Workload:
