@@ -129,9 +129,8 @@ int ge_sample(ge_sampler* sampler, void* stream, const ge_sample_args* args);
 const char* ge_sampler_last_error(void);
 
 /* Largest top_k handled by the selection path of this build. Rows whose
- * effective k exceeds it (top_k disabled or larger) take the full-order path,
- * which this build implements for bf16 logits only; fp32 rows get
- * GE_FLAG_UNSUPPORTED (or GE_ERR_UNSUPPORTED when known on the host). */
+ * effective k exceeds it (top_k disabled or larger, generation.cpp:80) take
+ * the full-order path, for bf16 and fp32 logits alike. */
 int ge_sampler_max_top_k(void);
 
 #ifdef __cplusplus
