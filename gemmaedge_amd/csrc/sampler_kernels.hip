@@ -54,6 +54,8 @@
 namespace ge {
 namespace {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kStage = 2048;    // LDS staging entries (candidates, union)
 constexpr int kLoadBatch = 8;   // independent global loads in flight per thread
 constexpr uint32_t kPenTag = 0x80000000u;     // staged entry: penalised token
@@ -79,6 +81,25 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
 }
+
+// Chunk list entries carry raw (pre-softcap) values:
+//   (raw order key << 32) | (penalised ? 0 : 2^31) | (2^31 - 1 - index).
+// Entries are distinct and non-zero; a larger entry has a larger raw value,
+// or the same raw value and (unpenalised before penalised, then) a lower
+// index. Final values are computed from them by the merging workgroup.
+__device__ __forceinline__ uint64_t raw_entry(uint32_t key, uint32_t index, bool pen) {
+    return (static_cast<uint64_t>(key) << 32) | ((pen ? 0u : 0x80000000u) | (0x7fffffffu - index));
+}
+__device__ __forceinline__ uint32_t raw_entry_index(uint64_t e) {
+    return 0x7fffffffu - (static_cast<uint32_t>(e) & 0x7fffffffu);
+}
+__device__ __forceinline__ bool raw_entry_pen(uint64_t e) { return (static_cast<uint32_t>(e) & 0x80000000u) == 0u; }
+__device__ __forceinline__ uint32_t raw_entry_low(uint32_t index, bool pen) {
+    return (pen ? 0u : 0x80000000u) | (0x7fffffffu - index);
+}
+// A chunk whose candidates could not be staged publishes this guarantee; the
+// merge rescans it exactly.
+constexpr uint64_t kGuaranteeFailed = ~0ull;
 
 __device__ __forceinline__ float readlane_f(float v, int i) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
@@ -138,23 +159,40 @@ __device__ __forceinline__ int lsb_exponent(float e) {
     return static_cast<int>(ex) - 150 + __builtin_ctz(man | 0x800000u);
 }
 
+// Largest list a chunk publishes (the top-m by raw value; m may exceed k by
+// a few entries so that the merge can certify the k-th).
+constexpr int kListCap = kMaxTopK + 8;
+
 // List length each chunk publishes for a row with effective top-k `k`: the
-// mean share k / cpr plus four binomial standard deviations plus 4, capped by
-// k, by the chunk length and by the row's slot capacity (cpr * (m + 1) words
-// <= kSlotWords). The host and every workgroup of the row compute the same m.
+// mean share k / cpr plus four binomial standard deviations plus 4, at least
+// 2 and at most k + 4 (the merge certifies its k-th entry against the
+// largest m-th entry, so a chunk lists a few more than it contributes), capped
+// by the chunk length and the chunk's slot (kSlotWords / cpr words:
+// guarantee, count, entries). Every workgroup of the row computes the same m.
 __device__ __forceinline__ uint32_t spec_m(uint32_t k, int cpr, int chunk_len) {
-    if (k <= 1u) return 1u;
     const float mu = static_cast<float>(k) / static_cast<float>(cpr);
     uint32_t m = static_cast<uint32_t>(ceilf(mu + 4.0f * sqrtf(mu))) + 4u;
-    m = min(m, k);
+    m = min(m, k + 4u);
+    m = max(m, 2u);
+    m = min(m, static_cast<uint32_t>(kListCap));
     m = min(m, static_cast<uint32_t>(chunk_len));
-    m = min(m, static_cast<uint32_t>(kSlotWords / cpr - 1));
+    m = min(m, static_cast<uint32_t>(kSlotWords / cpr - 2));
     return max(m, 1u);
+}
+
+// The merge's first level: it first trusts only the top j1 entries of each
+// chunk list (about the mean share plus three standard deviations, plus 2),
+// which certifies the row's top k in about 99% of rows with far fewer
+// entries to rank; the full lists (level m) are its second try.
+__device__ __forceinline__ uint32_t spec_level1(uint32_t k, int cpr, uint32_t m) {
+    const float mu = static_cast<float>(k) / static_cast<float>(cpr);
+    const uint32_t j = static_cast<uint32_t>(ceilf(mu + 3.0f * sqrtf(mu))) + 2u;
+    return min(j, m);
 }
 
 struct __align__(16) SelShared {
     uint64_t stage[kStage];      // candidates (staging) / union / sort area; floats of the softmax
-    uint64_t list[kMaxTopK];     // chunk routine output: its top-m, sorted descending
+    uint64_t list[kListCap];     // chunk routine output: its top-m, sorted descending
     uint64_t top[kMaxTopK];      // merge: the row's top-k, sorted descending
     uint64_t gam[kMaxChunks];    // merge: guarantee of each chunk
     uint64_t exp_tab[32];        // merge: the expf table (2^(i/32)), staged from constant memory
@@ -163,6 +201,7 @@ struct __align__(16) SelShared {
     double f64[kBlock / 64];
     int i32[kBlock / 64];
     uint32_t u32[32];
+    uint32_t cnt[kMaxChunks];    // merge: entries each chunk published
 };
 
 // Exclusive prefix over the workgroup of one value per thread; also returns
@@ -222,11 +261,12 @@ __device__ __forceinline__ void find_bin_desc(const uint32_t* hist, uint32_t k, 
 // Lower bound on the k-th largest of the keys that `visit` presents within
 // [lo, hi] (every thread calls visit(f) and f(key) runs once per key it
 // holds). Two radix passes over the 8-bit digits right below the common prefix
-// of lo and hi. Returns 0 if fewer than k keys lie in [lo, hi]. Uses sh.hist
-// and sh.u32[20..22]; block-uniform.
+// of lo and hi; the second is skipped when at most keep_max keys lie at or
+// above the first pass's bin. Returns 0 if fewer than k keys lie in [lo, hi].
+// Uses sh.hist and sh.u32[20..22]; block-uniform.
 template <typename Visit>
 __device__ __forceinline__ uint32_t block_kth(uint32_t lo, uint32_t hi, uint32_t k, Visit&& visit,
-                                              SelShared& sh) {
+                                              SelShared& sh, uint32_t keep_max = 0u) {
     const int tid = threadIdx.x;
     if (lo > hi || k == 0) return 0u;
     const uint32_t diff = lo ^ hi;
@@ -244,10 +284,12 @@ __device__ __forceinline__ uint32_t block_kth(uint32_t lo, uint32_t hi, uint32_t
     const uint32_t d1 = sh.u32[20];
     const uint32_t above = sh.u32[21];
     const bool short_set = sh.u32[22] != 0u;
+    const uint32_t in_bin = short_set ? 0u : sh.hist[d1];
     __syncthreads();
     if (short_set) return 0u;
     const uint32_t pre = base1 + d1;
     if (shift1 == 0) return pre;
+    if (above + in_bin <= keep_max) return pre << shift1;  // few enough at or above its bin
     const int shift2 = max(shift1 - 8, 0);
     const uint32_t bucket = pre << shift1;
     for (int i = tid; i < 256; i += kBlock) sh.hist[i] = 0u;
@@ -463,6 +505,67 @@ __device__ __forceinline__ uint32_t select_top(uint64_t* src, uint32_t n, uint32
     return out;
 }
 
+// Number of the n keys hk[0, n) (padded with zeros to a multiple of 16)
+// greater than h, counted on 31-bit halves: key >> 1 > h >> 1 exactly when
+// (h >> 1) - (key >> 1) borrows, so the count is a sum of sign bits (no
+// compare-to-mask round trips). Keys equal in all but their lowest bit are
+// not counted; callers detect the resulting equal ranks. Four 16-byte LDS
+// reads are issued per step before any is used.
+__device__ __forceinline__ uint32_t count_greater_hi(const uint32_t* hk, uint32_t n, uint32_t h) {
+    const uint4* p4 = reinterpret_cast<const uint4*>(hk);
+    const uint32_t hh = h >> 1;
+    uint32_t r = 0;
+    auto acc = [&](const uint4& q) {
+        r += ((hh - (q.x >> 1)) >> 31) + ((hh - (q.y >> 1)) >> 31);
+        r += ((hh - (q.z >> 1)) >> 31) + ((hh - (q.w >> 1)) >> 31);
+    };
+    for (uint32_t j = 0; j < (n + 15u) / 16u; ++j) {
+        const uint4 q0 = p4[4 * j + 0];
+        const uint4 q1 = p4[4 * j + 1];
+        const uint4 q2 = p4[4 * j + 2];
+        const uint4 q3 = p4[4 * j + 3];
+        acc(q0);
+        acc(q1);
+        acc(q2);
+        acc(q3);
+    }
+    return r;
+}
+
+// dst[0, min(n, m)) = the largest min(n, m) of the distinct non-zero keys
+// src[0, n) (n <= kBlock), sorted descending, by counting on their high words
+// only (count_greater_hi), about half the work of 64-bit keys. Two keys whose
+// high words agree but for the lowest bit can get the same rank; a
+// compare-and-swap into dst (cleared first) detects that and the exact 64-bit
+// ranking takes over. With `hk_ready`, sh.hist[0, n) already holds the high
+// words (padded to a multiple of 16). Block-uniform; uses sh.hist.
+__device__ __forceinline__ uint32_t rank_top_hi(SelShared& sh, uint64_t* src, uint32_t n, uint32_t m,
+                                                uint64_t* dst, bool hk_ready = false) {
+    const int tid = threadIdx.x;
+    const uint32_t out = min(n, m);
+    uint32_t* hk = sh.hist;
+    if (!hk_ready) {
+        if (static_cast<uint32_t>(tid) < n) hk[tid] = static_cast<uint32_t>(src[tid] >> 32);
+        else if (static_cast<uint32_t>(tid) < ((n + 15u) & ~15u)) hk[tid] = 0u;  // below every entry
+    }
+    if (static_cast<uint32_t>(tid) < out) dst[tid] = 0ull;
+    if (tid == 0) sh.u32[16 + 3] = 0u;
+    __syncthreads();
+    // (Read after the barrier: with hk_ready other waves have just written src.)
+    const uint64_t x = static_cast<uint32_t>(tid) < n ? src[tid] : 0ull;
+    if (static_cast<uint32_t>(tid) < n) {
+        const uint32_t r = count_greater_hi(hk, n, static_cast<uint32_t>(x >> 32));
+        if (r < m) {
+            const unsigned long long old = atomicCAS(reinterpret_cast<unsigned long long*>(&dst[r]), 0ull,
+                                                     static_cast<unsigned long long>(x));
+            if (old != 0ull) sh.u32[16 + 3] = 1u;  // equal ranks
+        }
+    }
+    __syncthreads();
+    if (sh.u32[16 + 3] != 0u) return select_top(src, n, m, dst);
+    return out;
+}
+
 // The row-level context every workgroup of a row shares.
 struct RowCtx {
     const void* rowp;   // the row's logits
@@ -629,6 +732,129 @@ __device__ __forceinline__ uint64_t chunk_slow(const RowCtx& rc, int c0, uint32_
     return n_out == m ? sh.list[m - 1] : 0ull;
 }
 
+// With a penalty below 1 a penalised token can rise above any bound taken
+// from raw values, so every penalised candidate of the chunk is listed: those
+// among sh.stage[0, n_c) below the m-th entry `last` are written to the
+// chunk's slot after the top m (slot[2 + m ...], stride words in all).
+// Returns the number appended; ok = false if they do not fit. Block-uniform.
+__device__ __forceinline__ uint32_t append_penalised(SelShared& sh, uint32_t n_c, uint32_t m, uint64_t last,
+                                                     uint64_t* slot, uint32_t stride, bool& ok) {
+    const int tid = threadIdx.x;
+    if (tid == 0) sh.u32[17] = 0u;
+    __syncthreads();
+    for (uint32_t i = tid; i < n_c; i += kBlock) {
+        const uint64_t x = sh.stage[i];
+        if (x != 0ull && raw_entry_pen(x) && x < last) {
+            const uint32_t pos = atomicAdd(&sh.u32[17], 1u);
+            if (m + 2u + pos < stride) store_shared(&slot[m + 2u + pos], x);
+        }
+    }
+    __syncthreads();
+    const uint32_t extra = sh.u32[17];
+    __syncthreads();
+    if (m + 2u + extra > stride) ok = false;
+    return extra;
+}
+
+// Exact raw top-m of one chunk for the rare cases of the streaming pass
+// (candidates that overflow LDS: massive ties, NaN-heavy or partial chunks).
+// Same contract as chunk_topm; the penalty bitmap pbits is already built.
+// Runtime loops over one 16-byte group per thread, reloading the chunk from
+// memory (L2 / MALL) in every pass:
+//   1. R = the exact m-th largest raw order key (radix select);
+//   2. Lq = the (m - #above R)-th largest entry low word among the keys
+//      equal to R (low words are distinct), so that exactly m entries are
+//      >= raw_entry(R, Lq);
+//   3. stage those (and, with a penalty below 1, every penalised element),
+//      sort, keep the top m.
+template <typename T, int EPT>
+__device__ __forceinline__ uint64_t chunk_slow_raw(const RowCtx& rc, int c0, uint32_t m, const uint32_t* pbits,
+                                                   SelShared& sh, uint64_t* slot, uint32_t stride,
+                                                   uint32_t& n_top, uint32_t& n_out, bool& ok) {
+    constexpr int W = sizeof(T) == 4 ? 4 : 8;
+    constexpr int NV = EPT / W;
+    constexpr int CHUNK = kBlock * EPT;
+    const int tid = opaque_tid();
+    const T* rowp = static_cast<const T*>(rc.rowp);
+    const int cend = min(c0 + CHUNK, rc.V);
+    const bool pen_all = rc.pen && !(rc.r >= 1.0f);
+    ok = true;
+    auto is_pen = [&](int e) -> bool {
+        return rc.pen && ((pbits[(e - c0) >> 5] >> ((e - c0) & 31)) & 1u);
+    };
+    auto load_group = [&](int v, float (&x)[W]) {
+        const int e0 = c0 + (v * kBlock + tid) * W;
+#pragma unroll
+        for (int j = 0; j < W; ++j) x[j] = e0 + j < cend ? load_one(rowp, e0 + j) : NAN;
+    };
+    auto visit_keys = [&](auto&& f) {
+#pragma unroll 1
+        for (int v = 0; v < NV; ++v) {
+            float x[W];
+            load_group(v, x);
+            const int e0 = c0 + (v * kBlock + tid) * W;
+#pragma unroll
+            for (int j = 0; j < W; ++j)
+                if (e0 + j < cend) f(order_key(x[j]));
+        }
+    };
+    const uint32_t R = block_kth_exact(1u, 0xffffffffu, m, visit_keys, sh);
+    uint32_t lq = 0u;  // R == 0: fewer than m elements, list them all
+    if (R != 0u) {
+        uint32_t above = 0;
+        visit_keys([&](uint32_t key) { above += key > R ? 1u : 0u; });
+        above = block_sum(above, sh);
+        const uint32_t q = m - above;  // >= 1
+        auto visit_lows = [&](auto&& f) {
+#pragma unroll 1
+            for (int v = 0; v < NV; ++v) {
+                float x[W];
+                load_group(v, x);
+                const int e0 = c0 + (v * kBlock + tid) * W;
+#pragma unroll
+                for (int j = 0; j < W; ++j)
+                    if (e0 + j < cend && order_key(x[j]) == R)
+                        f(raw_entry_low(static_cast<uint32_t>(e0 + j), is_pen(e0 + j)));
+            }
+        };
+        lq = block_kth_exact(1u, 0xffffffffu, q, visit_lows, sh);
+    }
+    const uint64_t thr = R != 0u ? ((static_cast<uint64_t>(R) << 32) | lq) : 0ull;
+    uint32_t n_c = 0;
+#pragma unroll 1
+    for (int v = 0; v < NV; ++v) {
+        float x[W];
+        load_group(v, x);
+        const int e0 = c0 + (v * kBlock + tid) * W;
+        uint64_t ent[W];
+        uint32_t cand = 0;
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+            const bool in = e0 + j < cend;
+            const bool pj = in && is_pen(e0 + j);
+            ent[j] = raw_entry(order_key(x[j]), static_cast<uint32_t>(e0 + j), pj);
+            cand |= static_cast<uint32_t>(in && (ent[j] >= thr || (pen_all && pj))) << j;
+        }
+        uint32_t total;
+        uint32_t pos = n_c + block_excl_scan(static_cast<uint32_t>(__popc(cand)), total, sh);
+        if (n_c + total > static_cast<uint32_t>(kStage)) {
+            ok = false;
+            n_top = n_out = 0;
+            return kGuaranteeFailed;
+        }
+#pragma unroll
+        for (int j = 0; j < W; ++j)
+            if ((cand >> j) & 1u) sh.stage[pos++] = ent[j];
+        n_c += total;
+    }
+    __syncthreads();
+    n_top = select_top(sh.stage, n_c, m, sh.list);
+    n_out = n_top;
+    const uint64_t g = (R != 0u && n_top == m) ? sh.list[m - 1] : 0ull;
+    if (pen_all && n_c > m) n_out += append_penalised(sh, n_c, m, g, slot, stride, ok);
+    return ok ? g : kGuaranteeFailed;
+}
+
 // The t-th largest (1 <= t <= 64) of the wave's 64 keys, wave-uniform. For
 // small t, t rounds of "maximum, then retire one lane holding it"; else a
 // bit-by-bit ballot search.
@@ -651,6 +877,8 @@ constexpr int kSeg = kStage / (kBlock / 64);
 // sh.u32 words holding the segment counts. Not shared with any other helper's
 // scratch: block_excl_scan (24..27) can run right after the counts are read.
 constexpr int kSegCount = 28;
+// Up to this many entries the merge ranks them by counting directly.
+constexpr uint32_t kRankDirect = 96;
 
 // dst[0, min(n, m)) = the largest of the n <= kBlock distinct non-zero keys in
 // the segments, sorted descending (rank by counting, keys in pairs).
@@ -708,21 +936,25 @@ __device__ __forceinline__ void seg_gather(uint64_t* stage, const uint32_t (&cnt
     __syncthreads();
 }
 
-// Exact top-m of one chunk (elements [c0, min(c0 + CHUNK, V))) by composite
-// final key, sorted descending into sh.list[0, n_out). Returns the chunk's
-// guarantee: every element of the chunk whose composite key is >= it is in
-// the list. ok = false if the candidates could not be staged (more than
-// kStage penalised ties). Block-uniform; every thread returns the same values.
+// Raw top-m of one chunk (elements [c0, min(c0 + CHUNK, V))): the m largest
+// raw list entries (raw value descending; see raw_entry), sorted descending
+// into sh.list[0, n_top). With a penalty below 1, every penalised element of
+// the chunk is listed too (appended to the slot after the top m; n_out counts
+// them all). Returns the chunk's guarantee g: every element left out has a
+// raw entry < g, so (softcap being monotone and a penalty >= 1 never raising
+// a value) its final value is at most softcap(value of g); g = 0 when the
+// chunk listed everything, kGuaranteeFailed when its candidates could not be
+// staged. The list being sorted, its j-th entry is such a guarantee for the
+// first j entries too. No softcap is evaluated here: the merge caps only what
+// it needs. Block-uniform; every thread returns the same values.
 //
-// Why the guarantee holds whatever bound tau is used: a non-penalised element
-// whose final value reaches softcap(tau) has raw >= floor (softcap is
-// monotone), so it is a candidate; a penalised one with r >= 1 ends at or
-// below its softcapped raw value, so it also needs raw >= floor; with r < 1
-// every penalised token is a candidate. tau only decides how strong the
-// guarantee is (and how many candidates there are).
+// The bound tau: at least m elements of the chunk have a raw order key >=
+// tau (from the maxima of groups of logits). Every element >= tau is staged,
+// so the top m of the staged entries is the chunk's top m.
 template <typename T, int EPT>
 __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_t m, uint32_t* pbits,
-                                               SelShared& sh, uint32_t& n_out, bool& ok) {
+                                               SelShared& sh, uint64_t* slot, uint32_t stride,
+                                               uint32_t& n_top, uint32_t& n_out, bool& ok) {
     constexpr int W = sizeof(T) == 4 ? 4 : 8;  // elements per 16-byte load
     constexpr int NV = EPT / W;                 // 16-byte loads per thread
     constexpr int NW = EPT * sizeof(T) / 4;     // 32-bit words per thread
@@ -735,8 +967,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     const int wave = tid >> 6;
     const T* rowp = static_cast<const T*>(rc.rowp);
     const int cend = min(c0 + CHUNK, rc.V);
-    const float cap = rc.cap;
-    const float r = rc.r;
+    const bool pen_all = rc.pen && !(rc.r >= 1.0f);
     ok = true;
 
     // Slot s of this thread is element c0 + ((s / W) * kBlock + tid) * W + s % W.
@@ -756,9 +987,11 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     uint32_t d[NW];
     uint64_t vmask = ~0ull;  // in-range slots
     if (rc.vec_ok && c0 + CHUNK <= rc.V) {
+        // Streaming loads: each logit is read once, so they carry the
+        // nontemporal hint and do not displace the lists and history in L2.
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
-            const uint4 q = *reinterpret_cast<const uint4*>(rowp + c0 + (v * kBlock + tid) * W);
+            const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + c0 + (v * kBlock + tid) * W));
             d[4 * v + 0] = q.x;
             d[4 * v + 1] = q.y;
             d[4 * v + 2] = q.z;
@@ -797,11 +1030,29 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             for (int i = 0; i < NW; ++i) asm volatile("" : "+v"(d[i]));
         }
     };
-    if (rc.pen)
-        for (int w = tid; w < CHUNK / 32; w += kBlock) pbits[w] = 0u;
 
-    // 2. The bound. Maxima of groups of 4 raw values (fmaxf ignores the NaN
-    //    of out-of-range slots; penalised slots take part, see above).
+    // 2. The penalty bitmap (one bit per element of the chunk) from the row's
+    //    history, while the logits are in flight: the ids arrive first.
+    if (rc.pen) {
+        for (int w = tid; w < CHUNK / 32; w += kBlock) pbits[w] = 0u;
+        __syncthreads();
+        for (int base = 0; base < rc.H; base += kBlock * kLoadBatch) {
+            if (base > 0) {
+#pragma unroll
+                for (int u = 0; u < kLoadBatch; ++u) {
+                    const int j = base + u * kBlock + tid;
+                    hid[u] = j < rc.H ? rc.hist[j] : -1;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kLoadBatch; ++u)
+                if (hid[u] >= c0 && hid[u] < cend)
+                    atomicOr(&pbits[(hid[u] - c0) >> 5], 1u << ((hid[u] - c0) & 31));
+        }
+    }
+
+    // 3. The bound. Maxima of groups of 4 raw values (fmaxf ignores the NaN
+    //    of out-of-range slots).
     float gm[NG];
     float lmf = NAN;
 #pragma unroll
@@ -817,10 +1068,11 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     uint32_t tau;
     if (m <= 64u) {
         // Each wave: the ceil(m/4)-th largest of its 64 lane maxima; the
-        // smallest of the four leaves >= m elements at or above it.
+        // smallest of the four leaves >= m elements at or above it. The
+        // barrier also orders the bitmap's marks before the staging reads.
         const uint32_t tw = wave_kth(lkey, (m + 3u) / 4u);
         if (lane == 0) sh.u32[8 + wave] = tw;
-        __syncthreads();  // also orders the bitmap clear before its fill
+        __syncthreads();
         tau = min(min(sh.u32[8], sh.u32[9]), min(sh.u32[10], sh.u32[11]));
     } else {
         uint32_t gmn = 0xffffffffu;
@@ -842,73 +1094,36 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
                         },
                         sh);
     }
+    // tau <= kKeyNaN: fewer than m real logits in some wave; no pruning.
+    const bool allpass = tau <= kKeyNaN;
+    if (allpass && cend - c0 > kStage) return chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
+    const float floor_v = key_value(max(tau, kKeyNegInf));  // raw >= floor_v <=> key >= tau
 
-    // 3. Wave 0: the tie floor, and the guarantee floor g_floor (every element
-    //    whose final key reaches it is staged). Alongside, every lane caps its
-    //    own maximum (most candidates are lane maxima, so their final values
-    //    are ready when they are staged), and every wave marks the penalised
-    //    tokens in the bitmap from the ids loaded at the start.
-    //    One softcap evaluation per lane: lanes 0 and 1 of wave 0 take
-    //    tau and tau - 1 (the tie floor's first probe), every other lane its
-    //    own maximum.
-    const bool probe = wave == 0 && lane < 2;
-    const float sc = softcap(probe ? key_value(tau - static_cast<uint32_t>(lane)) : lmf, cap);
-    const float lcap = sc;  // meaningful where !probe
-    if (wave == 0) {
-        const float ct = u2f(wave::readlane(f2u(sc), 0));
-        const float cb = u2f(wave::readlane(f2u(sc), 1));
-        const uint32_t thr0 = max(tie_floor_given(tau, cap, ct, cb), kKeyNaN);
-        if (lane == 0) {
-            sh.u32[2] = thr0;
-            sh.u32[3] = thr0 <= kKeyNaN ? 0u : order_key(cap > 0.0f ? ct : key_value(tau));
-        }
-    }
+    // Penalty bits of this thread's slots (bit s = slot s), read once: the W
+    //    elements of a 16-byte group lie in one bitmap word.
+    uint64_t pm = 0ull;
     if (rc.pen) {
-        for (int base = 0; base < rc.H; base += kBlock * kLoadBatch) {
-            if (base > 0) {
 #pragma unroll
-                for (int u = 0; u < kLoadBatch; ++u) {
-                    const int j = base + u * kBlock + tid;
-                    hid[u] = j < rc.H ? rc.hist[j] : -1;
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kLoadBatch; ++u)
-                if (hid[u] >= c0 && hid[u] < cend)
-                    atomicOr(&pbits[(hid[u] - c0) >> 5], 1u << ((hid[u] - c0) & 31));
+        for (int v = 0; v < NV; ++v) {
+            const int off = (v * kBlock + tid) * W;  // element offset in the chunk
+            pm |= static_cast<uint64_t>((pbits[off >> 5] >> (off & 31)) & ((1u << W) - 1u)) << (v * W);
         }
     }
-    __syncthreads();
-    const uint32_t thr = sh.u32[2];
-    const uint32_t g_floor = sh.u32[3];
-    const bool allpass = thr <= kKeyNaN;
-    const float floor_v = key_value(max(thr, kKeyNegInf));  // raw >= floor_v <=> key >= thr
-    const bool pen_all = rc.pen && !(r >= 1.0f);
-    if (allpass && cend - c0 > kStage) {
-        // No pruning possible (fewer than m real logits in some wave): the
-        // exact routine.
-        return chunk_slow<T, EPT>(rc, c0, m, pbits, sh, n_out, ok);
-    }
 
-    // 4. Stage the candidates from ballots into this wave's segment. Entry:
-    //    (index | kKnown if the value is already final-before-penalty) << 32
-    //    | value bits. A group of 4 slots is examined only if its maximum
-    //    reaches the floor; with r < 1 every penalised token is a candidate.
-    constexpr uint32_t kKnown = 0x80000000u;
+    // 4. Stage the candidates from ballots into this wave's segment as raw
+    //    entries. A group of 4 slots is examined only if its maximum reaches
+    //    the bound; with a penalty below 1 every penalised token is a
+    //    candidate.
     const int ebase = c0 + tid * W;
     uint32_t woff = 0;  // wave-uniform
     uint64_t* seg = sh.stage + wave * kSeg;
-    auto is_pen = [&](int e) -> bool { return ((pbits[(e - c0) >> 5] >> ((e - c0) & 31)) & 1u) != 0u; };
     auto put = [&](bool c, int s) {
         const uint64_t mk = __ballot(c);
         if (mk) {
             const uint32_t o = woff + lanes_below(mk);
             if (c && o < static_cast<uint32_t>(kSeg)) {
                 const int e = ebase + (s / W) * kBlock * W + s % W;
-                const float x = value(s);
-                const bool known = !probe && f2u(x) == f2u(lmf);
-                seg[o] = (static_cast<uint64_t>(static_cast<uint32_t>(e) | (known ? kKnown : 0u)) << 32) |
-                         f2u(known ? lcap : x);
+                seg[o] = raw_entry(order_key(value(s)), static_cast<uint32_t>(e), ((pm >> s) & 1ull) != 0ull);
             }
             woff += static_cast<uint32_t>(__popcll(mk));
         }
@@ -925,13 +1140,10 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
         }
     } else {
 #pragma unroll
-        for (int s = 0; s < EPT; ++s) {
-            const int e = ebase + (s / W) * kBlock * W + s % W;
-            put(value(s) >= floor_v || (((vmask >> s) & 1ull) && is_pen(e)), s);
-        }
+        for (int s = 0; s < EPT; ++s) put(value(s) >= floor_v || ((pm >> s) & 1ull) != 0ull, s);
     }
     fence_words();
-    // Pad an odd segment with an empty key (the rank reads keys in pairs).
+    // Pad an odd segment with an empty entry (the rank reads entries in pairs).
     if (lane == 0) {
         sh.u32[kSegCount + wave] = woff;
         if ((woff & 1u) && woff < static_cast<uint32_t>(kSeg)) seg[woff] = 0ull;
@@ -948,36 +1160,34 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     }
     if (seg_over) {
         // Massive ties or a loose bound: the exact routine.
-        return chunk_slow<T, EPT>(rc, c0, m, pbits, sh, n_out, ok);
+        return chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
     }
-    // 5. Final values of this wave's candidates: softcap where not already
-    //    known, then the penalty once per token.
-    for (uint32_t i = lane; i < cnt[wave]; i += 64) {
-        const uint64_t x = seg[i];
-        const uint32_t hi = static_cast<uint32_t>(x >> 32);
-        const uint32_t e = hi & ~kKnown;
-        float f = u2f(static_cast<uint32_t>(x));
-        if (!(hi & kKnown)) f = softcap(f, cap);
-        if (rc.pen && is_pen(static_cast<int>(e))) f = penalize(f, r);
-        seg[i] = composite(order_key(f), e);
-    }
-    __syncthreads();
-    // 6. Top m, sorted. Up to kBlock candidates: rank by counting over the
-    //    segments; more: gather them and sort.
+    // 5. The top m, sorted. Up to kBlock candidates: each wave moves its
+    //    segment to its place in stage[0, n_c) (inside segment 0's area past
+    //    wave 0's entries, so no wave overwrites another's unread entries)
+    //    with the high words beside it, then rank by counting. More: gather
+    //    and sort.
     if (n_c <= static_cast<uint32_t>(kBlock)) {
-        seg_rank_top(sh.stage, cnt, n_c, m, sh.list);
-        n_out = min(n_c, m);
+        uint32_t base = 0;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) base += w < wave ? cnt[w] : 0u;
+        for (uint32_t i = lane; i < cnt[wave]; i += 64) {
+            const uint64_t x = seg[i];
+            sh.stage[base + i] = x;
+            sh.hist[base + i] = static_cast<uint32_t>(x >> 32);
+        }
+        for (uint32_t i = n_c + tid; i < ((n_c + 15u) & ~15u); i += kBlock) sh.hist[i] = 0u;
+        n_top = rank_top_hi(sh, sh.stage, n_c, m, sh.list, true);
     } else {
         seg_gather(sh.stage, cnt, n_c);
-        n_out = select_top(sh.stage, n_c, m, sh.list);
+        n_top = select_top(sh.stage, n_c, m, sh.list);
     }
-    // The guarantee: the larger of the floor's and the m-th listed key.
-    uint64_t gamma = static_cast<uint64_t>(g_floor) << 32;
-    if (n_out == m) {
-        const uint64_t last = sh.list[m - 1];
-        gamma = last > gamma ? last : gamma;
-    }
-    return gamma;
+    n_out = n_top;
+    // Elements below tau are below the m-th entry; all-pass chunks with at
+    // most m elements listed everything.
+    const uint64_t g = n_top == m ? sh.list[m - 1] : 0ull;
+    if (pen_all && n_c > m) n_out += append_penalised(sh, n_c, m, g, slot, stride, ok);
+    return ok ? g : kGuaranteeFailed;
 }
 
 __device__ __forceinline__ void write_row(const DevArgs& a, int row, int32_t token, float prob,
@@ -992,6 +1202,8 @@ __device__ __forceinline__ void write_row(const DevArgs& a, int row, int32_t tok
         a.ring_len[row] = static_cast<int32_t>(len + 1u);
     }
     a.tickets[row] = 0u;  // ready for the next launch
+    a.row_gmax[2 * row] = 0ull;
+    a.row_gmax[2 * row + 1] = 0ull;
 }
 
 // generation.cpp:103-126 on probabilities sorted by value desc / index asc,
@@ -1240,62 +1452,91 @@ __device__ __forceinline__ uint32_t absorb_list(SelShared& sh, uint32_t nt, uint
     return min(kept_total, k);
 }
 
-// Merge, first part (last workgroup of the row): one round trip for every
-// chunk's guarantee and list (sh.gam[c] = guarantee of chunk c). If at least
-// k listed entries are >= the largest guarantee, their top-k is the row's:
-// sh.top[0, keff) holds it and the function returns true. Otherwise sh.top
-// holds the top of everything listed (nt entries) and the chunks whose
-// guarantee is above its k-th entry need a rescan; returns false.
-__device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, int row, uint32_t k,
-                                              uint32_t m, uint32_t& nt) {
+// Loads the row's slot words, kPer per thread: w[i], its position wp[i] in
+// its chunk's slot (0 = the guarantee, 1 = the count, 2.. = entries; past the
+// end: 0xffffffff) and its chunk wc[i]; stores each chunk's guarantee in
+// sh.gam[c] and its count in sh.cnt[c]. One round trip. After a barrier,
+// slot_entry(...) tells which words are entries of this launch (a chunk's
+// words past its count hold older data).
+template <int kPer>
+__device__ __forceinline__ void load_slots(const DevArgs& a, SelShared& sh, int row, uint32_t stride,
+                                           uint64_t (&w)[kPer], uint32_t (&wp)[kPer], uint32_t (&wc)[kPer]) {
     const int tid = threadIdx.x;
-    const int lane = __lane_id();
-    if (tid < 32) sh.exp_tab[tid] = exp2_table(static_cast<uint32_t>(tid));  // in flight with the slots
-    constexpr int kPer = kSlotWords / kBlock;
-    const uint32_t sl = m + 1;
-    const uint32_t words = static_cast<uint32_t>(a.cpr) * sl;  // <= kSlotWords
+    const uint32_t words = static_cast<uint32_t>(a.cpr) * stride;  // <= kSlotWords
     const uint64_t* slot_row = a.slots + static_cast<int64_t>(row) * kSlotWords;
-
-    uint64_t w[kPer];
-    uint32_t wp[kPer];  // position in the chunk's slot: 0 = guarantee
-    {
-        uint32_t c = static_cast<uint32_t>(tid) / sl, q = static_cast<uint32_t>(tid) % sl;
-        const uint32_t dc = kBlock / sl, dq = kBlock % sl;
+    // All loads first (independent round trips in flight together), then the
+    // LDS writes that need their results.
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const uint32_t g = static_cast<uint32_t>(i * kBlock + tid);
-            w[i] = g < words ? load_shared(&slot_row[g]) : 0ull;
-            wp[i] = g < words ? q : 1u;  // past the end: an empty entry
-            if (g < words && q == 0u) sh.gam[c] = w[i];
-            c += dc;
-            q += dq;
-            if (q >= sl) {
-                q -= sl;
-                ++c;
-            }
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t g = static_cast<uint32_t>(i * kBlock + tid);
+        w[i] = g < words ? load_shared(&slot_row[g]) : 0ull;
+    }
+    uint32_t c = static_cast<uint32_t>(tid) / stride, q = static_cast<uint32_t>(tid) % stride;
+    const uint32_t dc = kBlock / stride, dq = kBlock % stride;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t g = static_cast<uint32_t>(i * kBlock + tid);
+        wp[i] = g < words ? q : 0xffffffffu;
+        wc[i] = c;
+        c += dc;
+        q += dq;
+        if (q >= stride) {
+            q -= stride;
+            ++c;
         }
     }
-    if (tid == 0) sh.u64[0] = 0ull;
-    __syncthreads();
-    uint64_t gmax = 0ull;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i)
-        if (wp[i] == 0u) gmax = w[i] > gmax ? w[i] : gmax;
-    gmax = wave_max_u64(gmax);
-    if (lane == 0) atomicMax(reinterpret_cast<unsigned long long*>(&sh.u64[0]),
-                             static_cast<unsigned long long>(gmax));
-    __syncthreads();
-    const uint64_t gam_max = sh.u64[0];
+    for (int i = 0; i < kPer; ++i) {
+        if (wp[i] == 0u) sh.gam[wc[i]] = w[i];
+        if (wp[i] == 1u) sh.cnt[wc[i]] = static_cast<uint32_t>(w[i]);
+    }
+}
 
-    // Entries at or above the largest guarantee, staged in per-wave segments.
-    uint32_t nsel = 0;
+__device__ __forceinline__ bool slot_entry(const SelShared& sh, uint32_t wp, uint32_t wc) {
+    return wp >= 2u && wp != 0xffffffffu && wp - 2u < sh.cnt[wc];
+}
+
+// Final composite key of a raw list entry: softcap, then the penalty if the
+// entry is penalised.
+__device__ __forceinline__ uint64_t final_of(uint64_t e, const RowCtx& rc) {
+    float f = softcap(key_value(static_cast<uint32_t>(e >> 32)), rc.cap);
+    if (rc.pen && raw_entry_pen(e)) f = penalize(f, rc.r);
+    return composite(order_key(f), raw_entry_index(e));
+}
+
+// Merge, first part (last workgroup of the row), one round trip for every
+// chunk's guarantee and list. With G the largest guarantee, every element
+// whose raw entry is > G is listed, and every other element ends at most at
+// C = softcap(value of G). The merge caps and penalises the listed entries
+// above G (with a penalty below 1, also every listed penalised entry), takes
+// their top k by final value into sh.top[0, nt) and returns true when that is
+// certified to be the row's top k: the k-th final value is above C (so no
+// element outside can reach it or tie with it), or every chunk listed
+// everything. Otherwise returns false (a chunk held more of the top k than it
+// listed, or a tie at the bound): the caller falls back to merge_all_lists.
+__device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, const RowCtx& rc, uint32_t k,
+                                              uint32_t stride, uint32_t& nt) {
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const int wave = tid >> 6;
+    if (tid < 32) sh.exp_tab[tid] = exp2_table(static_cast<uint32_t>(tid));  // in flight with the slots
+    constexpr int kPer = kSlotWords / kBlock;
+    uint64_t w[kPer];
+    uint32_t wp[kPer], wc[kPer];
+    // The largest guarantee, folded in by every chunk before its ticket.
+    const uint64_t gam_max = load_shared(&a.row_gmax[2 * rc.row]);
+    load_slots(a, sh, rc.row, stride, w, wp, wc);
+    __syncthreads();
+    const bool bounded = gam_max != 0ull && gam_max != kGuaranteeFailed;
+    const bool pen_all = rc.pen && !(rc.r >= 1.0f);
+
+    // The entries above the largest guarantee, staged in per-wave segments.
+    uint64_t* seg = sh.stage + wave * kSeg;
     {
-        const int wave = tid >> 6;
-        uint64_t* seg = sh.stage + wave * kSeg;
         uint32_t woff = 0;  // <= kPer * 64 = kSeg
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const bool c = wp[i] != 0u && w[i] != 0ull && w[i] >= gam_max;
+            const bool c = slot_entry(sh, wp[i], wc[i]) && (w[i] > gam_max || (pen_all && raw_entry_pen(w[i])));
             const uint64_t mk = __ballot(c);
             if (c) seg[woff + lanes_below(mk)] = w[i];
             woff += static_cast<uint32_t>(__popcll(mk));
@@ -1307,31 +1548,48 @@ __device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, i
     }
     __syncthreads();
     uint32_t cnt[kBlock / 64];
+    uint32_t nsel = 0;
 #pragma unroll
     for (int v = 0; v < kBlock / 64; ++v) {
         cnt[v] = sh.u32[kSegCount + v];
         nsel += cnt[v];
     }
-    if (nsel >= k && nsel <= static_cast<uint32_t>(kBlock)) {
-        seg_rank_top(sh.stage, cnt, nsel, k, sh.top);
-        nt = k;
-        return true;
-    }
-    if (nsel >= k) {
-        seg_gather(sh.stage, cnt, nsel);
-        {
-            // Cut to the entries whose value key reaches a lower bound on the
-            // k-th largest one (two radix digits), so the sort sees fewer.
-            constexpr int kPerS = kStage / kBlock;
-            uint64_t e[kPerS];
-#pragma unroll
-            for (int q = 0; q < kPerS; ++q) {
-                const uint32_t i = static_cast<uint32_t>(q * kBlock + tid);
-                e[q] = i < nsel ? sh.stage[i] : 0ull;
+    // Final values in place, each wave over its own segment; wave 0 caps the
+    // largest guarantee's raw value as one more item of the same pass.
+    {
+        const uint32_t n = cnt[wave] + ((wave == 0 && bounded) ? 1u : 0u);
+        for (uint32_t i = lane; i < n; i += 64) {
+            const bool real = i < cnt[wave];
+            const uint64_t e = real ? seg[i] : gam_max;
+            float f = softcap(key_value(static_cast<uint32_t>(e >> 32)), rc.cap);
+            if (real) {
+                if (rc.pen && raw_entry_pen(e)) f = penalize(f, rc.r);
+                seg[i] = composite(order_key(f), raw_entry_index(e));
+            } else {
+                sh.u32[16] = order_key(f);
             }
+        }
+    }
+    __syncthreads();
+    // Top k by final value, sorted. Few entries: rank by counting. More: a
+    // radix lower bound on the k-th value key (one digit when that leaves
+    // few) cuts them to about k first.
+    if (nsel <= kRankDirect) {
+        seg_rank_top(sh.stage, cnt, nsel, k, sh.top);
+        nt = min(nsel, k);
+    } else {
+        constexpr int kPerW = kSeg / 64;
+        uint64_t e[kPerW];
+#pragma unroll
+        for (int q = 0; q < kPerW; ++q) {
+            const uint32_t i = static_cast<uint32_t>(q * 64 + lane);
+            e[q] = i < cnt[wave] ? seg[i] : 0ull;
+        }
+        uint32_t kk = 0u;  // keep entries whose value key is >= kk
+        if (nsel > k) {
             uint32_t kmin = 0xffffffffu, kmax = 0u;
 #pragma unroll
-            for (int q = 0; q < kPerS; ++q)
+            for (int q = 0; q < kPerW; ++q)
                 if (e[q] != 0ull) {
                     kmin = min(kmin, composite_key(e[q]));
                     kmax = max(kmax, composite_key(e[q]));
@@ -1339,45 +1597,138 @@ __device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, i
             kmin = wave_min(kmin);
             kmax = wave_max(kmax);
             if (lane == 0) {
-                sh.u32[8 + (tid >> 6)] = kmax;
-                sh.u32[12 + (tid >> 6)] = kmin;
+                sh.u32[8 + wave] = kmax;
+                sh.u32[12 + wave] = kmin;
             }
             __syncthreads();
             const uint32_t bmax = max(max(sh.u32[8], sh.u32[9]), max(sh.u32[10], sh.u32[11]));
             const uint32_t bmin = min(min(sh.u32[12], sh.u32[13]), min(sh.u32[14], sh.u32[15]));
-            const uint32_t kk = block_kth(bmin, bmax, k,
-                                          [&](auto&& f) {
+            kk = block_kth(bmin, bmax, k,
+                           [&](auto&& f) {
 #pragma unroll
-                                              for (int q = 0; q < kPerS; ++q)
-                                                  if (e[q] != 0ull) f(composite_key(e[q]));
-                                          },
-                                          sh);
-            uint32_t cnt2 = 0;
-#pragma unroll
-            for (int q = 0; q < kPerS; ++q) cnt2 += (e[q] != 0ull && composite_key(e[q]) >= kk) ? 1u : 0u;
-            uint32_t pos = block_excl_scan(cnt2, nsel, sh);
-#pragma unroll
-            for (int q = 0; q < kPerS; ++q)
-                if (e[q] != 0ull && composite_key(e[q]) >= kk) sh.stage[pos++] = e[q];
-            __syncthreads();
+                               for (int q = 0; q < kPerW; ++q)
+                                   if (e[q] != 0ull) f(composite_key(e[q]));
+                           },
+                           sh, 2u * k + 32u);
         }
+        uint32_t c2 = 0;
+#pragma unroll
+        for (int q = 0; q < kPerW; ++q) c2 += (e[q] != 0ull && composite_key(e[q]) >= kk) ? 1u : 0u;
+        // (The scan's barriers also order every wave's reads of its segment
+        // before the writes below.)
+        uint32_t pos = block_excl_scan(c2, nsel, sh);
+#pragma unroll
+        for (int q = 0; q < kPerW; ++q)
+            if (e[q] != 0ull && composite_key(e[q]) >= kk) sh.stage[pos++] = e[q];
+        __syncthreads();
         nt = select_top(sh.stage, nsel, k, sh.top);
-        return true;
     }
-    // Everything listed.
-    uint32_t nall;
-    {
-        uint32_t cnt = 0;
+    if (gam_max == 0ull) return true;  // every chunk listed everything
+    if (!bounded) return false;
+    return nt >= k && composite_key(sh.top[k - 1]) > sh.u32[16];
+}
+
+// Words per thread of the small-row merge: rows whose slot area (cpr *
+// stride words) fits kBlock * kSmallWords take merge_collect_small.
+constexpr int kSmallWords = 4;
+
+// Merge, first part, for rows with small slot areas. Same contract as
+// merge_collect, fewer steps, and two levels. At level j1 (then m) with G the
+// largest j1-th (m-th) list entry of the row's chunks, S = the listed entries
+// above G (with a penalty below 1, also every listed penalised entry) holds
+// every element whose raw entry is above G; every other element ends at most
+// at C = softcap(value of G). S is compacted into sh.stage, capped and
+// penalised in one balanced pass and ranked into sh.top; the top k is
+// certified when its k-th final value is above C. Block-uniform.
+__device__ __forceinline__ bool merge_collect_small(const DevArgs& a, SelShared& sh, const RowCtx& rc, uint32_t k,
+                                                    uint32_t stride, uint32_t& nt) {
+    const int tid = threadIdx.x;
+    if (tid < 32) sh.exp_tab[tid] = exp2_table(static_cast<uint32_t>(tid));  // in flight with the slots
+    const bool pen_all = rc.pen && !(rc.r >= 1.0f);
+    uint64_t w[kSmallWords];
+    uint32_t wp[kSmallWords], wc[kSmallWords];
+    // The row's largest guarantees at level j1 and at level m, folded in by
+    // every chunk before its ticket.
+    const uint64_t gam_lv[2] = {load_shared(&a.row_gmax[2 * rc.row + 1]), load_shared(&a.row_gmax[2 * rc.row])};
+    load_slots(a, sh, rc.row, stride, w, wp, wc);
+    __syncthreads();
+    bool ent[kSmallWords];
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) cnt += (wp[i] != 0u && w[i] != 0ull) ? 1u : 0u;
-        uint32_t pos = block_excl_scan(cnt, nall, sh);
+    for (int i = 0; i < kSmallWords; ++i) ent[i] = slot_entry(sh, wp[i], wc[i]);
+    for (int lv = 0; lv < 2; ++lv) {
+        const uint64_t gam = gam_lv[lv];
+        if (gam == kGuaranteeFailed) return false;
+        if (lv == 1 && gam == gam_lv[0]) break;  // the same bound again
+        const bool bounded = gam != 0ull;
+        uint32_t in = 0u, cnt = 0u;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i)
-            if (wp[i] != 0u && w[i] != 0ull) sh.stage[pos++] = w[i];
+        for (int i = 0; i < kSmallWords; ++i) {
+            const bool c = ent[i] && (w[i] > gam || (pen_all && raw_entry_pen(w[i])));
+            in |= static_cast<uint32_t>(c) << i;
+            cnt += c ? 1u : 0u;
+        }
+        uint32_t n;
+        uint32_t pos = block_excl_scan(cnt, n, sh);
+#pragma unroll
+        for (int i = 0; i < kSmallWords; ++i)
+            if ((in >> i) & 1u) sh.stage[pos++] = w[i];
+        __syncthreads();
+        // Final values in place; item n caps G's raw value.
+        const uint32_t items = n + (bounded ? 1u : 0u);
+        for (uint32_t i = tid; i < items; i += kBlock) {
+            const bool real = i < n;
+            const uint64_t e = real ? sh.stage[i] : gam;
+            float f = softcap(key_value(static_cast<uint32_t>(e >> 32)), rc.cap);
+            if (real) {
+                if (rc.pen && raw_entry_pen(e)) f = penalize(f, rc.r);
+                sh.stage[i] = composite(order_key(f), raw_entry_index(e));
+            } else {
+                sh.u32[16] = order_key(f);
+            }
+        }
+        __syncthreads();
+        nt = n <= static_cast<uint32_t>(kBlock) ? rank_top_hi(sh, sh.stage, n, k, sh.top)
+                                               : select_top(sh.stage, n, k, sh.top);
+        if (!bounded) return true;  // every chunk listed everything
+        if (nt >= k && composite_key(sh.top[k - 1]) > sh.u32[16]) return true;
+    }
+    return false;
+}
+
+// Merge fallback: the top k of every listed entry by final value into
+// sh.top[0, nt), and in sh.gam[c] a bound for chunk c: a composite key that
+// no element the chunk left out can exceed (0: it listed everything;
+// kGuaranteeFailed: it must be rescanned). Block-uniform.
+__device__ __forceinline__ void merge_all_lists(const DevArgs& a, SelShared& sh, const RowCtx& rc, uint32_t k,
+                                                uint32_t stride, uint32_t& nt) {
+    const int tid = threadIdx.x;
+    constexpr int kPer = kSlotWords / kBlock;
+    uint64_t w[kPer];
+    uint32_t wp[kPer], wc[kPer];
+    load_slots(a, sh, rc.row, stride, w, wp, wc);
+    __syncthreads();
+    bool ent[kPer];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        ent[i] = slot_entry(sh, wp[i], wc[i]);
+        cnt += ent[i] ? 1u : 0u;
+    }
+    uint32_t n;
+    uint32_t pos = block_excl_scan(cnt, n, sh);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (ent[i]) sh.stage[pos++] = w[i];
+    __syncthreads();
+    for (uint32_t i = tid; i < n; i += kBlock) sh.stage[i] = final_of(sh.stage[i], rc);
+    for (int c = tid; c < a.cpr; c += kBlock) {
+        const uint64_t g = sh.gam[c];
+        if (g != 0ull && g != kGuaranteeFailed)
+            sh.gam[c] = (static_cast<uint64_t>(order_key(softcap(key_value(static_cast<uint32_t>(g >> 32)), rc.cap)))
+                         << 32) | 0xffffffffull;
     }
     __syncthreads();
-    nt = select_top(sh.stage, nall, k, sh.top);
-    return false;
+    nt = select_top(sh.stage, n, k, sh.top);
 }
 
 // Next chunk at or after c whose guarantee is above the running k-th key
@@ -1530,8 +1881,10 @@ __device__ __forceinline__ uint32_t rescan_chunk(const RowCtx& rc, int c, uint32
     return n_out;
 }
 
+// Four waves per SIMD (at most 128 VGPRs): with 4 workgroups per CU, the
+// 1024 workgroups of a 64-row batch are all resident from the start.
 template <typename T, int EPT>
-__global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
+__global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
     constexpr int CHUNK = kBlock * EPT;
     __shared__ uint32_t s_pbits[CHUNK / 32];
     __shared__ SelShared sh;
@@ -1566,18 +1919,35 @@ __global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
     rc.pen = rc.H > 0 && !(rc.r == 1.0f);
     rc.cap = p.softcap;
     const uint32_t m = spec_m(k, a.cpr, CHUNK);
+    // Slot stride: room for about twice the usual candidate count (words
+    // past a chunk's count are not read); with a penalty below 1 the row's
+    // slot area split evenly, so a chunk can append its penalised tokens.
+    const bool pen_all = rc.pen && !(rc.r >= 1.0f);
+    const uint32_t stride = pen_all ? static_cast<uint32_t>(kSlotWords / a.cpr)
+                                    : min(static_cast<uint32_t>(kSlotWords / a.cpr), 2u * m + 24u);
+    uint64_t* slot = a.slots + static_cast<int64_t>(row) * kSlotWords + static_cast<int64_t>(chunk) * stride;
 
-    uint32_t n_out;
+    uint32_t n_top, n_out;
     bool ok;
-    const uint64_t gamma = chunk_topm<T, EPT>(rc, chunk * CHUNK, m, s_pbits, sh, n_out, ok);
+    const uint64_t gamma = chunk_topm<T, EPT>(rc, chunk * CHUNK, m, s_pbits, sh, slot, stride, n_top, n_out, ok);
 
-    // Publish [guarantee, list padded with zeros], wait for the stores, then
-    // one ticket per workgroup; the last workgroup of the row merges.
-    uint64_t* slot = a.slots + static_cast<int64_t>(row) * kSlotWords + static_cast<int64_t>(chunk) * (m + 1);
-    for (uint32_t i = tid; i <= m; i += kBlock) {
-        const uint64_t v = i == 0 ? gamma : (i - 1 < n_out ? sh.list[i - 1] : 0ull);
-        store_shared(&slot[i], v);
+    // Publish [guarantee, count, entries] (candidate lists and appended
+    // penalised entries are already written) and fold the guarantee into the
+    // row's maximum, wait for the stores, then one ticket per workgroup; the
+    // last workgroup of the row merges.
+    if (tid == 0) {
+        // Row maxima of the level-m guarantee and of the level-j1 one (the
+        // j1-th entry: every element outside the first j1 is below it).
+        const uint32_t j1 = spec_level1(k, a.cpr, m);
+        const uint64_t g1 = gamma == kGuaranteeFailed ? kGuaranteeFailed : (n_top >= j1 ? sh.list[j1 - 1] : 0ull);
+        if (gamma != 0ull)
+            (void)__hip_atomic_fetch_max(&a.row_gmax[2 * row], gamma, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (g1 != 0ull)
+            (void)__hip_atomic_fetch_max(&a.row_gmax[2 * row + 1], g1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        store_shared(&slot[0], gamma);
+        store_shared(&slot[1], static_cast<uint64_t>(min(n_out, stride - 2u)));
     }
+    for (uint32_t i = tid; i < n_top; i += kBlock) store_shared(&slot[2u + i], sh.list[i]);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -1593,9 +1963,13 @@ __global__ __launch_bounds__(kBlock) void select_kernel(DevArgs a) {
     const float u = greedy ? 0.0f : a.uniforms[row];
     const float x0 = greedy ? load_one(static_cast<const T*>(rc.rowp), 0) : 0.0f;
     uint32_t nt;
-    if (!merge_collect(a, sh, row, k, m, nt)) {
-        // Fallback: chunks whose guarantee is above the k-th largest listed
-        // key may hold more of the row's top-k than they listed.
+    const bool collected = static_cast<uint32_t>(a.cpr) * stride <= static_cast<uint32_t>(kBlock * kSmallWords)
+                               ? merge_collect_small(a, sh, rc, k, stride, nt)
+                               : merge_collect(a, sh, rc, k, stride, nt);
+    if (!collected) {
+        // Fallback: every listed entry with its final value, then an exact
+        // rescan of each chunk whose bound reaches the k-th largest so far.
+        merge_all_lists(a, sh, rc, k, stride, nt);
         for (int c = next_rescan(sh, 0, a.cpr, nt, k); c >= 0; c = next_rescan(sh, c + 1, a.cpr, nt, k)) {
             bool rok;
             const uint32_t nl = rescan_chunk<T, EPT>(rc, c, k, s_pbits, sh, rok);
