@@ -1425,6 +1425,97 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, uint32_t keff, 
 }
 
 
+// generation.cpp:103-126 for at most 64 probabilities in one wave's
+// registers (lane j holds p_j, j < keff; none NaN, so they are
+// non-increasing). The sequential fp32 sums are fully unrolled in blocks of
+// 16 steps: every lane runs the same chain with p_j broadcast from lane j
+// (v_readlane, off the add chain), lane j keeps the sum after step j, and one
+// ballot per block finds the stop, with no replay and no per-step branch. The
+// double boundary sums come from a wave prefix sum when it is exact (every
+// term a multiple of 2^-52; the partial sums are below 2), else from a
+// sequential replay.
+__device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge_sample_params& p, float u,
+                                               uint32_t& pos_out, bool& near_out) {
+    const int lane = __lane_id();
+    const float p0 = readlane_f(pr, 0);
+    const float minimum = p0 * p.min_p;
+    // min-p: the first j >= 1 with p_j < minimum (checked before adding p_j).
+    uint32_t limit = keff;
+    if (minimum > 0.0f) {
+        const uint64_t h = __ballot(lane >= 1 && lane < static_cast<int>(keff) && pr < minimum);
+        if (h) limit = static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(h)) - 1);
+    }
+    // top-p: the first j in [1, limit) with cum_j >= top_p. Entries past the
+    // limit add exact zeros.
+    const float pl = lane < static_cast<int>(limit) ? pr : 0.0f;
+    float cum = 0.0f, mass = 0.0f, cl = 0.0f;
+    uint32_t keep = limit;
+    bool stopped = false;
+    static_for<0, 4>([&](auto B) {
+        constexpr int b = decltype(B)::value * 16;
+        if (stopped || static_cast<uint32_t>(b) >= limit) return;
+        static_for<0, 16>([&](auto J) {
+            constexpr int j = b + decltype(J)::value;
+            cum = cum + readlane_f(pl, j);
+            cl = lane == j ? cum : cl;
+        });
+        const uint64_t th = __ballot(lane >= b && lane < b + 16 && lane >= 1 && lane < static_cast<int>(limit) &&
+                                     cl >= p.top_p);
+        if (th) {
+            const int j = __ffsll(static_cast<unsigned long long>(th)) - 1;
+            keep = static_cast<uint32_t>(j) + 1u;
+            mass = readlane_f(cl, j);
+            stopped = true;
+        }
+    });
+    if (!stopped) mass = cum;
+    // Draw: uniform_real_distribution(0, mass), then the subtract walk; the
+    // fall-through returns entry keep - 1 (generation.cpp:126).
+    const float choice0 = u * mass + 0.0f;
+    const float pw = lane < static_cast<int>(keep) ? pr : 0.0f;
+    float choice = choice0, chl = 0.0f;
+    uint32_t pos = keep - 1u;
+    bool found = false;
+    static_for<0, 4>([&](auto B) {
+        constexpr int b = decltype(B)::value * 16;
+        if (found || static_cast<uint32_t>(b) >= keep) return;
+        static_for<0, 16>([&](auto J) {
+            constexpr int j = b + decltype(J)::value;
+            choice = choice - readlane_f(pw, j);
+            chl = lane == j ? choice : chl;
+        });
+        const uint64_t hit = __ballot(lane >= b && lane < b + 16 && lane < static_cast<int>(keep) && chl <= 0.0f);
+        if (hit) {
+            pos = static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(hit)) - 1);
+            found = true;
+        }
+    });
+    // Boundary sums c_at = sum_{i <= pos} (double)p_i in order, c_before up to
+    // pos - 1.
+    double c_before = 0.0, c_at = 0.0;
+    {
+        const float pc = lane <= static_cast<int>(pos) ? pr : 0.0f;
+        const int lsb = pc > 0.0f ? lsb_exponent(pc) : INT_MAX;
+        if (wave_min_i(lsb) >= -52) {
+            const double incl = wave_incl_f64(static_cast<double>(pc));
+            c_at = readlane_d(incl, static_cast<int>(pos));
+            c_before = pos > 0 ? readlane_d(incl, static_cast<int>(pos) - 1) : 0.0;
+        } else {
+            double dc = 0.0;
+            for (uint32_t i = 0; i <= pos; ++i) {
+                c_before = dc;
+                dc = dc + static_cast<double>(readlane_f(pc, static_cast<int>(i)));
+            }
+            c_at = dc;
+        }
+    }
+    bool near = false;
+    if (pos > 0 && fabs(static_cast<double>(choice0) - c_before) < 1e-6) near = true;
+    if (pos + 1 < keep && fabs(static_cast<double>(choice0) - c_at) < 1e-6) near = true;
+    pos_out = pos;
+    near_out = near;
+}
+
 // sh.top[0, nt) := the largest k distinct keys of sh.top[0, nt) and
 // sh.list[0, nl), sorted descending. Returns the new nt. Block-uniform.
 __device__ __forceinline__ uint32_t absorb_list(SelShared& sh, uint32_t nt, uint32_t nl, uint32_t k) {
@@ -1865,7 +1956,8 @@ __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, co
     };
     uint32_t pos;
     bool near;
-    if (!any_nan) scan_and_walk_fast(seg_prob, keff, p, u, pos, near);
+    if (!any_nan && one_wave) scan_walk_wave(pr_reg, keff, p, u, pos, near);
+    else if (!any_nan) scan_and_walk_fast(seg_prob, keff, p, u, pos, near);
     else scan_and_walk(seg_prob, keff, p, u, pos, near);
     const float ppos = one_wave ? readlane_f(pr_reg, static_cast<int>(pos)) : prob[pos];
     if (lane == 0)
