@@ -1982,8 +1982,13 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
     __shared__ SelShared sh;
 
     const int tid = threadIdx.x;
-    const int row = blockIdx.x / a.cpr;
-    const int chunk = blockIdx.x - row * a.cpr;
+    // Workgroups are dispatched to the 8 XCDs round-robin (block b to XCD
+    // b % 8). When the rows split evenly, XCD x takes whole rows: the row's
+    // lists then meet in one XCD's L2.
+    int bid = static_cast<int>(blockIdx.x);
+    if ((a.rows & 7) == 0) bid = (bid & 7) * static_cast<int>(gridDim.x >> 3) + (bid >> 3);
+    const int row = bid / a.cpr;
+    const int chunk = bid - row * a.cpr;
     const int V = a.vocab;
     const ge_sample_params p = row_params(a, row);
     const bool greedy = p.temperature <= 0.0f;  // generation.cpp:66
