@@ -117,30 +117,78 @@ __host__ __device__ inline float expm1f_fdlibm(float x) {
     return y;
 }
 
-// fdlibm tanhf.
+// fdlibm expm1f restricted to the arguments tanhf gives it, y = +-2|x| with
+// 2^-55 <= |x| < 22, and written without branches: every case of
+// expm1f_fdlibm is computed and the result selected, so a wave whose lanes
+// take different cases runs the code once. The operations and their order
+// are those of expm1f_fdlibm case by case:
+//   * the argument reduction with k = +-1 (|y| in (ln2/2, 3 ln2/2)) uses
+//     hi = y -+ ln2_hi, lo = +-ln2_lo; the general form y - t*ln2_hi, t*ln2_lo
+//     with t = k = +-1 computes the same values (t*ln2_hi and t*ln2_lo are
+//     exact), and with t = 0 it leaves y and c = 0 as the k = 0 case does;
+//   * |y| < 2^-25 returns y; the overflow and y <= -27 ln2 cases cannot occur.
+__host__ __device__ inline float expm1f_tanh(float y) {
+    const float one = 1.0f;
+    const float ln2_hi = u2f(0x3f317180u);
+    const float ln2_lo = u2f(0x3717f7d1u);
+    const float invln2 = u2f(0x3fb8aa3bu);
+    const float Q1 = u2f(0xbd088889u), Q2 = u2f(0x3ad00d01u), Q3 = u2f(0xb8a670cdu),
+                Q4 = u2f(0x36867e54u), Q5 = u2f(0xb457edbbu);
+    const uint32_t hy = f2u(y);
+    const bool neg = (hy & 0x80000000u) != 0u;
+    const uint32_t hx = hy & 0x7fffffffu;
+    const int32_t kg = static_cast<int32_t>(invln2 * y + (neg ? -0.5f : 0.5f));
+    const int32_t k = hx <= 0x3eb17218u ? 0 : (hx < 0x3F851592u ? (neg ? -1 : 1) : kg);
+    const float t = static_cast<float>(k);
+    const float hi = y - t * ln2_hi;
+    const float lo = t * ln2_lo;
+    const float x = hi - lo;
+    const float c = (hi - x) - lo;
+    const float hfx = 0.5f * x;
+    const float hxs = x * hfx;
+    const float r1 = one + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+    const float tt = 3.0f - r1 * hfx;
+    const float e0 = hxs * ((r1 - tt) / (6.0f - x * tt));
+    const float res0 = x - (x * e0 - hxs);                    // k == 0
+    const float e = (x * (e0 - c) - c) - hxs;
+    const float resm1 = 0.5f * (x - e) - 0.5f;                // k == -1
+    const float resp1 = x < -0.25f ? -2.0f * (e - (x + 0.5f)) : one + 2.0f * (x - e);  // k == 1
+    const uint32_t k23 = static_cast<uint32_t>(k) << 23;
+    const float yb = u2f(f2u(one - (e - x)) + k23) - one;    // k <= -2 or k > 56
+    const int ks = k < 0 ? 0 : (k > 31 ? 31 : k);            // shift counts used only where valid
+    const float ys = u2f(f2u(u2f(0x3f800000u - (0x1000000u >> ks)) - (e - x)) + k23);  // 2 <= k < 23
+    const float yl = u2f(f2u((x - (e + u2f(static_cast<uint32_t>(0x7f - k) << 23))) + one) + k23);  // 23 <= k <= 56
+    float r = yl;
+    if (k < 23) r = ys;
+    if (k <= -2 || k > 56) r = yb;
+    if (k == 1) r = resp1;
+    if (k == -1) r = resm1;
+    if (k == 0) r = res0;
+    if (hx < 0x33000000u) r = y;                              // |y| < 2^-25
+    return r;
+}
+
+// fdlibm tanhf, with the two expm1f calls merged into one on a selected
+// argument and the two divisions into one on a selected numerator (the
+// quotient 2/(t+2) or -t/(t+2) is the same single rounding either way).
 __host__ __device__ inline float tanhf_fdlibm(float x) {
     const uint32_t jx = f2u(x);
     const uint32_t ix = jx & 0x7fffffffu;
-    float t, z;
     if (ix >= 0x7f800000u) {          // inf or NaN
         if ((jx >> 31) == 0) return 1.0f / x + 1.0f;
         return 1.0f / x - 1.0f;
     }
-    if (ix < 0x41b00000u) {           // |x| < 22
-        if (ix == 0) return x;
-        if (ix < 0x24000000u) return x * (1.0f + x);  // |x| < 2^-55
-        const float ax = u2f(ix);
-        if (ix >= 0x3f800000u) {      // |x| >= 1
-            t = expm1f_fdlibm(2.0f * ax);
-            z = 1.0f - 2.0f / (t + 2.0f);
-        } else {
-            t = expm1f_fdlibm(-2.0f * ax);
-            z = -t / (t + 2.0f);
-        }
-    } else {
-        z = 1.0f - 1.0e-30f;          // +-1
-    }
-    return (jx >> 31) ? -z : z;
+    // |x| >= 22 returns +-1 below; its expm1 argument is replaced by one in
+    // range (the value is discarded) so the conversions stay defined.
+    const float ax = ix >= 0x41b00000u ? 1.0f : u2f(ix);
+    const bool big = ax >= 1.0f;                              // |x| >= 1
+    const float t = expm1f_tanh(big ? 2.0f * ax : -2.0f * ax);
+    const float q = (big ? 2.0f : -t) / (t + 2.0f);
+    float z = big ? 1.0f - q : q;
+    if (ix >= 0x41b00000u) z = 1.0f - 1.0e-30f;               // |x| >= 22: +-1
+    z = (jx >> 31) ? -z : z;
+    if (ix < 0x24000000u) z = x * (1.0f + x);                 // |x| < 2^-55 (and +-0)
+    return z;
 }
 
 // 2^(i/32) nearest double, minus (i << 47) in the bit pattern.
