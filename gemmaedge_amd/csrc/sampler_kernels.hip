@@ -1206,6 +1206,18 @@ __device__ __forceinline__ void write_row(const DevArgs& a, int row, int32_t tok
     a.row_gmax[2 * row + 1] = 0ull;
 }
 
+// The 16 floats p[0, 16) (16-byte aligned, in LDS) in every lane: four
+// broadcast 16-byte reads issued together. The sequential chains add them as
+// VGPR operands, so no step waits on a v_readlane.
+struct F16 {
+    float v[16];
+};
+__device__ __forceinline__ F16 lds16(const float* p) {
+    const float4* q = reinterpret_cast<const float4*>(p);
+    const float4 a = q[0], b = q[1], c = q[2], d = q[3];
+    return F16{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w}};
+}
+
 // generation.cpp:103-126 on probabilities sorted by value desc / index asc,
 // evaluated by one whole wave, for any values (NaN included). seg_prob(g)
 // returns this lane's probability of entry g * 64 + lane (0 past keff). Every
@@ -1303,8 +1315,9 @@ __device__ __forceinline__ void scan_and_walk(P&& seg_prob, uint32_t keff, const
 // seg_prob(g) returns this lane's probability of entry g * 64 + lane (any
 // finite value past keff; those entries are masked here).
 template <typename P>
-__device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, uint32_t keff, const ge_sample_params& p,
-                                                   float u, uint32_t& pos_out, bool& near_out) {
+__device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, const float* probs, uint32_t keff,
+                                                   const ge_sample_params& p, float u, uint32_t& pos_out,
+                                                   bool& near_out) {
     const int lane = __lane_id();
     const float p0 = readlane_f(seg_prob(0u), 0);
     const float minimum = p0 * p.min_p;
@@ -1322,9 +1335,10 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, uint32_t keff, 
         }
     }
     // top-p: first j >= 1, j < limit, with cum_j >= top_p. The chain runs in
-    // sub-blocks of 16 plain adds; cum is non-decreasing, so the stop lies in
-    // the first sub-block that ends at or above top_p, which is then replayed
-    // step by step from its starting value (same adds, same bits).
+    // blocks of 16 plain adds, fully unrolled; cum is non-decreasing, so the
+    // stop lies in the first block that ends at or above top_p, which is then
+    // replayed from its starting value (same adds, same bits) with lane j
+    // keeping the sum after step j, and one ballot finds it.
     float cum = 0.0f;
     float mass = 0.0f;
     uint32_t keep = limit;
@@ -1332,27 +1346,36 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, uint32_t keff, 
     for (uint32_t g = 0; g * 64 < limit && !stopped; ++g) {
         const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
         const float pl = idx < limit ? seg_prob(g) : 0.0f;
-        for (int q = 0; q < 64 && !stopped; q += 16) {
+        static_for<0, 4>([&](auto B) {
+            constexpr int b = decltype(B)::value * 16;
+            if (stopped) return;
             const float before = cum;
-            static_for<0, 16>([&](auto J) { cum = cum + readlane_f(pl, q + J); });
+            if (g * 64 + b + 16 <= limit) {
+                const F16 q = lds16(probs + g * 64 + b);  // whole block below the limit
+                static_for<0, 16>([&](auto J) { cum = cum + q.v[decltype(J)::value]; });
+            } else {
+                static_for<0, 16>([&](auto J) { cum = cum + readlane_f(pl, b + decltype(J)::value); });
+            }
             if (cum >= p.top_p) {
-                float c = before;
-                for (int i = 0; i < 16; ++i) {
-                    const uint32_t j = g * 64 + static_cast<uint32_t>(q + i);
-                    c = c + readlane_f(pl, q + i);
-                    if (j >= 1 && j < limit && c >= p.top_p) {
-                        keep = j + 1;
-                        mass = c;
-                        stopped = true;
-                        break;
-                    }
+                float c = before, cl = 0.0f;
+                static_for<0, 16>([&](auto J) {
+                    constexpr int j = b + decltype(J)::value;
+                    c = c + readlane_f(pl, j);
+                    cl = lane == j ? c : cl;
+                });
+                const uint64_t th = __ballot(lane >= b && lane < b + 16 && idx >= 1 && idx < limit && cl >= p.top_p);
+                if (th) {
+                    const int j = __ffsll(static_cast<unsigned long long>(th)) - 1;
+                    keep = g * 64 + static_cast<uint32_t>(j) + 1u;
+                    mass = readlane_f(cl, j);
+                    stopped = true;
                 }
             }
-        }
+        });
     }
     if (!stopped) mass = cum;  // min-p cut or all keff kept
     // Draw: uniform_real_distribution(0, mass), then the subtract walk
-    // (choice is non-increasing: the same sub-block search).
+    // (choice is non-increasing: the same block search).
     const float choice0 = u * mass + 0.0f;
     float choice = choice0;
     uint32_t pos = keep - 1;  // fallthrough return, generation.cpp:126
@@ -1360,22 +1383,30 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, uint32_t keff, 
     for (uint32_t g = 0; g * 64 < keep && !found; ++g) {
         const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
         const float pl = idx < keep ? seg_prob(g) : 0.0f;
-        for (int q = 0; q < 64 && !found; q += 16) {
+        static_for<0, 4>([&](auto B) {
+            constexpr int b = decltype(B)::value * 16;
+            if (found) return;
             const float before = choice;
-            static_for<0, 16>([&](auto J) { choice = choice - readlane_f(pl, q + J); });
+            if (g * 64 + b + 16 <= keep) {
+                const F16 q = lds16(probs + g * 64 + b);
+                static_for<0, 16>([&](auto J) { choice = choice - q.v[decltype(J)::value]; });
+            } else {
+                static_for<0, 16>([&](auto J) { choice = choice - readlane_f(pl, b + decltype(J)::value); });
+            }
             if (choice <= 0.0f) {
-                float c = before;
-                for (int i = 0; i < 16; ++i) {
-                    const uint32_t j = g * 64 + static_cast<uint32_t>(q + i);
-                    c = c - readlane_f(pl, q + i);
-                    if (j < keep && c <= 0.0f) {
-                        pos = j;
-                        found = true;
-                        break;
-                    }
+                float c = before, cl = 0.0f;
+                static_for<0, 16>([&](auto J) {
+                    constexpr int j = b + decltype(J)::value;
+                    c = c - readlane_f(pl, j);
+                    cl = lane == j ? c : cl;
+                });
+                const uint64_t hit = __ballot(lane >= b && lane < b + 16 && idx < keep && cl <= 0.0f);
+                if (hit) {
+                    pos = g * 64 + static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(hit)) - 1);
+                    found = true;
                 }
             }
-        }
+        });
     }
     // The reference's boundary sums: c_at = sum_{i <= pos} (double)p_i in
     // order, c_before the same up to pos - 1. A wave prefix sum gives them
@@ -1435,7 +1466,7 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, uint32_t keff, 
 // term a multiple of 2^-52; the partial sums are below 2), else from a
 // sequential replay.
 __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge_sample_params& p, float u,
-                                               uint32_t& pos_out, bool& near_out) {
+                                               float* lds, uint32_t& pos_out, bool& near_out) {
     const int lane = __lane_id();
     const float p0 = readlane_f(pr, 0);
     const float minimum = p0 * p.min_p;
@@ -1448,15 +1479,18 @@ __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge
     // top-p: the first j in [1, limit) with cum_j >= top_p. Entries past the
     // limit add exact zeros.
     const float pl = lane < static_cast<int>(limit) ? pr : 0.0f;
+    lds[lane] = pl;  // lds[64, 128): the draw's copy
+    lds[64 + lane] = 0.0f;
     float cum = 0.0f, mass = 0.0f, cl = 0.0f;
     uint32_t keep = limit;
     bool stopped = false;
     static_for<0, 4>([&](auto B) {
         constexpr int b = decltype(B)::value * 16;
         if (stopped || static_cast<uint32_t>(b) >= limit) return;
+        const F16 q = lds16(lds + b);
         static_for<0, 16>([&](auto J) {
             constexpr int j = b + decltype(J)::value;
-            cum = cum + readlane_f(pl, j);
+            cum = cum + q.v[decltype(J)::value];
             cl = lane == j ? cum : cl;
         });
         const uint64_t th = __ballot(lane >= b && lane < b + 16 && lane >= 1 && lane < static_cast<int>(limit) &&
@@ -1472,16 +1506,17 @@ __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge
     // Draw: uniform_real_distribution(0, mass), then the subtract walk; the
     // fall-through returns entry keep - 1 (generation.cpp:126).
     const float choice0 = u * mass + 0.0f;
-    const float pw = lane < static_cast<int>(keep) ? pr : 0.0f;
+    lds[64 + lane] = lane < static_cast<int>(keep) ? pr : 0.0f;
     float choice = choice0, chl = 0.0f;
     uint32_t pos = keep - 1u;
     bool found = false;
     static_for<0, 4>([&](auto B) {
         constexpr int b = decltype(B)::value * 16;
         if (found || static_cast<uint32_t>(b) >= keep) return;
+        const F16 q = lds16(lds + 64 + b);
         static_for<0, 16>([&](auto J) {
             constexpr int j = b + decltype(J)::value;
-            choice = choice - readlane_f(pw, j);
+            choice = choice - q.v[decltype(J)::value];
             chl = lane == j ? choice : chl;
         });
         const uint64_t hit = __ballot(lane >= b && lane < b + 16 && lane < static_cast<int>(keep) && chl <= 0.0f);
@@ -1956,8 +1991,8 @@ __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, co
     };
     uint32_t pos;
     bool near;
-    if (!any_nan && one_wave) scan_walk_wave(pr_reg, keff, p, u, pos, near);
-    else if (!any_nan) scan_and_walk_fast(seg_prob, keff, p, u, pos, near);
+    if (!any_nan && one_wave) scan_walk_wave(pr_reg, keff, p, u, prob, pos, near);
+    else if (!any_nan) scan_and_walk_fast(seg_prob, prob, keff, p, u, pos, near);
     else scan_and_walk(seg_prob, keff, p, u, pos, near);
     const float ppos = one_wave ? readlane_f(pr_reg, static_cast<int>(pos)) : prob[pos];
     if (lane == 0)
