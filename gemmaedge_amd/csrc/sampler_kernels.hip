@@ -112,6 +112,14 @@ __device__ __forceinline__ double readlane_d(double v, int i) {
     return u2d((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// Orders this wave's LDS accesses: LDS operations of one wave execute in
+// issue order, so a compiler-level barrier suffices.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Calls f(std::integral_constant<int, J>) for J = 0 .. N-1, in order.
 template <int J, int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -952,9 +960,10 @@ __device__ __forceinline__ void seg_gather(uint64_t* stage, const uint32_t (&cnt
 // tau (from the maxima of groups of logits). Every element >= tau is staged,
 // so the top m of the staged entries is the chunk's top m.
 template <typename T, int EPT>
-__device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_t m, uint32_t* pbits,
+__device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_t m, uint32_t j1, uint32_t* pbits,
                                                SelShared& sh, uint64_t* slot, uint32_t stride,
-                                               uint32_t& n_top, uint32_t& n_out, bool& ok) {
+                                               uint32_t& n_top, uint32_t& n_out, uint64_t& g1, bool& direct,
+                                               bool& ok) {
     constexpr int W = sizeof(T) == 4 ? 4 : 8;  // elements per 16-byte load
     constexpr int NV = EPT / W;                 // 16-byte loads per thread
     constexpr int NW = EPT * sizeof(T) / 4;     // 32-bit words per thread
@@ -969,6 +978,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     const int cend = min(c0 + CHUNK, rc.V);
     const bool pen_all = rc.pen && !(rc.r >= 1.0f);
     ok = true;
+    direct = false;
 
     // Slot s of this thread is element c0 + ((s / W) * kBlock + tid) * W + s % W.
     auto elem = [&](int s) { return c0 + ((s / W) * kBlock + tid) * W + (s % W); };
@@ -1096,7 +1106,11 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     }
     // tau <= kKeyNaN: fewer than m real logits in some wave; no pruning.
     const bool allpass = tau <= kKeyNaN;
-    if (allpass && cend - c0 > kStage) return chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
+    if (allpass && cend - c0 > kStage) {
+        const uint64_t gs = chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
+        g1 = gs == kGuaranteeFailed ? kGuaranteeFailed : (n_top >= j1 ? sh.list[j1 - 1] : 0ull);
+        return gs;
+    }
     const float floor_v = key_value(max(tau, kKeyNegInf));  // raw >= floor_v <=> key >= tau
 
     // Penalty bits of this thread's slots (bit s = slot s), read once: the W
@@ -1160,7 +1174,42 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     }
     if (seg_over) {
         // Massive ties or a loose bound: the exact routine.
-        return chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
+        const uint64_t gs = chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
+        g1 = gs == kGuaranteeFailed ? kGuaranteeFailed : (n_top >= j1 ? sh.list[j1 - 1] : 0ull);
+        return gs;
+    }
+    if (n_c <= 64u && !pen_all) {
+        // 5. The usual case: wave 0 ranks the candidates by counting (exact
+        //    64-bit keys read in pairs from LDS broadcasts, four pairs per
+        //    step) and writes the sorted top m straight to the slot; the
+        //    other waves go on to the ticket.
+        n_top = min(n_c, m);
+        n_out = n_top;
+        direct = true;
+        uint64_t g = 0ull;
+        g1 = 0ull;
+        if (wave == 0) {
+            const uint32_t b1 = cnt[0], b2 = b1 + cnt[1], b3 = b2 + cnt[2];
+            const uint32_t i = static_cast<uint32_t>(lane);
+            const int w = (i >= b1 ? 1 : 0) + (i >= b2 ? 1 : 0) + (i >= b3 ? 1 : 0);
+            const uint32_t base = w == 0 ? 0u : (w == 1 ? b1 : (w == 2 ? b2 : b3));
+            const uint64_t x = i < n_c ? sh.stage[w * kSeg + (i - base)] : 0ull;
+            sh.top[lane] = x;  // scratch (unused by the chunk phase); zeros past n_c
+            wave_lds_sync();
+            const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(sh.top);
+            uint32_t r = 0;
+            for (uint32_t j = 0; j < (n_c + 7u) / 8u; ++j) {
+                const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
+                r += (q0.x > x ? 1u : 0u) + (q0.y > x ? 1u : 0u) + (q1.x > x ? 1u : 0u) + (q1.y > x ? 1u : 0u);
+                r += (q2.x > x ? 1u : 0u) + (q2.y > x ? 1u : 0u) + (q3.x > x ? 1u : 0u) + (q3.y > x ? 1u : 0u);
+            }
+            if (i < n_c && r < m) store_shared(&slot[2u + r], x);
+            const uint64_t hm = __ballot(i < n_c && r == m - 1u);
+            const uint64_t hj = __ballot(i < n_c && r == j1 - 1u);
+            if (hm) g = wave::readlane64(x, __ffsll(static_cast<unsigned long long>(hm)) - 1);
+            if (hj) g1 = wave::readlane64(x, __ffsll(static_cast<unsigned long long>(hj)) - 1);
+        }
+        return g;  // meaningful in wave 0, which publishes it
     }
     // 5. The top m, sorted. Up to kBlock candidates: each wave moves its
     //    segment to its place in stage[0, n_c) (inside segment 0's area past
@@ -1187,6 +1236,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     // most m elements listed everything.
     const uint64_t g = n_top == m ? sh.list[m - 1] : 0ull;
     if (pen_all && n_c > m) n_out += append_penalised(sh, n_c, m, g, slot, stride, ok);
+    g1 = ok ? (n_top >= j1 ? sh.list[j1 - 1] : 0ull) : kGuaranteeFailed;
     return ok ? g : kGuaranteeFailed;
 }
 
@@ -2059,9 +2109,12 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
                                     : min(static_cast<uint32_t>(kSlotWords / a.cpr), 2u * m + 24u);
     uint64_t* slot = a.slots + static_cast<int64_t>(row) * kSlotWords + static_cast<int64_t>(chunk) * stride;
 
+    const uint32_t j1 = spec_level1(k, a.cpr, m);
     uint32_t n_top, n_out;
-    bool ok;
-    const uint64_t gamma = chunk_topm<T, EPT>(rc, chunk * CHUNK, m, s_pbits, sh, slot, stride, n_top, n_out, ok);
+    uint64_t g1;
+    bool direct, ok;
+    const uint64_t gamma = chunk_topm<T, EPT>(rc, chunk * CHUNK, m, j1, s_pbits, sh, slot, stride, n_top, n_out, g1,
+                                              direct, ok);
 
     // Publish [guarantee, count, entries] (candidate lists and appended
     // penalised entries are already written) and fold the guarantee into the
@@ -2070,8 +2123,6 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
     if (tid == 0) {
         // Row maxima of the level-m guarantee and of the level-j1 one (the
         // j1-th entry: every element outside the first j1 is below it).
-        const uint32_t j1 = spec_level1(k, a.cpr, m);
-        const uint64_t g1 = gamma == kGuaranteeFailed ? kGuaranteeFailed : (n_top >= j1 ? sh.list[j1 - 1] : 0ull);
         if (gamma != 0ull)
             (void)__hip_atomic_fetch_max(&a.row_gmax[2 * row], gamma, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (g1 != 0ull)
@@ -2079,7 +2130,8 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
         store_shared(&slot[0], gamma);
         store_shared(&slot[1], static_cast<uint64_t>(min(n_out, stride - 2u)));
     }
-    for (uint32_t i = tid; i < n_top; i += kBlock) store_shared(&slot[2u + i], sh.list[i]);
+    if (!direct)
+        for (uint32_t i = tid; i < n_top; i += kBlock) store_shared(&slot[2u + i], sh.list[i]);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
