@@ -1113,10 +1113,12 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     }
     const float floor_v = key_value(max(tau, kKeyNegInf));  // raw >= floor_v <=> key >= tau
 
-    // Penalty bits of this thread's slots (bit s = slot s), read once: the W
-    //    elements of a 16-byte group lie in one bitmap word.
+    // With a penalty below 1, the penalty bits of this thread's slots (bit s
+    //    = slot s) select candidates: read them once (the W elements of a
+    //    16-byte group lie in one bitmap word). Otherwise entries are staged
+    //    unmarked and the few candidates get their penalty flag afterwards.
     uint64_t pm = 0ull;
-    if (rc.pen) {
+    if (pen_all) {
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             const int off = (v * kBlock + tid) * W;  // element offset in the chunk
@@ -1141,6 +1143,13 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             }
             woff += static_cast<uint32_t>(__popcll(mk));
         }
+    };
+    // The penalty flag of an entry staged unmarked (bit 31 of the low word
+    // cleared for a penalised token).
+    const bool fix_pen = rc.pen && !pen_all;
+    auto mark_pen = [&](uint64_t x) -> uint64_t {
+        const uint32_t off = raw_entry_index(x) - static_cast<uint32_t>(c0);
+        return ((pbits[off >> 5] >> (off & 31)) & 1u) ? (x & ~0x80000000ull) : x;
     };
     if (allpass) {
 #pragma unroll
@@ -1193,7 +1202,8 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             const uint32_t i = static_cast<uint32_t>(lane);
             const int w = (i >= b1 ? 1 : 0) + (i >= b2 ? 1 : 0) + (i >= b3 ? 1 : 0);
             const uint32_t base = w == 0 ? 0u : (w == 1 ? b1 : (w == 2 ? b2 : b3));
-            const uint64_t x = i < n_c ? sh.stage[w * kSeg + (i - base)] : 0ull;
+            uint64_t x = i < n_c ? sh.stage[w * kSeg + (i - base)] : 0ull;
+            if (fix_pen && i < n_c) x = mark_pen(x);
             sh.top[lane] = x;  // scratch (unused by the chunk phase); zeros past n_c
             wave_lds_sync();
             const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(sh.top);
@@ -1221,13 +1231,17 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
 #pragma unroll
         for (int w = 0; w < kBlock / 64; ++w) base += w < wave ? cnt[w] : 0u;
         for (uint32_t i = lane; i < cnt[wave]; i += 64) {
-            const uint64_t x = seg[i];
+            const uint64_t x = fix_pen ? mark_pen(seg[i]) : seg[i];
             sh.stage[base + i] = x;
             sh.hist[base + i] = static_cast<uint32_t>(x >> 32);
         }
         for (uint32_t i = n_c + tid; i < ((n_c + 15u) & ~15u); i += kBlock) sh.hist[i] = 0u;
         n_top = rank_top_hi(sh, sh.stage, n_c, m, sh.list, true);
     } else {
+        if (fix_pen) {
+            for (uint32_t i = lane; i < cnt[wave]; i += 64) seg[i] = mark_pen(seg[i]);
+            __syncthreads();
+        }
         seg_gather(sh.stage, cnt, n_c);
         n_top = select_top(sh.stage, n_c, m, sh.list);
     }
