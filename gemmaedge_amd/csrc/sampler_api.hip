@@ -24,7 +24,6 @@ struct ge_sampler {
     int max_vocab;
     int max_history;
     uint32_t* tickets;
-    uint64_t* row_gmax;
     uint64_t* slots;
     // Full-order path (bf16 rows with k > kMaxTopK); allocated when max_vocab > kMaxTopK.
     uint64_t* fo_items;
@@ -128,10 +127,8 @@ int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, 
         if (e == hipSuccess) e = hipMalloc(p, bytes);
     };
     alloc(reinterpret_cast<void**>(&s->tickets), rows * sizeof(uint32_t));
-    alloc(reinterpret_cast<void**>(&s->row_gmax), rows * 2 * sizeof(uint64_t));
     alloc(reinterpret_cast<void**>(&s->slots), rows * ge::kSlotWords * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMemset(s->tickets, 0, rows * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(s->row_gmax, 0, rows * 2 * sizeof(uint64_t));
     if (max_vocab > ge::kMaxTopK) {
         s->fo_items_stride = ge::fo_items_stride(max_history);
         s->fo_extras_cap = max_history < ge::kFoExtrasCap ? (max_history > 0 ? max_history : 1) : ge::kFoExtrasCap;
@@ -161,7 +158,6 @@ void ge_sampler_destroy(ge_sampler* s) {
     if (!s) return;
     DeviceGuard guard(s->device);
     (void)hipFree(s->tickets);
-    (void)hipFree(s->row_gmax);
     (void)hipFree(s->slots);
     (void)hipFree(s->fo_items);
     (void)hipFree(s->fo_aux);
@@ -241,7 +237,6 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     a.probs = x.probs_out;
     a.flags = x.flags_out;
     a.tickets = s->tickets;
-    a.row_gmax = s->row_gmax;
     a.slots = s->slots;
     a.cpr = cpr;
     a.chunk_len = chunk_len;

@@ -36,7 +36,6 @@ struct DevArgs {
 
     // Workspace (allocated by ge_sampler_create, sized for max_rows x max_vocab).
     uint32_t* tickets;            // [max_rows]          zero between calls
-    uint64_t* row_gmax;           // [2 * max_rows]      largest chunk guarantees (level m, level j1); zero between calls
     uint64_t* slots;              // [max_rows * kSlotWords]  per chunk: guarantee + sorted top-m list
 
     // Launch geometry of the streaming pass.

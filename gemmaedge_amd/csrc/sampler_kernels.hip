@@ -960,10 +960,9 @@ __device__ __forceinline__ void seg_gather(uint64_t* stage, const uint32_t (&cnt
 // tau (from the maxima of groups of logits). Every element >= tau is staged,
 // so the top m of the staged entries is the chunk's top m.
 template <typename T, int EPT>
-__device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_t m, uint32_t j1, uint32_t* pbits,
+__device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_t m, uint32_t* pbits,
                                                SelShared& sh, uint64_t* slot, uint32_t stride,
-                                               uint32_t& n_top, uint32_t& n_out, uint64_t& g1, bool& direct,
-                                               bool& ok) {
+                                               uint32_t& n_top, uint32_t& n_out, bool& direct, bool& ok) {
     constexpr int W = sizeof(T) == 4 ? 4 : 8;  // elements per 16-byte load
     constexpr int NV = EPT / W;                 // 16-byte loads per thread
     constexpr int NW = EPT * sizeof(T) / 4;     // 32-bit words per thread
@@ -1107,9 +1106,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     // tau <= kKeyNaN: fewer than m real logits in some wave; no pruning.
     const bool allpass = tau <= kKeyNaN;
     if (allpass && cend - c0 > kStage) {
-        const uint64_t gs = chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
-        g1 = gs == kGuaranteeFailed ? kGuaranteeFailed : (n_top >= j1 ? sh.list[j1 - 1] : 0ull);
-        return gs;
+        return chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
     }
     const float floor_v = key_value(max(tau, kKeyNegInf));  // raw >= floor_v <=> key >= tau
 
@@ -1183,9 +1180,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     }
     if (seg_over) {
         // Massive ties or a loose bound: the exact routine.
-        const uint64_t gs = chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
-        g1 = gs == kGuaranteeFailed ? kGuaranteeFailed : (n_top >= j1 ? sh.list[j1 - 1] : 0ull);
-        return gs;
+        return chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
     }
     if (n_c <= 64u && !pen_all) {
         // 5. The usual case: wave 0 ranks the candidates by counting (exact
@@ -1196,7 +1191,6 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
         n_out = n_top;
         direct = true;
         uint64_t g = 0ull;
-        g1 = 0ull;
         if (wave == 0) {
             const uint32_t b1 = cnt[0], b2 = b1 + cnt[1], b3 = b2 + cnt[2];
             const uint32_t i = static_cast<uint32_t>(lane);
@@ -1215,9 +1209,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             }
             if (i < n_c && r < m) store_shared(&slot[2u + r], x);
             const uint64_t hm = __ballot(i < n_c && r == m - 1u);
-            const uint64_t hj = __ballot(i < n_c && r == j1 - 1u);
             if (hm) g = wave::readlane64(x, __ffsll(static_cast<unsigned long long>(hm)) - 1);
-            if (hj) g1 = wave::readlane64(x, __ffsll(static_cast<unsigned long long>(hj)) - 1);
         }
         return g;  // meaningful in wave 0, which publishes it
     }
@@ -1250,7 +1242,6 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     // most m elements listed everything.
     const uint64_t g = n_top == m ? sh.list[m - 1] : 0ull;
     if (pen_all && n_c > m) n_out += append_penalised(sh, n_c, m, g, slot, stride, ok);
-    g1 = ok ? (n_top >= j1 ? sh.list[j1 - 1] : 0ull) : kGuaranteeFailed;
     return ok ? g : kGuaranteeFailed;
 }
 
@@ -1266,8 +1257,6 @@ __device__ __forceinline__ void write_row(const DevArgs& a, int row, int32_t tok
         a.ring_len[row] = static_cast<int32_t>(len + 1u);
     }
     a.tickets[row] = 0u;  // ready for the next launch
-    a.row_gmax[2 * row] = 0ull;
-    a.row_gmax[2 * row + 1] = 0ull;
 }
 
 // The 16 floats p[0, 16) (16-byte aligned, in LDS) in every lane: four
@@ -1682,6 +1671,38 @@ __device__ __forceinline__ void load_slots(const DevArgs& a, SelShared& sh, int 
     }
 }
 
+// The row's largest guarantees from the words load_slots loaded (after the
+// barrier that follows it; sh.u64[0..1] cleared before that barrier): at
+// level m each chunk's guarantee word, at level j1 each chunk's j1-th entry
+// (every element outside a chunk's first j1 entries is below it). A chunk
+// that listed fewer than j1 entries listed everything and adds nothing; a
+// chunk that failed makes both levels fail. Block-uniform.
+template <int kPer>
+__device__ __forceinline__ void row_guarantees(SelShared& sh, uint32_t j1, const uint64_t (&w)[kPer],
+                                               const uint32_t (&wp)[kPer], const uint32_t (&wc)[kPer],
+                                               uint64_t& gm, uint64_t& g1) {
+    const int lane = __lane_id();
+    uint64_t a = 0ull, b = 0ull;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        if (wp[i] == 0u) a = w[i] > a ? w[i] : a;
+        if (wp[i] == 1u + j1) {
+            const uint64_t g = sh.gam[wc[i]];
+            const uint64_t v = g == kGuaranteeFailed ? kGuaranteeFailed : (sh.cnt[wc[i]] >= j1 ? w[i] : 0ull);
+            b = v > b ? v : b;
+        }
+    }
+    a = wave_max_u64(a);
+    b = wave_max_u64(b);
+    if (lane == 0) {
+        atomicMax(reinterpret_cast<unsigned long long*>(&sh.u64[0]), static_cast<unsigned long long>(a));
+        atomicMax(reinterpret_cast<unsigned long long*>(&sh.u64[1]), static_cast<unsigned long long>(b));
+    }
+    __syncthreads();
+    gm = sh.u64[0];
+    g1 = sh.u64[1];
+}
+
 __device__ __forceinline__ bool slot_entry(const SelShared& sh, uint32_t wp, uint32_t wc) {
     return wp >= 2u && wp != 0xffffffffu && wp - 2u < sh.cnt[wc];
 }
@@ -1713,10 +1734,11 @@ __device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, c
     constexpr int kPer = kSlotWords / kBlock;
     uint64_t w[kPer];
     uint32_t wp[kPer], wc[kPer];
-    // The largest guarantee, folded in by every chunk before its ticket.
-    const uint64_t gam_max = load_shared(&a.row_gmax[2 * rc.row]);
+    if (tid == 0) sh.u64[0] = sh.u64[1] = 0ull;
     load_slots(a, sh, rc.row, stride, w, wp, wc);
     __syncthreads();
+    uint64_t gam_max, gam1;
+    row_guarantees(sh, 1u, w, wp, wc, gam_max, gam1);
     const bool bounded = gam_max != 0ull && gam_max != kGuaranteeFailed;
     const bool pen_all = rc.pen && !(rc.r >= 1.0f);
 
@@ -1831,17 +1853,18 @@ constexpr int kSmallWords = 4;
 // penalised in one balanced pass and ranked into sh.top; the top k is
 // certified when its k-th final value is above C. Block-uniform.
 __device__ __forceinline__ bool merge_collect_small(const DevArgs& a, SelShared& sh, const RowCtx& rc, uint32_t k,
-                                                    uint32_t stride, uint32_t& nt) {
+                                                    uint32_t j1, uint32_t stride, uint32_t& nt) {
     const int tid = threadIdx.x;
     if (tid < 32) sh.exp_tab[tid] = exp2_table(static_cast<uint32_t>(tid));  // in flight with the slots
     const bool pen_all = rc.pen && !(rc.r >= 1.0f);
     uint64_t w[kSmallWords];
     uint32_t wp[kSmallWords], wc[kSmallWords];
-    // The row's largest guarantees at level j1 and at level m, folded in by
-    // every chunk before its ticket.
-    const uint64_t gam_lv[2] = {load_shared(&a.row_gmax[2 * rc.row + 1]), load_shared(&a.row_gmax[2 * rc.row])};
+    if (tid == 0) sh.u64[0] = sh.u64[1] = 0ull;
     load_slots(a, sh, rc.row, stride, w, wp, wc);
     __syncthreads();
+    // The row's largest guarantees at level j1 and at level m.
+    uint64_t gam_lv[2];
+    row_guarantees(sh, j1, w, wp, wc, gam_lv[1], gam_lv[0]);
     bool ent[kSmallWords];
 #pragma unroll
     for (int i = 0; i < kSmallWords; ++i) ent[i] = slot_entry(sh, wp[i], wc[i]);
@@ -2123,24 +2146,16 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
                                     : min(static_cast<uint32_t>(kSlotWords / a.cpr), 2u * m + 24u);
     uint64_t* slot = a.slots + static_cast<int64_t>(row) * kSlotWords + static_cast<int64_t>(chunk) * stride;
 
-    const uint32_t j1 = spec_level1(k, a.cpr, m);
     uint32_t n_top, n_out;
-    uint64_t g1;
     bool direct, ok;
-    const uint64_t gamma = chunk_topm<T, EPT>(rc, chunk * CHUNK, m, j1, s_pbits, sh, slot, stride, n_top, n_out, g1,
-                                              direct, ok);
+    const uint64_t gamma =
+        chunk_topm<T, EPT>(rc, chunk * CHUNK, m, s_pbits, sh, slot, stride, n_top, n_out, direct, ok);
 
-    // Publish [guarantee, count, entries] (candidate lists and appended
-    // penalised entries are already written) and fold the guarantee into the
-    // row's maximum, wait for the stores, then one ticket per workgroup; the
-    // last workgroup of the row merges.
+    // Publish [guarantee, count, sorted entries] (a list ranked by one wave
+    // or with appended penalised entries is already written), wait for the
+    // stores, then one ticket per workgroup; the last workgroup of the row
+    // merges.
     if (tid == 0) {
-        // Row maxima of the level-m guarantee and of the level-j1 one (the
-        // j1-th entry: every element outside the first j1 is below it).
-        if (gamma != 0ull)
-            (void)__hip_atomic_fetch_max(&a.row_gmax[2 * row], gamma, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (g1 != 0ull)
-            (void)__hip_atomic_fetch_max(&a.row_gmax[2 * row + 1], g1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         store_shared(&slot[0], gamma);
         store_shared(&slot[1], static_cast<uint64_t>(min(n_out, stride - 2u)));
     }
@@ -2162,7 +2177,7 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
     const float x0 = greedy ? load_one(static_cast<const T*>(rc.rowp), 0) : 0.0f;
     uint32_t nt;
     const bool collected = static_cast<uint32_t>(a.cpr) * stride <= static_cast<uint32_t>(kBlock * kSmallWords)
-                               ? merge_collect_small(a, sh, rc, k, stride, nt)
+                               ? merge_collect_small(a, sh, rc, k, spec_level1(k, a.cpr, m), stride, nt)
                                : merge_collect(a, sh, rc, k, stride, nt);
     if (!collected) {
         // Fallback: every listed entry with its final value, then an exact
