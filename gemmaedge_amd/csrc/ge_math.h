@@ -202,12 +202,14 @@ __host__ __device__ inline float tanhf_fdlibm(float x) {
      0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull, \
      0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull}
 
-__constant__ const uint64_t kExp2TableDev[32] = GE_EXP2_TABLE;
 static const uint64_t kExp2TableHost[32] = GE_EXP2_TABLE;
 
 __host__ __device__ inline uint64_t exp2_table(uint32_t i) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    return kExp2TableDev[i];
+    // A local constant array: addressed PC-relative, with no load of its
+    // address first (a __constant__ variable is reached through the GOT).
+    static constexpr uint64_t kTab[32] = GE_EXP2_TABLE;
+    return kTab[i];
 #else
     return kExp2TableHost[i];
 #endif

@@ -33,11 +33,11 @@
 // runs the reference's softmax / min-p / top-p / draw in its exact operation
 // order (src/generation.cpp:89-126).
 //
-// Cross-workgroup data is written with agent-scope relaxed atomic stores and
-// read with agent-scope relaxed atomic loads: on gfx950 these carry the sc1
-// bit and are coherent across the XCDs' L2s. Each wave waits for its stores
-// (s_waitcnt) before the barrier that precedes the ticket; no __threadfence()
-// (which writes back and invalidates the XCD's whole L2).
+// Cross-workgroup data is written with agent-scope relaxed atomic stores: on
+// gfx950 these carry the sc1 bit and are coherent across the XCDs' L2s. Each
+// wave waits for its stores (s_waitcnt) before the barrier that precedes the
+// ticket; no __threadfence() (which writes back and invalidates the XCD's
+// whole L2). The merging workgroup reads the lists with agent-scope loads.
 //
 // No MFMA: nothing here is a contraction. The bound is HBM bandwidth.
 #include <hip/hip_runtime.h>
@@ -1634,7 +1634,8 @@ __device__ __forceinline__ uint32_t absorb_list(SelShared& sh, uint32_t nt, uint
 // Loads the row's slot words, kPer per thread: w[i], its position wp[i] in
 // its chunk's slot (0 = the guarantee, 1 = the count, 2.. = entries; past the
 // end: 0xffffffff) and its chunk wc[i]; stores each chunk's guarantee in
-// sh.gam[c] and its count in sh.cnt[c]. One round trip. After a barrier,
+// sh.gam[c] and its count in sh.cnt[c], and stages the expf table in
+// sh.exp_tab. One round trip. After a barrier,
 // slot_entry(...) tells which words are entries of this launch (a chunk's
 // words past its count hold older data).
 template <int kPer>
@@ -1650,6 +1651,9 @@ __device__ __forceinline__ void load_slots(const DevArgs& a, SelShared& sh, int 
         const uint32_t g = static_cast<uint32_t>(i * kBlock + tid);
         w[i] = g < words ? load_shared(&slot_row[g]) : 0ull;
     }
+    // The expf table (2^(i/32)) from constant memory, in flight with the
+    // lists (a wait for it alone would delay their issue by a round trip).
+    const uint64_t et = tid < 32 ? exp2_table(static_cast<uint32_t>(tid)) : 0ull;
     uint32_t c = static_cast<uint32_t>(tid) / stride, q = static_cast<uint32_t>(tid) % stride;
     const uint32_t dc = kBlock / stride, dq = kBlock % stride;
 #pragma unroll
@@ -1669,6 +1673,7 @@ __device__ __forceinline__ void load_slots(const DevArgs& a, SelShared& sh, int 
         if (wp[i] == 0u) sh.gam[wc[i]] = w[i];
         if (wp[i] == 1u) sh.cnt[wc[i]] = static_cast<uint32_t>(w[i]);
     }
+    if (tid < 32) sh.exp_tab[tid] = et;
 }
 
 // The row's largest guarantees from the words load_slots loaded (after the
@@ -1730,7 +1735,6 @@ __device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, c
     const int tid = threadIdx.x;
     const int lane = __lane_id();
     const int wave = tid >> 6;
-    if (tid < 32) sh.exp_tab[tid] = exp2_table(static_cast<uint32_t>(tid));  // in flight with the slots
     constexpr int kPer = kSlotWords / kBlock;
     uint64_t w[kPer];
     uint32_t wp[kPer], wc[kPer];
@@ -1855,7 +1859,6 @@ constexpr int kSmallWords = 4;
 __device__ __forceinline__ bool merge_collect_small(const DevArgs& a, SelShared& sh, const RowCtx& rc, uint32_t k,
                                                     uint32_t j1, uint32_t stride, uint32_t& nt) {
     const int tid = threadIdx.x;
-    if (tid < 32) sh.exp_tab[tid] = exp2_table(static_cast<uint32_t>(tid));  // in flight with the slots
     const bool pen_all = rc.pen && !(rc.r >= 1.0f);
     uint64_t w[kSmallWords];
     uint32_t wp[kSmallWords], wc[kSmallWords];
@@ -2171,8 +2174,8 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
     __syncthreads();
     if (sh.u32[0] == 0u) return;
 
-    // Row inputs of the merge's last steps, loaded now so their latency
-    // overlaps the collection.
+    // Row inputs of the merge's last steps (scalar loads), loaded now so
+    // their latency overlaps the collection.
     const float u = greedy ? 0.0f : a.uniforms[row];
     const float x0 = greedy ? load_one(static_cast<const T*>(rc.rowp), 0) : 0.0f;
     uint32_t nt;
