@@ -1112,8 +1112,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
 
     // With a penalty below 1, the penalty bits of this thread's slots (bit s
     //    = slot s) select candidates: read them once (the W elements of a
-    //    16-byte group lie in one bitmap word). Otherwise entries are staged
-    //    unmarked and the few candidates get their penalty flag afterwards.
+    //    16-byte group lie in one bitmap word).
     uint64_t pm = 0ull;
     if (pen_all) {
 #pragma unroll
@@ -1123,30 +1122,37 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
         }
     }
 
-    // 4. Stage the candidates from ballots into this wave's segment as raw
-    //    entries. A group of 4 slots is examined only if its maximum reaches
-    //    the bound; with a penalty below 1 every penalised token is a
-    //    candidate.
+    // 4. Stage the candidates from ballots into this wave's segment, as
+    //    (value bits << 32 | element index): the fewest instructions per
+    //    candidate on this serial path. Their raw entries (order key, penalty
+    //    flag) are built where they are read, one candidate per lane. A group
+    //    of 4 slots is examined only if its maximum reaches the bound; with a
+    //    penalty below 1 every penalised token is a candidate. A position
+    //    past the segment is clamped to its last word: the count then shows
+    //    the overflow and the exact routine takes over.
     const int ebase = c0 + tid * W;
     uint32_t woff = 0;  // wave-uniform
     uint64_t* seg = sh.stage + wave * kSeg;
     auto put = [&](bool c, int s) {
         const uint64_t mk = __ballot(c);
         if (mk) {
-            const uint32_t o = woff + lanes_below(mk);
-            if (c && o < static_cast<uint32_t>(kSeg)) {
-                const int e = ebase + (s / W) * kBlock * W + s % W;
-                seg[o] = raw_entry(order_key(value(s)), static_cast<uint32_t>(e), ((pm >> s) & 1ull) != 0ull);
+            if (c) {
+                const uint32_t o = min(woff + lanes_below(mk), static_cast<uint32_t>(kSeg - 1));
+                const uint32_t e = static_cast<uint32_t>(ebase + (s / W) * kBlock * W + s % W);
+                seg[o] = (static_cast<uint64_t>(f2u(value(s))) << 32) | e;
             }
             woff += static_cast<uint32_t>(__popcll(mk));
         }
     };
-    // The penalty flag of an entry staged unmarked (bit 31 of the low word
-    // cleared for a penalised token).
-    const bool fix_pen = rc.pen && !pen_all;
-    auto mark_pen = [&](uint64_t x) -> uint64_t {
-        const uint32_t off = raw_entry_index(x) - static_cast<uint32_t>(c0);
-        return ((pbits[off >> 5] >> (off & 31)) & 1u) ? (x & ~0x80000000ull) : x;
+    // The raw entry of a staged candidate.
+    auto entry_of = [&](uint64_t y) -> uint64_t {
+        const uint32_t e = static_cast<uint32_t>(y);
+        bool pen = false;
+        if (rc.pen) {
+            const uint32_t off = e - static_cast<uint32_t>(c0);
+            pen = ((pbits[off >> 5] >> (off & 31)) & 1u) != 0u;
+        }
+        return raw_entry(order_key(u2f(static_cast<uint32_t>(y >> 32))), e, pen);
     };
     if (allpass) {
 #pragma unroll
@@ -1163,11 +1169,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
         for (int s = 0; s < EPT; ++s) put(value(s) >= floor_v || ((pm >> s) & 1ull) != 0ull, s);
     }
     fence_words();
-    // Pad an odd segment with an empty entry (the rank reads entries in pairs).
-    if (lane == 0) {
-        sh.u32[kSegCount + wave] = woff;
-        if ((woff & 1u) && woff < static_cast<uint32_t>(kSeg)) seg[woff] = 0ull;
-    }
+    if (lane == 0) sh.u32[kSegCount + wave] = woff;
     __syncthreads();
     uint32_t cnt[kBlock / 64];
     uint32_t n_c = 0;
@@ -1196,8 +1198,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             const uint32_t i = static_cast<uint32_t>(lane);
             const int w = (i >= b1 ? 1 : 0) + (i >= b2 ? 1 : 0) + (i >= b3 ? 1 : 0);
             const uint32_t base = w == 0 ? 0u : (w == 1 ? b1 : (w == 2 ? b2 : b3));
-            uint64_t x = i < n_c ? sh.stage[w * kSeg + (i - base)] : 0ull;
-            if (fix_pen && i < n_c) x = mark_pen(x);
+            const uint64_t x = i < n_c ? entry_of(sh.stage[w * kSeg + (i - base)]) : 0ull;
             sh.top[lane] = x;  // scratch (unused by the chunk phase); zeros past n_c
             wave_lds_sync();
             const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(sh.top);
@@ -1223,17 +1224,15 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
 #pragma unroll
         for (int w = 0; w < kBlock / 64; ++w) base += w < wave ? cnt[w] : 0u;
         for (uint32_t i = lane; i < cnt[wave]; i += 64) {
-            const uint64_t x = fix_pen ? mark_pen(seg[i]) : seg[i];
+            const uint64_t x = entry_of(seg[i]);
             sh.stage[base + i] = x;
             sh.hist[base + i] = static_cast<uint32_t>(x >> 32);
         }
         for (uint32_t i = n_c + tid; i < ((n_c + 15u) & ~15u); i += kBlock) sh.hist[i] = 0u;
         n_top = rank_top_hi(sh, sh.stage, n_c, m, sh.list, true);
     } else {
-        if (fix_pen) {
-            for (uint32_t i = lane; i < cnt[wave]; i += 64) seg[i] = mark_pen(seg[i]);
-            __syncthreads();
-        }
+        for (uint32_t i = lane; i < cnt[wave]; i += 64) seg[i] = entry_of(seg[i]);
+        __syncthreads();
         seg_gather(sh.stage, cnt, n_c);
         n_top = select_top(sh.stage, n_c, m, sh.list);
     }
