@@ -574,6 +574,28 @@ __device__ __forceinline__ uint32_t rank_top_hi(SelShared& sh, uint64_t* src, ui
     return out;
 }
 
+// dst[0, min(n, m)) = the largest min(n, m) of the distinct non-zero keys
+// src[0, n) (n <= kBlock), sorted descending, by counting with exact 64-bit
+// compares on keys read in pairs from LDS broadcasts. The caller has padded
+// src[n, roundup(n, 8)) with zeros and synchronised. Block-uniform (one
+// barrier at the end).
+__device__ __forceinline__ uint32_t rank_top_exact(const uint64_t* src, uint32_t n, uint32_t m, uint64_t* dst) {
+    const int tid = threadIdx.x;
+    if (static_cast<uint32_t>(tid) < n) {
+        const uint64_t x = src[tid];
+        const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(src);
+        uint32_t r = 0;
+        for (uint32_t j = 0; j < (n + 7u) / 8u; ++j) {
+            const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
+            r += (q0.x > x ? 1u : 0u) + (q0.y > x ? 1u : 0u) + (q1.x > x ? 1u : 0u) + (q1.y > x ? 1u : 0u);
+            r += (q2.x > x ? 1u : 0u) + (q2.y > x ? 1u : 0u) + (q3.x > x ? 1u : 0u) + (q3.y > x ? 1u : 0u);
+        }
+        if (r < m) dst[r] = x;
+    }
+    __syncthreads();
+    return min(n, m);
+}
+
 // The row-level context every workgroup of a row shares.
 struct RowCtx {
     const void* rowp;   // the row's logits
@@ -1888,7 +1910,9 @@ __device__ __forceinline__ bool merge_collect_small(const DevArgs& a, SelShared&
         for (int i = 0; i < kSmallWords; ++i)
             if ((in >> i) & 1u) sh.stage[pos++] = w[i];
         __syncthreads();
-        // Final values in place; item n caps G's raw value.
+        // Final values in place; item n caps G's raw value. Zeros pad the
+        // entries to a multiple of 8 for the rank's paired reads.
+        if (static_cast<uint32_t>(tid) >= n && static_cast<uint32_t>(tid) < ((n + 7u) & ~7u)) sh.stage[tid] = 0ull;
         const uint32_t items = n + (bounded ? 1u : 0u);
         for (uint32_t i = tid; i < items; i += kBlock) {
             const bool real = i < n;
@@ -1902,7 +1926,7 @@ __device__ __forceinline__ bool merge_collect_small(const DevArgs& a, SelShared&
             }
         }
         __syncthreads();
-        nt = n <= static_cast<uint32_t>(kBlock) ? rank_top_hi(sh, sh.stage, n, k, sh.top)
+        nt = n <= static_cast<uint32_t>(kBlock) ? rank_top_exact(sh.stage, n, k, sh.top)
                                                : select_top(sh.stage, n, k, sh.top);
         if (!bounded) return true;  // every chunk listed everything
         if (nt >= k && composite_key(sh.top[k - 1]) > sh.u32[16]) return true;
