@@ -513,67 +513,6 @@ __device__ __forceinline__ uint32_t select_top(uint64_t* src, uint32_t n, uint32
     return out;
 }
 
-// Number of the n keys hk[0, n) (padded with zeros to a multiple of 16)
-// greater than h, counted on 31-bit halves: key >> 1 > h >> 1 exactly when
-// (h >> 1) - (key >> 1) borrows, so the count is a sum of sign bits (no
-// compare-to-mask round trips). Keys equal in all but their lowest bit are
-// not counted; callers detect the resulting equal ranks. Four 16-byte LDS
-// reads are issued per step before any is used.
-__device__ __forceinline__ uint32_t count_greater_hi(const uint32_t* hk, uint32_t n, uint32_t h) {
-    const uint4* p4 = reinterpret_cast<const uint4*>(hk);
-    const uint32_t hh = h >> 1;
-    uint32_t r = 0;
-    auto acc = [&](const uint4& q) {
-        r += ((hh - (q.x >> 1)) >> 31) + ((hh - (q.y >> 1)) >> 31);
-        r += ((hh - (q.z >> 1)) >> 31) + ((hh - (q.w >> 1)) >> 31);
-    };
-    for (uint32_t j = 0; j < (n + 15u) / 16u; ++j) {
-        const uint4 q0 = p4[4 * j + 0];
-        const uint4 q1 = p4[4 * j + 1];
-        const uint4 q2 = p4[4 * j + 2];
-        const uint4 q3 = p4[4 * j + 3];
-        acc(q0);
-        acc(q1);
-        acc(q2);
-        acc(q3);
-    }
-    return r;
-}
-
-// dst[0, min(n, m)) = the largest min(n, m) of the distinct non-zero keys
-// src[0, n) (n <= kBlock), sorted descending, by counting on their high words
-// only (count_greater_hi), about half the work of 64-bit keys. Two keys whose
-// high words agree but for the lowest bit can get the same rank; a
-// compare-and-swap into dst (cleared first) detects that and the exact 64-bit
-// ranking takes over. With `hk_ready`, sh.hist[0, n) already holds the high
-// words (padded to a multiple of 16). Block-uniform; uses sh.hist.
-__device__ __forceinline__ uint32_t rank_top_hi(SelShared& sh, uint64_t* src, uint32_t n, uint32_t m,
-                                                uint64_t* dst, bool hk_ready = false) {
-    const int tid = threadIdx.x;
-    const uint32_t out = min(n, m);
-    uint32_t* hk = sh.hist;
-    if (!hk_ready) {
-        if (static_cast<uint32_t>(tid) < n) hk[tid] = static_cast<uint32_t>(src[tid] >> 32);
-        else if (static_cast<uint32_t>(tid) < ((n + 15u) & ~15u)) hk[tid] = 0u;  // below every entry
-    }
-    if (static_cast<uint32_t>(tid) < out) dst[tid] = 0ull;
-    if (tid == 0) sh.u32[16 + 3] = 0u;
-    __syncthreads();
-    // (Read after the barrier: with hk_ready other waves have just written src.)
-    const uint64_t x = static_cast<uint32_t>(tid) < n ? src[tid] : 0ull;
-    if (static_cast<uint32_t>(tid) < n) {
-        const uint32_t r = count_greater_hi(hk, n, static_cast<uint32_t>(x >> 32));
-        if (r < m) {
-            const unsigned long long old = atomicCAS(reinterpret_cast<unsigned long long*>(&dst[r]), 0ull,
-                                                     static_cast<unsigned long long>(x));
-            if (old != 0ull) sh.u32[16 + 3] = 1u;  // equal ranks
-        }
-    }
-    __syncthreads();
-    if (sh.u32[16 + 3] != 0u) return select_top(src, n, m, dst);
-    return out;
-}
-
 // dst[0, min(n, m)) = the largest min(n, m) of the distinct non-zero keys
 // src[0, n) (n <= kBlock), sorted descending, by counting with exact 64-bit
 // compares on keys read in pairs from LDS broadcasts. The caller has padded
@@ -1238,20 +1177,17 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     }
     // 5. The top m, sorted. Up to kBlock candidates: each wave moves its
     //    segment to its place in stage[0, n_c) (inside segment 0's area past
-    //    wave 0's entries, so no wave overwrites another's unread entries)
-    //    with the high words beside it, then rank by counting. More: gather
-    //    and sort.
+    //    wave 0's entries, so no wave overwrites another's unread entries),
+    //    then rank by counting. More: gather and sort.
     if (n_c <= static_cast<uint32_t>(kBlock)) {
         uint32_t base = 0;
 #pragma unroll
         for (int w = 0; w < kBlock / 64; ++w) base += w < wave ? cnt[w] : 0u;
-        for (uint32_t i = lane; i < cnt[wave]; i += 64) {
-            const uint64_t x = entry_of(seg[i]);
-            sh.stage[base + i] = x;
-            sh.hist[base + i] = static_cast<uint32_t>(x >> 32);
-        }
-        for (uint32_t i = n_c + tid; i < ((n_c + 15u) & ~15u); i += kBlock) sh.hist[i] = 0u;
-        n_top = rank_top_hi(sh, sh.stage, n_c, m, sh.list, true);
+        for (uint32_t i = lane; i < cnt[wave]; i += 64) sh.stage[base + i] = entry_of(seg[i]);
+        if (static_cast<uint32_t>(tid) >= n_c && static_cast<uint32_t>(tid) < ((n_c + 7u) & ~7u))
+            sh.stage[tid] = 0ull;
+        __syncthreads();
+        n_top = rank_top_exact(sh.stage, n_c, m, sh.list);
     } else {
         for (uint32_t i = lane; i < cnt[wave]; i += 64) seg[i] = entry_of(seg[i]);
         __syncthreads();
