@@ -945,15 +945,34 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     constexpr uint32_t kHole = 0x7fc00000u;  // NaN placed in out-of-range slots
 
     // 1. The first kBlock * kLoadBatch history ids, then the chunk's 16-byte
-    //    loads; both round trips overlap (loads return in issue order).
+    //    loads; both round trips overlap (loads return in issue order). The
+    //    id loads are unconditional (index clamped, validity checked at use)
+    //    so that the wait for them counts only them, not the logits.
     int hid[kLoadBatch];
     if (rc.pen) {
 #pragma unroll
-        for (int u = 0; u < kLoadBatch; ++u) {
-            const int j = u * kBlock + tid;
-            hid[u] = j < rc.H ? rc.hist[j] : -1;
-        }
+        for (int u = 0; u < kLoadBatch; ++u) hid[u] = rc.hist[min(u * kBlock + tid, rc.H - 1)];
     }
+    // 2. The penalty bitmap (one bit per element of the chunk) from the row's
+    //    history. Built on each load path separately: on the vector path
+    //    after the logit loads are issued, while they are in flight (the ids
+    //    arrive first); a build after the paths join would wait for every
+    //    load of either path.
+    auto mark_history = [&]() {
+        if (!rc.pen) return;
+        for (int w = tid; w < CHUNK / 32; w += kBlock) pbits[w] = 0u;
+        __syncthreads();
+        for (int base = 0; base < rc.H; base += kBlock * kLoadBatch) {
+            if (base > 0) {
+#pragma unroll
+                for (int u = 0; u < kLoadBatch; ++u) hid[u] = rc.hist[min(base + u * kBlock + tid, rc.H - 1)];
+            }
+#pragma unroll
+            for (int u = 0; u < kLoadBatch; ++u)
+                if (base + u * kBlock + tid < rc.H && hid[u] >= c0 && hid[u] < cend)
+                    atomicOr(&pbits[(hid[u] - c0) >> 5], 1u << ((hid[u] - c0) & 31));
+        }
+    };
     uint32_t d[NW];
     uint64_t vmask = ~0ull;  // in-range slots
     if (rc.vec_ok && c0 + CHUNK <= rc.V) {
@@ -968,7 +987,9 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             d[4 * v + 3] = q.w;
         }
         if constexpr (EPT < 64) vmask = (1ull << EPT) - 1ull;
+        mark_history();
     } else {
+        mark_history();
         vmask = 0ull;
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
@@ -1000,26 +1021,6 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             for (int i = 0; i < NW; ++i) asm volatile("" : "+v"(d[i]));
         }
     };
-
-    // 2. The penalty bitmap (one bit per element of the chunk) from the row's
-    //    history, while the logits are in flight: the ids arrive first.
-    if (rc.pen) {
-        for (int w = tid; w < CHUNK / 32; w += kBlock) pbits[w] = 0u;
-        __syncthreads();
-        for (int base = 0; base < rc.H; base += kBlock * kLoadBatch) {
-            if (base > 0) {
-#pragma unroll
-                for (int u = 0; u < kLoadBatch; ++u) {
-                    const int j = base + u * kBlock + tid;
-                    hid[u] = j < rc.H ? rc.hist[j] : -1;
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kLoadBatch; ++u)
-                if (hid[u] >= c0 && hid[u] < cend)
-                    atomicOr(&pbits[(hid[u] - c0) >> 5], 1u << ((hid[u] - c0) & 31));
-        }
-    }
 
     // 3. The bound. Maxima of groups of 4 raw values (fmaxf ignores the NaN
     //    of out-of-range slots).
