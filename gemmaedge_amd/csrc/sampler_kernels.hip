@@ -177,9 +177,15 @@ constexpr int kListCap = kMaxTopK + 8;
 // largest m-th entry, so a chunk lists a few more than it contributes), capped
 // by the chunk length and the chunk's slot (kSlotWords / cpr words:
 // guarantee, count, entries). Every workgroup of the row computes the same m.
+// mu = k / cpr with the hardware reciprocal, and its hardware square root:
+// any m is correct (it only sizes the lists), and these few instructions are
+// deterministic, so every workgroup of a row gets the same m.
+__device__ __forceinline__ float spec_mu(uint32_t k, int cpr) {
+    return static_cast<float>(k) * __builtin_amdgcn_rcpf(static_cast<float>(cpr));
+}
 __device__ __forceinline__ uint32_t spec_m(uint32_t k, int cpr, int chunk_len) {
-    const float mu = static_cast<float>(k) / static_cast<float>(cpr);
-    uint32_t m = static_cast<uint32_t>(ceilf(mu + 4.0f * sqrtf(mu))) + 4u;
+    const float mu = spec_mu(k, cpr);
+    uint32_t m = static_cast<uint32_t>(ceilf(mu + 4.0f * __builtin_amdgcn_sqrtf(mu))) + 4u;
     m = min(m, k + 4u);
     m = max(m, 2u);
     m = min(m, static_cast<uint32_t>(kListCap));
@@ -193,8 +199,8 @@ __device__ __forceinline__ uint32_t spec_m(uint32_t k, int cpr, int chunk_len) {
 // which certifies the row's top k in about 99% of rows with far fewer
 // entries to rank; the full lists (level m) are its second try.
 __device__ __forceinline__ uint32_t spec_level1(uint32_t k, int cpr, uint32_t m) {
-    const float mu = static_cast<float>(k) / static_cast<float>(cpr);
-    const uint32_t j = static_cast<uint32_t>(ceilf(mu + 3.0f * sqrtf(mu))) + 2u;
+    const float mu = spec_mu(k, cpr);
+    const uint32_t j = static_cast<uint32_t>(ceilf(mu + 3.0f * __builtin_amdgcn_sqrtf(mu))) + 2u;
     return min(j, m);
 }
 
@@ -975,6 +981,18 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     };
     uint32_t d[NW];
     uint64_t vmask = ~0ull;  // in-range slots
+    auto value = [&](int s) -> float {
+        if constexpr (W == 4) return u2f(d[s]);
+        else return u2f((s % 2 == 0) ? (d[s / 2] << 16) : (d[s / 2] & 0xffff0000u));
+    };
+    // bf16: makes the packed words opaque so that the unpacked floats of one
+    // phase are recomputed in the next instead of being held in registers.
+    auto fence_words = [&]() {
+        if constexpr (W == 8) {
+#pragma unroll
+            for (int i = 0; i < NW; ++i) asm volatile("" : "+v"(d[i]));
+        }
+    };
     if (rc.vec_ok && c0 + CHUNK <= rc.V) {
         // Streaming loads: each logit is read once, so they carry the
         // nontemporal hint and do not displace the lists and history in L2.
@@ -1009,18 +1027,6 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             }
         }
     }
-    auto value = [&](int s) -> float {
-        if constexpr (W == 4) return u2f(d[s]);
-        else return u2f((s % 2 == 0) ? (d[s / 2] << 16) : (d[s / 2] & 0xffff0000u));
-    };
-    // bf16: makes the packed words opaque so that the unpacked floats of one
-    // phase are recomputed in the next instead of being held in registers.
-    auto fence_words = [&]() {
-        if constexpr (W == 8) {
-#pragma unroll
-            for (int i = 0; i < NW; ++i) asm volatile("" : "+v"(d[i]));
-        }
-    };
 
     // 3. The bound. Maxima of groups of 4 raw values (fmaxf ignores the NaN
     //    of out-of-range slots).
