@@ -1640,33 +1640,44 @@ __device__ __forceinline__ void load_slots(const DevArgs& a, SelShared& sh, int 
     if (tid < 32) sh.exp_tab[tid] = et;
 }
 
-// The row's largest guarantees from the words load_slots loaded (after the
-// barrier that follows it; sh.u64[0..1] cleared before that barrier): at
-// level m each chunk's guarantee word, at level j1 each chunk's j1-th entry
-// (every element outside a chunk's first j1 entries is below it). A chunk
-// that listed fewer than j1 entries listed everything and adds nothing; a
-// chunk that failed makes both levels fail. Block-uniform.
-template <int kPer>
+// LDS *p = max(*p, v), one ds_max_u64 per lane. Written out because the
+// compiler's atomic optimizer turns an atomicMax on one LDS address from
+// divergent lanes into a serial loop over the active lanes (readlane per
+// lane). Not ordered by the compiler: callers wait (lds_wait) before the
+// barrier that publishes the result.
+__device__ __forceinline__ void lds_max_u64(uint64_t* p, uint64_t v) {
+    const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint64_t*)p));
+    asm volatile("ds_max_u64 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// After the barrier that follows load_slots (sh.u64[0..1] cleared before
+// it): which loaded words are entries of this launch (ent[i]; a chunk's words
+// past its count hold older data), and the row's largest guarantees, at
+// level m each chunk's guarantee word and at level j1 each chunk's j1-th
+// entry (every element outside a chunk's first j1 entries is below it). A
+// chunk that listed fewer than j1 entries listed everything and adds
+// nothing; a chunk that failed makes both levels fail. The lanes holding
+// those words fold them into LDS with atomicMax: no cross-lane reduction.
+// kLevel1 = false: level m only (g1 = 0). Block-uniform (one barrier).
+template <bool kLevel1, int kPer>
 __device__ __forceinline__ void row_guarantees(SelShared& sh, uint32_t j1, const uint64_t (&w)[kPer],
                                                const uint32_t (&wp)[kPer], const uint32_t (&wc)[kPer],
-                                               uint64_t& gm, uint64_t& g1) {
-    const int lane = __lane_id();
-    uint64_t a = 0ull, b = 0ull;
+                                               bool (&ent)[kPer], uint64_t& gm, uint64_t& g1) {
+    uint32_t cn[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) cn[i] = wp[i] != 0xffffffffu ? sh.cnt[wc[i]] : 0u;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-        if (wp[i] == 0u) a = w[i] > a ? w[i] : a;
-        if (wp[i] == 1u + j1) {
+        ent[i] = wp[i] >= 2u && wp[i] != 0xffffffffu && wp[i] - 2u < cn[i];
+        if (wp[i] == 0u && w[i] != 0ull) lds_max_u64(&sh.u64[0], w[i]);
+        if (kLevel1 && wp[i] == 1u + j1) {
             const uint64_t g = sh.gam[wc[i]];
-            const uint64_t v = g == kGuaranteeFailed ? kGuaranteeFailed : (sh.cnt[wc[i]] >= j1 ? w[i] : 0ull);
-            b = v > b ? v : b;
+            const uint64_t v = g == kGuaranteeFailed ? kGuaranteeFailed : (cn[i] >= j1 ? w[i] : 0ull);
+            if (v != 0ull) lds_max_u64(&sh.u64[1], v);
         }
     }
-    a = wave_max_u64(a);
-    b = wave_max_u64(b);
-    if (lane == 0) {
-        atomicMax(reinterpret_cast<unsigned long long*>(&sh.u64[0]), static_cast<unsigned long long>(a));
-        atomicMax(reinterpret_cast<unsigned long long*>(&sh.u64[1]), static_cast<unsigned long long>(b));
-    }
+    lds_wait();
     __syncthreads();
     gm = sh.u64[0];
     g1 = sh.u64[1];
@@ -1706,7 +1717,8 @@ __device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, c
     load_slots(a, sh, rc.row, stride, w, wp, wc);
     __syncthreads();
     uint64_t gam_max, gam1;
-    row_guarantees(sh, 1u, w, wp, wc, gam_max, gam1);
+    bool ent[kPer];
+    row_guarantees<false>(sh, 1u, w, wp, wc, ent, gam_max, gam1);
     const bool bounded = gam_max != 0ull && gam_max != kGuaranteeFailed;
     const bool pen_all = rc.pen && !(rc.r >= 1.0f);
 
@@ -1716,7 +1728,7 @@ __device__ __forceinline__ bool merge_collect(const DevArgs& a, SelShared& sh, c
         uint32_t woff = 0;  // <= kPer * 64 = kSeg
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const bool c = slot_entry(sh, wp[i], wc[i]) && (w[i] > gam_max || (pen_all && raw_entry_pen(w[i])));
+            const bool c = ent[i] && (w[i] > gam_max || (pen_all && raw_entry_pen(w[i])));
             const uint64_t mk = __ballot(c);
             if (c) seg[woff + lanes_below(mk)] = w[i];
             woff += static_cast<uint32_t>(__popcll(mk));
@@ -1831,10 +1843,8 @@ __device__ __forceinline__ bool merge_collect_small(const DevArgs& a, SelShared&
     __syncthreads();
     // The row's largest guarantees at level j1 and at level m.
     uint64_t gam_lv[2];
-    row_guarantees(sh, j1, w, wp, wc, gam_lv[1], gam_lv[0]);
     bool ent[kSmallWords];
-#pragma unroll
-    for (int i = 0; i < kSmallWords; ++i) ent[i] = slot_entry(sh, wp[i], wc[i]);
+    row_guarantees<true>(sh, j1, w, wp, wc, ent, gam_lv[1], gam_lv[0]);
     for (int lv = 0; lv < 2; ++lv) {
         const uint64_t gam = gam_lv[lv];
         if (gam == kGuaranteeFailed) return false;
