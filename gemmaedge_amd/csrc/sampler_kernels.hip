@@ -114,6 +114,17 @@ __device__ __forceinline__ double readlane_d(double v, int i) {
 
 // Orders this wave's LDS accesses: LDS operations of one wave execute in
 // issue order, so a compiler-level barrier suffices.
+// Lane j of the result is v, every other lane keeps old: one v_cndmask with
+// the constant lane mask in an SGPR pair, instead of a compare against the
+// lane id that writes VCC and the wait states before the select reads it.
+template <int j>
+__device__ __forceinline__ float put_lane(float old, float v) {
+    static_assert(j >= 0 && j < 64, "lane");
+    float r;
+    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(old), "v"(v), "s"(1ull << j));
+    return r;
+}
+
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1378,7 +1389,7 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, const float* pr
                 static_for<0, 16>([&](auto J) {
                     constexpr int j = b + decltype(J)::value;
                     c = c + readlane_f(pl, j);
-                    cl = lane == j ? c : cl;
+                    cl = put_lane<j>(cl, c);
                 });
                 const uint64_t th = __ballot(lane >= b && lane < b + 16 && idx >= 1 && idx < limit && cl >= p.top_p);
                 if (th) {
@@ -1415,7 +1426,7 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, const float* pr
                 static_for<0, 16>([&](auto J) {
                     constexpr int j = b + decltype(J)::value;
                     c = c - readlane_f(pl, j);
-                    cl = lane == j ? c : cl;
+                    cl = put_lane<j>(cl, c);
                 });
                 const uint64_t hit = __ballot(lane >= b && lane < b + 16 && idx < keep && cl <= 0.0f);
                 if (hit) {
@@ -1508,7 +1519,7 @@ __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge
         static_for<0, 16>([&](auto J) {
             constexpr int j = b + decltype(J)::value;
             cum = cum + q.v[decltype(J)::value];
-            cl = lane == j ? cum : cl;
+            cl = put_lane<j>(cl, cum);
         });
         const uint64_t th = __ballot(lane >= b && lane < b + 16 && lane >= 1 && lane < static_cast<int>(limit) &&
                                      cl >= p.top_p);
@@ -1534,7 +1545,7 @@ __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge
         static_for<0, 16>([&](auto J) {
             constexpr int j = b + decltype(J)::value;
             choice = choice - q.v[decltype(J)::value];
-            chl = lane == j ? choice : chl;
+            chl = put_lane<j>(chl, choice);
         });
         const uint64_t hit = __ballot(lane >= b && lane < b + 16 && lane < static_cast<int>(keep) && chl <= 0.0f);
         if (hit) {
