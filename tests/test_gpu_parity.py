@@ -231,3 +231,21 @@ def test_repeated_rescans_are_stable(sampler):
             t, _, _ = sampler.sample(dx, cfg, uniforms=du, history=dh, history_offsets=do)
             bad += int(np.count_nonzero(t.cpu().numpy() != ora.tokens))
         assert bad == 0, f"k={k}: {bad} mismatching row-launches over 40 launches"
+
+
+def test_penalty_below_one_with_long_histories(sampler):
+    # r < 1 raises penalised positive logits, so every penalised token of a
+    # chunk is listed besides its top m. About 250 history ids per chunk
+    # overflow a chunk's slot: it publishes a failed guarantee and the merge
+    # rescans it exactly. About 40 per chunk fit, and the appended entries
+    # take part in the merge.
+    rng = np.random.default_rng(55)
+    rows, V = 8, W.VOCAB
+    x = (rng.standard_normal((rows, V)) * 3).astype(np.float32)
+    for H in (640, 4096):
+        hist = rng.integers(0, V, size=rows * H).astype(np.int32)
+        offs = (np.arange(rows + 1) * H).astype(np.int32)
+        w = small_workload(f"pen0.8-H{H}", x, dict(temperature=0.7, top_k=40, top_p=0.9, softcap=30.0,
+                                                     repetition_penalty=0.8),
+                           history=hist, offsets=offs, uniforms=W.mt_uniforms(H, rows))
+        _check(sampler, w)
