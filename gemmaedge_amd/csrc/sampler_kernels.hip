@@ -1538,10 +1538,23 @@ __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge
     float choice = choice0, chl = 0.0f;
     uint32_t pos = keep - 1u;
     bool found = false;
+    // Boundary sums for the near flag, c_at = sum_{i <= pos} (double)p_i in
+    // order and c_before up to pos - 1: an inclusive double scan over the kept
+    // entries is exact (any order gives the sequential sum) when every kept
+    // p_i is a multiple of 2^-52, their total being below 2. It does not
+    // depend on pos, so it runs inside the walk's first block, in the shadow
+    // of that block's LDS read; the sequential sum is the fallback.
+    const float pk = lane < static_cast<int>(keep) ? pr : 0.0f;
+    double incl = 0.0;
+    bool incl_exact = false;
     static_for<0, 4>([&](auto B) {
         constexpr int b = decltype(B)::value * 16;
         if (found || static_cast<uint32_t>(b) >= keep) return;
         const F16 q = lds16(lds + 64 + b);
+        if constexpr (b == 0) {
+            incl_exact = wave_min_i(pk > 0.0f ? lsb_exponent(pk) : INT_MAX) >= -52;
+            incl = wave_incl_f64(static_cast<double>(pk));
+        }
         static_for<0, 16>([&](auto J) {
             constexpr int j = b + decltype(J)::value;
             choice = choice - q.v[decltype(J)::value];
@@ -1553,24 +1566,17 @@ __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge
             found = true;
         }
     });
-    // Boundary sums c_at = sum_{i <= pos} (double)p_i in order, c_before up to
-    // pos - 1.
     double c_before = 0.0, c_at = 0.0;
-    {
-        const float pc = lane <= static_cast<int>(pos) ? pr : 0.0f;
-        const int lsb = pc > 0.0f ? lsb_exponent(pc) : INT_MAX;
-        if (wave_min_i(lsb) >= -52) {
-            const double incl = wave_incl_f64(static_cast<double>(pc));
-            c_at = readlane_d(incl, static_cast<int>(pos));
-            c_before = pos > 0 ? readlane_d(incl, static_cast<int>(pos) - 1) : 0.0;
-        } else {
-            double dc = 0.0;
-            for (uint32_t i = 0; i <= pos; ++i) {
-                c_before = dc;
-                dc = dc + static_cast<double>(readlane_f(pc, static_cast<int>(i)));
-            }
-            c_at = dc;
+    if (incl_exact) {
+        c_at = readlane_d(incl, static_cast<int>(pos));
+        c_before = pos > 0 ? readlane_d(incl, static_cast<int>(pos) - 1) : 0.0;
+    } else {
+        double dc = 0.0;
+        for (uint32_t i = 0; i <= pos; ++i) {
+            c_before = dc;
+            dc = dc + static_cast<double>(readlane_f(pk, static_cast<int>(i)));
         }
+        c_at = dc;
     }
     bool near = false;
     if (pos > 0 && fabs(static_cast<double>(choice0) - c_before) < 1e-6) near = true;
