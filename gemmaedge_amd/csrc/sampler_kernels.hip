@@ -72,7 +72,6 @@ __device__ __forceinline__ U load_shared(const U* p) {
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) { return wave::incl_add(v); }
 __device__ __forceinline__ uint32_t wave_max(uint32_t v) { return wave::max_u32(v); }
 __device__ __forceinline__ uint32_t wave_min(uint32_t v) { return wave::min_u32(v); }
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { return wave::max_u64(v); }
 __device__ __forceinline__ int wave_min_i(int v) { return wave::min_i32(v); }
 __device__ __forceinline__ double wave_sum(double v) { return wave::sum_f64(v); }
 __device__ __forceinline__ double wave_incl_f64(double v) { return wave::incl_f64(v); }

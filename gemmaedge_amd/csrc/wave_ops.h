@@ -72,16 +72,6 @@ __device__ __forceinline__ uint64_t dpp64(uint64_t x, uint64_t fill) {
     const uint32_t hi = dpp<kCtrl, kRowMask>(static_cast<uint32_t>(x >> 32), static_cast<uint32_t>(fill >> 32));
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
-__device__ __forceinline__ uint64_t max_u64(uint64_t v) {
-    auto mx = [](uint64_t a, uint64_t b) { return a > b ? a : b; };
-    v = mx(v, dpp64<kRowShr1, 0xf>(v, 0));
-    v = mx(v, dpp64<kRowShr2, 0xf>(v, 0));
-    v = mx(v, dpp64<kRowShr4, 0xf>(v, 0));
-    v = mx(v, dpp64<kRowShr8, 0xf>(v, 0));
-    v = mx(v, dpp64<kRowBcast15, 0xa>(v, 0));
-    v = mx(v, dpp64<kRowBcast31, 0xc>(v, 0));
-    return readlane64(v, 63);
-}
 // Sum in the scan's order (not the reference's): callers use it only where
 // every order gives the same result, or as a certificate check.
 __device__ __forceinline__ double sum_f64(double v) {
