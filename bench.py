@@ -276,6 +276,7 @@ def c5_sweep(torch, sampler, W, steps):
     ring_len.zero_()
     stream = torch.cuda.current_stream()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    step_tokens = torch.empty(steps, dtype=torch.int32, device="cuda")
     torch.cuda.synchronize()
     for i in range(steps):
         logits.copy_(all_logits[i])
@@ -283,10 +284,42 @@ def c5_sweep(torch, sampler, W, steps):
         ev[i][0].record(stream)
         g.replay()
         ev[i][1].record(stream)
+        step_tokens[i:i + 1].copy_(tokens)
     torch.cuda.synchronize()
     us = np.array([e0.elapsed_time(e1) * 1000.0 for e0, e1 in ev])
-    return {"steps": steps, "p50_us": float(np.median(us)), "p99_us": float(np.percentile(us, 99)),
-            "mean_us": float(np.mean(us)), "history_len_final": int(ring_len.item())}
+    out = {"steps": steps, "p50_us": float(np.median(us)), "p99_us": float(np.percentile(us, 99)),
+           "mean_us": float(np.mean(us)), "history_len_final": int(ring_len.item())}
+
+    # The same decode loop with every step captured in one graph: launch i
+    # reads step i's logits and uniform in place and appends to the device
+    # history ring, so the per-step cost is the sampler's own, without a graph
+    # launch per step. Its tokens must equal the step-by-step run's.
+    graph_tokens = torch.empty(steps, dtype=torch.int32, device="cuda")
+    g_all = torch.cuda.CUDAGraph()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g_all, stream=side):
+            cs = torch.cuda.current_stream().cuda_stream
+            for i in range(steps):
+                a.logits = all_logits[i].data_ptr()
+                a.uniforms = uni_all[i:i + 1].data_ptr()
+                a.tokens_out = graph_tokens[i:i + 1].data_ptr()
+                rc = lib.ge_sample(sampler._h, ctypes.c_void_p(cs), ctypes.byref(a))
+                if rc != 0:
+                    raise RuntimeError(S.last_error())
+    torch.cuda.synchronize()
+    for _ in range(2):  # the first replay uploads the graph; the second is timed
+        ring.zero_()
+        ring_len.zero_()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g_all.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    out["one_graph_us_per_step"] = e0.elapsed_time(e1) * 1000.0 / steps
+    out["one_graph_tokens_match"] = bool(torch.equal(graph_tokens, step_tokens))
+    return out
 
 
 def main():
