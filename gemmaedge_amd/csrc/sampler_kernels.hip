@@ -529,6 +529,26 @@ __device__ __forceinline__ uint32_t select_top(uint64_t* src, uint32_t n, uint32
     return out;
 }
 
+// r + the number of the four keys a, b, c, d greater than x. Each compare
+// writes its own SGPR pair and feeds an add-with-carry, and every mask is
+// read three instructions after it is written: no compare into VCC followed
+// by wait states and a select, as the compiler emits for (q > x ? 1 : 0).
+__device__ __forceinline__ uint32_t add_greater4(uint32_t r, uint64_t a, uint64_t b, uint64_t c, uint64_t d,
+                                                 uint64_t x) {
+    uint64_t s0, s1, s2, s3, co;
+    asm("v_cmp_gt_u64_e64 %1, %6, %10\n\t"
+        "v_cmp_gt_u64_e64 %2, %7, %10\n\t"
+        "v_cmp_gt_u64_e64 %3, %8, %10\n\t"
+        "v_cmp_gt_u64_e64 %4, %9, %10\n\t"
+        "v_addc_co_u32_e64 %0, %5, %0, 0, %1\n\t"
+        "v_addc_co_u32_e64 %0, %5, %0, 0, %2\n\t"
+        "v_addc_co_u32_e64 %0, %5, %0, 0, %3\n\t"
+        "v_addc_co_u32_e64 %0, %5, %0, 0, %4"
+        : "+v"(r), "=&s"(s0), "=&s"(s1), "=&s"(s2), "=&s"(s3), "=&s"(co)
+        : "v"(a), "v"(b), "v"(c), "v"(d), "v"(x));
+    return r;
+}
+
 // dst[0, min(n, m)) = the largest min(n, m) of the distinct non-zero keys
 // src[0, n) (n <= kBlock), sorted descending, by counting with exact 64-bit
 // compares on keys read in pairs from LDS broadcasts. The caller has padded
@@ -542,8 +562,8 @@ __device__ __forceinline__ uint32_t rank_top_exact(const uint64_t* src, uint32_t
         uint32_t r = 0;
         for (uint32_t j = 0; j < (n + 7u) / 8u; ++j) {
             const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
-            r += (q0.x > x ? 1u : 0u) + (q0.y > x ? 1u : 0u) + (q1.x > x ? 1u : 0u) + (q1.y > x ? 1u : 0u);
-            r += (q2.x > x ? 1u : 0u) + (q2.y > x ? 1u : 0u) + (q3.x > x ? 1u : 0u) + (q3.y > x ? 1u : 0u);
+            r = add_greater4(r, q0.x, q0.y, q1.x, q1.y, x);
+            r = add_greater4(r, q2.x, q2.y, q3.x, q3.y, x);
         }
         if (r < m) dst[r] = x;
     }
@@ -1183,8 +1203,8 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             uint32_t r = 0;
             for (uint32_t j = 0; j < (n_c + 7u) / 8u; ++j) {
                 const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
-                r += (q0.x > x ? 1u : 0u) + (q0.y > x ? 1u : 0u) + (q1.x > x ? 1u : 0u) + (q1.y > x ? 1u : 0u);
-                r += (q2.x > x ? 1u : 0u) + (q2.y > x ? 1u : 0u) + (q3.x > x ? 1u : 0u) + (q3.y > x ? 1u : 0u);
+                r = add_greater4(r, q0.x, q0.y, q1.x, q1.y, x);
+                r = add_greater4(r, q2.x, q2.y, q3.x, q3.y, x);
             }
             if (i < n_c && r < m) store_shared(&slot[2u + r], x);
             const uint64_t hm = __ballot(i < n_c && r == m - 1u);
