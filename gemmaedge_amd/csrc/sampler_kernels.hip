@@ -474,19 +474,33 @@ __device__ __forceinline__ uint32_t tie_ceil(uint32_t r, float cap) {
 }
 
 // Descending bitonic sort of s[0, n), n a power of two <= kStage, by the
-// whole workgroup through LDS.
+// whole workgroup through LDS. In each stage a thread's pairs are disjoint, so
+// it loads all of them before comparing and storing any: one LDS round trip
+// per stage instead of one per pair (the compiler cannot prove that a pair's
+// stores miss the next pair's loads).
 __device__ __forceinline__ void bitonic_desc_block(uint64_t* s, uint32_t n) {
+    constexpr int kPairs = kStage / 2 / kBlock;  // pairs per thread at most
     const int tid = threadIdx.x;
     for (uint32_t size = 2; size <= n; size <<= 1) {
         for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t i = tid; i < n / 2; i += kBlock) {
+            uint64_t x[kPairs], y[kPairs];
+#pragma unroll
+            for (int u = 0; u < kPairs; ++u) {
+                const uint32_t i = static_cast<uint32_t>(u * kBlock + tid);
                 const uint32_t pos = 2 * i - (i & (stride - 1));
-                const uint32_t q = pos + stride;
+                if (i < n / 2) {
+                    x[u] = s[pos];
+                    y[u] = s[pos + stride];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kPairs; ++u) {
+                const uint32_t i = static_cast<uint32_t>(u * kBlock + tid);
+                const uint32_t pos = 2 * i - (i & (stride - 1));
                 const bool desc = (pos & size) == 0;
-                const uint64_t x = s[pos], y = s[q];
-                if ((x < y) == desc) {
-                    s[pos] = y;
-                    s[q] = x;
+                if (i < n / 2 && (x[u] < y[u]) == desc) {
+                    s[pos] = y[u];
+                    s[pos + stride] = x[u];
                 }
             }
             __syncthreads();
