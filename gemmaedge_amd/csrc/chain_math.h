@@ -288,29 +288,29 @@ GE_CHAIN_HD void float_fields(uint32_t bits, uint32_t& man, int& e) {
 
 // D = round(a / U) with the tie flag (D is then the even neighbour) and the
 // big flag (a / U >= 2^24: the step leaves the binade).
+//
+// Written with selects only (no early exits), so a wave evaluating it for
+// many addends at once runs no divergent branches:
+//   ma == 0      -> D = 0
+//   sh < 0       -> big (ma >= 2^23 here, so a / U >= 2^24), D = 0
+//   sh >= 32     -> a / U < 2^-8: rounds to 0, no tie
+//   0 <= sh < 32 -> D = ma >> sh rounded to nearest by the sh dropped bits
+//                   (sh = 0 drops none: frac = half = 0, never a tie).
 GE_CHAIN_HD void step_bits(uint32_t ab, int uexp, uint32_t& D, bool& tie, bool& big) {
     uint32_t ma;
     int ea;
     float_fields(ab, ma, ea);
     const int sh = uexp + 150 - ea;  // a / U = ma * 2^-sh
-    tie = false;
-    big = false;
-    D = 0;
-    if (ma == 0) return;
-    if (sh < 0) {
-        big = true;  // ma >= 2^23 here, so a / U >= 2^24
-        return;
-    }
-    if (sh >= 32) return;  // a / U < 2^-8: rounds to 0, no tie
-    const uint32_t d0 = ma >> sh;
-    if (sh == 0) {
-        D = d0;
-        return;
-    }
-    const uint32_t frac = ma & ((1u << sh) - 1u);
-    const uint32_t half = 1u << (sh - 1);
-    tie = frac == half;
-    D = tie ? d0 + (d0 & 1u) : d0 + (frac > half ? 1u : 0u);
+    const bool nz = ma != 0u;
+    const bool in_range = nz && sh >= 0 && sh < 32;
+    const uint32_t shc = static_cast<uint32_t>(sh < 0 ? 0 : (sh > 31 ? 31 : sh));
+    const uint32_t d0 = ma >> shc;
+    const uint32_t frac = ma & ((1u << shc) - 1u);
+    const uint32_t half = (1u << shc) >> 1;
+    big = nz && sh < 0;
+    tie = in_range && shc != 0u && frac == half;
+    const uint32_t up = tie ? (d0 & 1u) : (frac > half ? 1u : 0u);
+    D = in_range ? d0 + up : 0u;
 }
 
 // Smallest m with m * 2^uexp >= thr, for a float thr; kNoThreshold when thr is
@@ -336,131 +336,141 @@ GE_CHAIN_HD uint32_t threshold_bits(uint32_t tb, int uexp) {
 // ---- float accumulator, in 32-bit integers --------------------------------
 //
 // The same two runs for a float accumulator, the case of the top-p
-// cumulative and the draw walk. m < 2^24, so the binade arithmetic fits in
-// 32-bit integers; the ulp and its inverse come straight from the float's
-// exponent field (exact powers of two), and the quotients are 32-bit.
+// cumulative and the draw walk. The accumulator is carried as its float bits:
+// binade_bits gives m = accumulator / U, step_bits the per-element increment
+// D (with the tie and big flags), threshold_bits the threshold in ulps, and
+// the run lengths inside a binade are 32-bit quotients (m < 2^24, D <= 2^24).
+// The one element that leaves a binade, and a tie from an odd m, is a plain
+// float operation. thr must be a float value (or NaN); s, c >= 0.
 
-struct BinadeF {
-    uint32_t m;     // accumulator / U
-    uint32_t lo;    // smallest m a descending step may produce and stay exact
-    double ulp;     // U
-    double scale;   // 1 / U
-};
-constexpr uint32_t kHiF = 0xFFFFFFu;  // largest m an ascending step may produce
-
-GE_CHAIN_HD BinadeF binade_f32(double s) {
-    const uint32_t sb = __builtin_bit_cast(uint32_t, static_cast<float>(s));
-    const uint32_t ex = sb >> 23;
-    const bool low = ex <= 1u;  // subnormals and the first normal binade share U = 2^-149
-    const int uexp = low ? -149 : static_cast<int>(ex) - 150;
-    BinadeF b;
-    b.m = low ? (sb & 0x00FFFFFFu) : ((sb & 0x7FFFFFu) | 0x800000u);
-    b.lo = low ? 1u : 0x800001u;
-    b.ulp = __builtin_bit_cast(double, static_cast<uint64_t>(1023 + uexp) << 52);
-    b.scale = __builtin_bit_cast(double, static_cast<uint64_t>(1023 - uexp) << 52);
-    return b;
+GE_CHAIN_HD uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
+GE_CHAIN_HD float fval(uint32_t b) { return __builtin_bit_cast(float, b); }
+// Bits of m * U for an m that stays in the binade of sb.
+GE_CHAIN_HD uint32_t rebuild_bits(uint32_t sb, uint32_t m) {
+    return (sb >> 23) <= 1u ? m : ((sb & 0x7F800000u) | (m & 0x7FFFFFu));
 }
+constexpr uint32_t kHiF = 0xFFFFFFu;  // largest m an ascending step may produce
 
 GE_CHAIN_HD uint64_t asc_run_f32(double& s, double a, uint64_t n, double thr, bool& hit) {
     hit = false;
+    if (n == 0) return 0;
+    if (!(a > 0.0)) {
+        if (s >= thr) {
+            hit = true;
+            return 1;
+        }
+        return n;
+    }
+    const float af = static_cast<float>(a);
+    const uint32_t ab = fbits(af);
+    const uint32_t tb = fbits(static_cast<float>(thr));
+    uint32_t sb = fbits(static_cast<float>(s));
+    if ((sb & 0x7F800000u) == 0x7F800000u) {  // inf or NaN: no later element changes it
+        sb = fbits(fval(sb) + af);
+        s = static_cast<double>(fval(sb));
+        if (s >= thr) {
+            hit = true;
+            return 1;
+        }
+        return n;
+    }
     uint64_t done = 0;
     while (done < n) {
-        if (!(a > 0.0)) {
-            if (s >= thr) {
-                hit = true;
-                return done + 1;
-            }
-            return n;
-        }
-        BinadeF b = binade_f32(s);
-        const double A = a * b.scale;
-        const double D0 = std::floor(A);
-        const double fr = A - D0;
-        const uint32_t d0 = A < 16777216.0 ? static_cast<uint32_t>(D0) : 0u;
-        const bool tie = fr == 0.5;
-        if (s == 0.0 || A >= 16777216.0 || (tie && (b.m & 1u))) {  // one ordinary step
-            s = add_once<float>(s, a);
+        const StepBits b = binade_bits(sb);
+        uint32_t D;
+        bool tie, big;
+        step_bits(ab, b.uexp, D, tie, big);
+        if ((sb & 0x7FFFFFFFu) == 0u || big || (tie && (b.m & 1u))) {  // one ordinary step
+            sb = fbits(fval(sb) + af);
             ++done;
-            if (s >= thr) {
+            if (static_cast<double>(fval(sb)) >= thr) {
                 hit = true;
+                s = static_cast<double>(fval(sb));
                 return done;
             }
             continue;
         }
-        const uint32_t D = tie ? d0 + (d0 & 1u) : d0 + (fr > 0.5 ? 1u : 0u);
         const uint64_t rem = n - done;
-        const uint64_t jv = D ? (kHiF - b.m) / D : kNone;
-        uint64_t jh = kNone;
-        if (thr == thr) {
-            if (!(thr > 0.0)) {
-                jh = 1;
-            } else {
-                const double tmd = std::ceil(thr * b.scale);
-                if (tmd <= 16777216.0) {
-                    const uint32_t tm = static_cast<uint32_t>(tmd);
-                    if (b.m >= tm) jh = 1;
-                    else if (D) jh = (tm - b.m + D - 1) / D;
-                }
-            }
+        const uint64_t jv = D ? static_cast<uint64_t>((kHiF - b.m) / D) : kNone;  // steps that stay in the binade
+        uint64_t jh = kNone;                                                       // steps to reach thr
+        const uint32_t tm = threshold_bits(tb, b.uexp);
+        if (tm != kNoThreshold) {
+            if (b.m >= tm) jh = 1;
+            else if (D) jh = (tm - b.m + D - 1u) / D;
         }
         uint64_t j = rem < jv ? rem : jv;
         if (jh < j) j = jh;
-        b.m += static_cast<uint32_t>(j) * D;
-        s = static_cast<double>(b.m) * b.ulp;
+        sb = rebuild_bits(sb, b.m + static_cast<uint32_t>(j) * D);
         done += j;
         if (j == jh) {
             hit = true;
+            s = static_cast<double>(fval(sb));
             return done;
         }
         if (done < n) {
-            s = add_once<float>(s, a);
+            sb = fbits(fval(sb) + af);
             ++done;
-            if (s >= thr) {
+            if (static_cast<double>(fval(sb)) >= thr) {
                 hit = true;
+                s = static_cast<double>(fval(sb));
                 return done;
             }
         }
     }
+    s = static_cast<double>(fval(sb));
     return n;
 }
 
 GE_CHAIN_HD uint64_t desc_run_f32(double& c, double a, uint64_t n, bool& stop) {
     stop = false;
-    uint64_t done = 0;
-    while (done < n) {
-        if (c <= a) {
+    if (n == 0) return 0;
+    const float af = static_cast<float>(a);
+    const uint32_t ab = fbits(af);
+    uint32_t cb = fbits(static_cast<float>(c));
+    if ((cb & 0x7F800000u) == 0x7F800000u) {  // inf or NaN
+        if (fval(cb) <= af) {
             stop = true;
-            return done;
+            return 0;
         }
         if (!(a > 0.0)) return n;
-        BinadeF b = binade_f32(c);
-        const double A = a * b.scale;  // a < c, so A < 2^24
-        const double D0 = std::floor(A);
-        const double fr = A - D0;
-        const uint32_t d0 = static_cast<uint32_t>(D0);
-        const bool tie = fr == 0.5;
+        cb = fbits(fval(cb) - af);  // stays inf or NaN
+        c = static_cast<double>(fval(cb));
+        return n;
+    }
+    uint64_t done = 0;
+    while (done < n) {
+        if (fval(cb) <= af) {
+            stop = true;
+            c = static_cast<double>(fval(cb));
+            return done;
+        }
+        if (!(a > 0.0)) break;
+        const StepBits b = binade_bits(cb);
+        uint32_t D;
+        bool tie, big;
+        step_bits(ab, b.uexp, D, tie, big);  // a < c: never big
         if (tie && (b.m & 1u)) {
-            c = sub_once<float>(c, a);
+            cb = fbits(fval(cb) - af);
             ++done;
             continue;
         }
-        const uint32_t D = tie ? d0 + (d0 & 1u) : d0 + (fr > 0.5 ? 1u : 0u);
-        if (D == 0 && b.m >= b.lo) return n;
-        const uint64_t jv = (D && b.m >= b.lo) ? (b.m - b.lo) / D : 0;
+        if (D == 0 && b.m >= b.lo) break;  // every remaining step leaves c unchanged
+        const uint64_t jv = (D && b.m >= b.lo) ? static_cast<uint64_t>((b.m - b.lo) / D) : 0;
         const uint64_t rem = n - done;
         const uint64_t j = rem < jv ? rem : jv;
-        b.m -= static_cast<uint32_t>(j) * D;
-        c = static_cast<double>(b.m) * b.ulp;
+        cb = rebuild_bits(cb, b.m - static_cast<uint32_t>(j) * D);
         done += j;
         if (done < n) {
-            if (c <= a) {
+            if (fval(cb) <= af) {
                 stop = true;
+                c = static_cast<double>(fval(cb));
                 return done;
             }
-            c = sub_once<float>(c, a);
+            cb = fbits(fval(cb) - af);
             ++done;
         }
     }
+    c = static_cast<double>(fval(cb));
     return n;
 }
 

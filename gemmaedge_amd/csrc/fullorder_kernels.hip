@@ -949,7 +949,10 @@ __device__ bool wave_chain_f32(const View& iv, int G, ChainPos& cp, uint32_t L, 
         for (int j = 0; j <= kPerLane; ++j) bound[j] = iv.start(min(i0 + j, G));
         uint32_t ab[kPerLane];
 #pragma unroll
-        for (int j = 0; j < kPerLane; ++j) ab[j] = i0 + j < G ? f2u(iv.addend(i0 + j)) : 0u;
+        for (int j = 0; j < kPerLane; ++j) {  // G >= 1: the clamped read is in range
+            const uint32_t v = f2u(iv.addend(min(i0 + j, G - 1)));
+            ab[j] = i0 + j < G ? v : 0u;
+        }
         const chain::StepBits bb = chain::binade_bits(sb);
         const uint32_t tm = kDesc ? 0u : chain::threshold_bits(tb, bb.uexp);
         uint32_t nt[kPerLane], lo_e[kPerLane], pre_in[kPerLane + 1];
@@ -963,11 +966,9 @@ __device__ bool wave_chain_f32(const View& iv, int G, ChainPos& cp, uint32_t L, 
             uint32_t D;
             bool tie, big;
             chain::step_bits(ab[j], bb.uexp, D, tie, big);
-            uint32_t tot = 0;
-            if (nt[j] && !big) {
-                const uint32_t lo32 = nt[j] * D;
-                tot = (__umulhi(nt[j], D) != 0u || lo32 > kCap) ? kCap : lo32;
-            }
+            const uint32_t lo32 = nt[j] * D;
+            const uint32_t capped = (__umulhi(nt[j], D) != 0u || lo32 > kCap) ? kCap : lo32;
+            const uint32_t tot = big ? 0u : capped;  // nt = 0 gives 0
             pre_in[j + 1] = pre_in[j] + tot;  // <= 4 * 2^24
             evj[j] = nt[j] && (big || tie);
         }
@@ -1188,9 +1189,11 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     int minlsb = INT_MAX;
     bool nan = false;
     uint32_t run_base = 0;
+    uint64_t it_next = tid < G ? items[tid] : 0ull;
     for (int r0 = 0; r0 < G; r0 += kDThreads) {
         const int i = r0 + tid;
-        const uint64_t it = i < G ? items[i] : 0ull;
+        const uint64_t it = it_next;  // the next round's item loads while this one is scanned
+        it_next = i + kDThreads < G ? items[i + kDThreads] : 0ull;
         const uint32_t n = static_cast<uint32_t>(it);
         uint32_t tot;
         const uint32_t pi = run_base + dblock_excl_scan(n, sh.scan, tot);
@@ -1260,11 +1263,11 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     const float q0 = p0 * inv;
     const float minimum = q0 * p.min_p;
     int first_low = INT_MAX;
-    for (int i = tid; i < G; i += kDThreads) {
-        const float q = aux[i] * inv;
+    for (int i = tid; i < G; i += kDThreads) {  // this thread staged item i in 4a
+        const float q = (i < kStage ? sh.st.add[i] : aux[i]) * inv;
         aux[i] = q;
         if (i < kStage) sh.st.add[i] = q;
-        if (i >= 1 && first_low == INT_MAX && q < minimum && pre[i] < k) first_low = i;
+        if (i >= 1 && first_low == INT_MAX && q < minimum && (i <= kStage ? sh.st.pre[i] : pre[i]) < k) first_low = i;
     }
     first_low = wave_reduce(first_low, [](int x, int y) { return min(x, y); });
     __syncthreads();  // every reader of sh.ired above is done
