@@ -937,7 +937,9 @@ __device__ bool wave_chain(const View& iv, int G, ChainPos& cp, uint32_t L, doub
 // step covers 64 * kPerLane items.
 template <bool kDesc, typename View>
 __device__ bool wave_chain_f32(const View& iv, int G, ChainPos& cp, uint32_t L, double& s, double thr) {
-    constexpr int kPerLane = 4;
+    // LDS rows (at most kStage items) are mostly binade crossings: shorter
+    // steps; global rows (up to V items) are mostly plain steps: longer ones.
+    constexpr int kPerLane = __is_same(View, LdsView) ? 2 : 4;
     constexpr uint32_t kCap = 0x1000000u;
     const int lane = __lane_id();
     const uint32_t tb = f2u(static_cast<float>(thr));
