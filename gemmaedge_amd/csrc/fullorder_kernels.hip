@@ -367,7 +367,7 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
     const int V = a.vocab;
     const ge_sample_params p = params_of(a, row);
     uint32_t k;
-    if (!full_order_row(p, V, k)) return;
+    if (!full_order_row(p, V, k) || row_done(a, row)) return;  // done rows: fo_decide_kernel reports them
 
     const uint16_t* rowp = static_cast<const uint16_t*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
     const int32_t* hist;
@@ -627,7 +627,7 @@ __global__ __launch_bounds__(kThreads) void fo_sort_f32_kernel(DevArgs a) {
     const int V = a.vocab;
     const ge_sample_params p = params_of(a, row);
     uint32_t k;
-    if (!full_order_row(p, V, k)) return;
+    if (!full_order_row(p, V, k) || row_done(a, row)) return;  // done rows: fo_decide_kernel reports them
 
     const float* rowp = static_cast<const float*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
     const int32_t* hist;
@@ -1143,6 +1143,10 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     const ge_sample_params p = params_of(a, row);
     uint32_t k;
     if (!full_order_row(p, V, k)) return;
+    if (row_done(a, row)) {  // finished by an earlier call: the first kernel skipped it too
+        if (tid == 0) skipped_row(a, row);
+        return;
+    }
 
     const int32_t* hist;
     int H;
@@ -1150,26 +1154,20 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     const bool pen = H > 0 && !(p.repetition_penalty == 1.0f);
     uint32_t* bitmap = a.fo_bitmap + static_cast<int64_t>(row) * a.fo_bitmap_words;
     const uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * 4;
+    // The bitmap is all zero again after every call. It is cleared from the
+    // history before the token is appended: with a device ring the history
+    // IS the ring, and once it is full the new token overwrites the oldest
+    // id, whose bit must be cleared from the id read here, not from the token.
     auto finish = [&](int32_t token, float prob, int32_t flags) {
-        if (tid == 0) {
-            a.tokens[row] = token;
-            if (a.probs) a.probs[row] = prob;
-            if (a.flags) a.flags[row] = flags;
-            if (a.ring) {
-                const uint32_t len = static_cast<uint32_t>(a.ring_len[row]);
-                a.ring[static_cast<int64_t>(row) * a.ring_capacity +
-                       static_cast<int64_t>(len % static_cast<uint32_t>(a.ring_capacity))] = token;
-                a.ring_len[row] = static_cast<int32_t>(len + 1u);
-            }
-        }
-        // The bitmap is all zero again after every call.
         if (pen) {
             __syncthreads();
             for (int i = tid; i < H; i += kDThreads) {
                 const int32_t id = hist[i];
                 if (id >= 0 && id < V) bitmap[id >> 5] = 0u;
             }
+            __syncthreads();  // every read of the ring precedes the append below
         }
+        if (tid == 0) emit_row(a, row, token, prob, flags);
     };
     if (meta[kMetaStatus] != kStatusOk) {
         finish(-1, 0.0f, GE_FLAG_UNSUPPORTED);

@@ -73,6 +73,11 @@ Context& context(std::size_t vocab, std::size_t hist) {
         (void)hipFree(ctx.d_hist);
         ctx.d_logits = nullptr;
         ctx.d_hist = nullptr;
+        // Until the new buffers exist the context holds none: a failure
+        // below leaves capacity 0, so the next call retries the allocation
+        // instead of using the freed buffers.
+        ctx.vocab_cap = 0;
+        ctx.hist_cap = 0;
         if (v > static_cast<std::size_t>(std::numeric_limits<int>::max()) ||
             h > static_cast<std::size_t>(std::numeric_limits<int>::max()))
             throw std::invalid_argument("logits or history too large");

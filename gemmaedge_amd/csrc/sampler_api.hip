@@ -168,17 +168,40 @@ void ge_sampler_destroy(ge_sampler* s) {
     delete s;
 }
 
-int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
-    if (!s || !args) return fail(GE_ERR_INVALID_ARG, "sampler or args is NULL");
-    const ge_sample_args& x = *args;
+}  // extern "C"
+
+namespace {
+
+// The workspace one call runs on (a handle's buffers).
+struct Workspace {
+    int device;
+    int max_rows;
+    int max_vocab;
+    uint32_t* tickets;
+    uint64_t* slots;
+    uint64_t* fo_items;
+    float* fo_aux;
+    uint32_t* fo_pre;
+    uint64_t* fo_extras;
+    uint32_t* fo_bitmap;
+    uint32_t* fo_meta;
+    int64_t fo_items_stride;
+    int64_t fo_capacity;
+    int32_t fo_extras_cap;
+    int64_t fo_bitmap_words;
+};
+
+// Validates the arguments against the workspace and launches the kernels on
+// `stream` (the caller has made ws.device current).
+int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
     if (x.vocab < 1) return fail(GE_ERR_INVALID_ARG, "cannot sample empty logits");  // generation.cpp:63
     if (!x.logits || !x.tokens_out) return fail(GE_ERR_INVALID_ARG, "logits or tokens_out is NULL");
     if (x.dtype != GE_DTYPE_F32 && x.dtype != GE_DTYPE_BF16)
         return fail(GE_ERR_INVALID_ARG, "dtype %d", x.dtype);
     if (x.rows < 1) return fail(GE_ERR_INVALID_ARG, "rows %d", x.rows);
-    if (x.rows > s->max_rows || x.vocab > s->max_vocab)
-        return fail(GE_ERR_CAPACITY, "rows %d / vocab %d above handle capacity %d / %d", x.rows,
-                    x.vocab, s->max_rows, s->max_vocab);
+    if (x.rows > ws.max_rows || x.vocab > ws.max_vocab)
+        return fail(GE_ERR_CAPACITY, "rows %d / vocab %d above capacity %d / %d", x.rows, x.vocab,
+                    ws.max_rows, ws.max_vocab);
     if (x.row_stride < x.vocab) return fail(GE_ERR_INVALID_ARG, "row_stride %lld < vocab %d",
                                             static_cast<long long>(x.row_stride), x.vocab);
     if (x.ring) {
@@ -187,6 +210,10 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
         if (x.history) return fail(GE_ERR_INVALID_ARG, "history and ring are exclusive");
     }
     if (x.history && !x.history_offsets) return fail(GE_ERR_INVALID_ARG, "history without offsets");
+    if (x.n_stop < 0 || x.n_stop > GE_MAX_STOP_TOKENS || (x.n_stop > 0 && !x.stop_tokens))
+        return fail(GE_ERR_INVALID_ARG, "n_stop %d (at most %d, with stop_tokens)", x.n_stop, GE_MAX_STOP_TOKENS);
+    if (x.stop_mode != GE_STOP_AFTER_PUSH && x.stop_mode != GE_STOP_BEFORE_PUSH)
+        return fail(GE_ERR_INVALID_ARG, "stop_mode %d", x.stop_mode);
     const bool maybe_sampling = x.row_params != nullptr || !(x.params.temperature <= 0.0f);
     if (maybe_sampling && !x.uniforms) return fail(GE_ERR_INVALID_ARG, "uniforms required when sampling");
 
@@ -205,7 +232,12 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     } else {
         run_full = x.vocab > ge::kMaxTopK;
     }
-    if (run_full && !s->fo_items) return fail(GE_ERR_CAPACITY, "handle has no full-order workspace");
+    if (run_full && !ws.fo_items) {
+        // With per-row parameters (on the device) the select kernel flags
+        // each row that needs the full-order path instead.
+        if (!x.row_params) return fail(GE_ERR_CAPACITY, "top_k %u needs the full-order workspace", x.params.top_k);
+        run_full = false;
+    }
 
     // Launch geometry: 64 logits per thread when there are enough rows to fill
     // the chip, else 16 so a single row still spreads over 64+ workgroups.
@@ -236,24 +268,26 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     a.tokens = x.tokens_out;
     a.probs = x.probs_out;
     a.flags = x.flags_out;
-    a.tickets = s->tickets;
-    a.slots = s->slots;
+    a.stop_tokens = x.n_stop > 0 ? x.stop_tokens : nullptr;
+    a.n_stop = x.n_stop;
+    a.stop_mode = x.stop_mode;
+    a.done = x.done;
+    a.tickets = ws.tickets;
+    a.slots = ws.slots;
     a.cpr = cpr;
     a.chunk_len = chunk_len;
     a.vec_ok = vec_ok ? 1 : 0;
-    a.fo_items = s->fo_items;
-    a.fo_aux = s->fo_aux;
-    a.fo_pre = s->fo_pre;
-    a.fo_extras = s->fo_extras;
-    a.fo_bitmap = s->fo_bitmap;
-    a.fo_meta = s->fo_meta;
-    a.fo_items_stride = s->fo_items_stride;
-    a.fo_extras_cap = s->fo_extras_cap;
-    a.fo_bitmap_words = s->fo_bitmap_words;
-    a.fo_capacity = s->fo_capacity;
+    a.fo_items = ws.fo_items;
+    a.fo_aux = ws.fo_aux;
+    a.fo_pre = ws.fo_pre;
+    a.fo_extras = ws.fo_extras;
+    a.fo_bitmap = ws.fo_bitmap;
+    a.fo_meta = ws.fo_meta;
+    a.fo_items_stride = ws.fo_items_stride;
+    a.fo_extras_cap = ws.fo_extras_cap;
+    a.fo_bitmap_words = ws.fo_bitmap_words;
+    a.fo_capacity = ws.fo_capacity;
 
-    DeviceGuard guard(s->device);
-    if (!guard.ok) return fail(GE_ERR_DEVICE, "hipSetDevice(%d) failed", s->device);
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (run_select) {
         const hipError_t e = ge::launch_select(a, st, ept);
@@ -264,6 +298,33 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
         if (e != hipSuccess) return hip_fail(e, "launch (full order)");
     }
     return GE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
+    if (!s || !args) return fail(GE_ERR_INVALID_ARG, "sampler or args is NULL");
+    DeviceGuard guard(s->device);
+    if (!guard.ok) return fail(GE_ERR_DEVICE, "hipSetDevice(%d) failed", s->device);
+    Workspace ws{};
+    ws.device = s->device;
+    ws.max_rows = s->max_rows;
+    ws.max_vocab = s->max_vocab;
+    ws.tickets = s->tickets;
+    ws.slots = s->slots;
+    ws.fo_items = s->fo_items;
+    ws.fo_aux = s->fo_aux;
+    ws.fo_pre = s->fo_pre;
+    ws.fo_extras = s->fo_extras;
+    ws.fo_bitmap = s->fo_bitmap;
+    ws.fo_meta = s->fo_meta;
+    ws.fo_items_stride = s->fo_items_stride;
+    ws.fo_capacity = s->fo_capacity;
+    ws.fo_extras_cap = s->fo_extras_cap;
+    ws.fo_bitmap_words = s->fo_bitmap_words;
+    return sample_on(ws, stream, *args);
 }
 
 }  // extern "C"

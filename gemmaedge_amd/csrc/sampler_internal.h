@@ -33,6 +33,10 @@ struct DevArgs {
     int32_t* tokens;
     float* probs;
     int32_t* flags;
+    const int32_t* stop_tokens;   // [n_stop] or NULL
+    int32_t n_stop;
+    int32_t stop_mode;            // GE_STOP_AFTER_PUSH / GE_STOP_BEFORE_PUSH
+    int32_t* done;                // [rows] or NULL
 
     // Workspace (allocated by ge_sampler_create, sized for max_rows x max_vocab).
     uint32_t* tickets;            // [max_rows]          zero between calls
@@ -72,6 +76,40 @@ inline int64_t fo_items_stride(int max_history) {
 // f32 rows: one item per distinct final value (up to V) and the end
 // boundary; the sort also uses the aux and pre arrays as two V-entry buffers.
 inline int64_t fo_items_stride_f32(int vocab) { return (static_cast<int64_t>(vocab) + 2 + 63) / 64 * 64; }
+
+// True when the row was finished by an earlier call (done[row] != 0): every
+// kernel skips it, and the one that owns the row reports it (skipped_row).
+__device__ __forceinline__ bool row_done(const DevArgs& a, int row) { return a.done && a.done[row] != 0; }
+
+__device__ __forceinline__ void skipped_row(const DevArgs& a, int row) {
+    a.tokens[row] = -1;
+    if (a.probs) a.probs[row] = 0.0f;
+    if (a.flags) a.flags[row] = GE_FLAG_DONE;
+}
+
+// The row's results, by one thread: token, probability and flags; the stop
+// check (generation.cpp:463-465) and the done flag; the append to the
+// device ring (before the stop under GE_STOP_AFTER_PUSH, as
+// Gemma4Session::generate pushes at generation.cpp:461; not at all under
+// GE_STOP_BEFORE_PUSH, as the CLI loop breaks first at main.cpp:140-143).
+__device__ __forceinline__ void emit_row(const DevArgs& a, int row, int32_t token, float prob, int32_t flags) {
+    bool stop = false;
+    if (token >= 0)
+        for (int i = 0; i < a.n_stop; ++i) stop |= a.stop_tokens[i] == token;
+    if (stop) {
+        flags |= GE_FLAG_STOP;
+        if (a.done) a.done[row] = 1;
+    }
+    a.tokens[row] = token;
+    if (a.probs) a.probs[row] = prob;
+    if (a.flags) a.flags[row] = flags;
+    if (a.ring && token >= 0 && !(stop && a.stop_mode == GE_STOP_BEFORE_PUSH)) {
+        const uint32_t len = static_cast<uint32_t>(a.ring_len[row]);
+        a.ring[static_cast<int64_t>(row) * a.ring_capacity +
+               static_cast<int64_t>(len % static_cast<uint32_t>(a.ring_capacity))] = token;
+        a.ring_len[row] = static_cast<int32_t>(len + 1u);
+    }
+}
 
 // Launches the fused select/sample kernel for rows whose k <= kMaxTopK.
 // ept in {16, 64}. Returns a hipError_t.

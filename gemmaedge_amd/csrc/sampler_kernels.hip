@@ -1258,15 +1258,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
 
 __device__ __forceinline__ void write_row(const DevArgs& a, int row, int32_t token, float prob,
                                           int32_t flags) {
-    a.tokens[row] = token;
-    if (a.probs) a.probs[row] = prob;
-    if (a.flags) a.flags[row] = flags;
-    if (a.ring) {
-        const uint32_t len = static_cast<uint32_t>(a.ring_len[row]);
-        a.ring[static_cast<int64_t>(row) * a.ring_capacity +
-               static_cast<int64_t>(len % static_cast<uint32_t>(a.ring_capacity))] = token;
-        a.ring_len[row] = static_cast<int32_t>(len + 1u);
-    }
+    emit_row(a, row, token, prob, flags);
     a.tickets[row] = 0u;  // ready for the next launch
 }
 
@@ -2154,10 +2146,19 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
         // whenever the handle has their workspace.
         if (a.fo_items) return;
         if (chunk == 0 && tid == 0) {
-            a.tokens[row] = -1;
-            if (a.probs) a.probs[row] = 0.0f;
-            if (a.flags) a.flags[row] = GE_FLAG_UNSUPPORTED;
+            if (row_done(a, row)) {
+                skipped_row(a, row);
+            } else {
+                a.tokens[row] = -1;
+                if (a.probs) a.probs[row] = 0.0f;
+                if (a.flags) a.flags[row] = GE_FLAG_UNSUPPORTED;
+            }
         }
+        return;
+    }
+    if (row_done(a, row)) {
+        // Finished by an earlier call: nothing is read, no ticket is taken.
+        if (chunk == 0 && tid == 0) skipped_row(a, row);
         return;
     }
     RowCtx rc;

@@ -31,6 +31,12 @@ GE_DTYPE_BF16 = 1
 
 GE_FLAG_NEAR_BOUNDARY = 1
 GE_FLAG_UNSUPPORTED = 2
+GE_FLAG_STOP = 4
+GE_FLAG_DONE = 8
+
+GE_STOP_AFTER_PUSH = 0   # Gemma4Session::generate (src/generation.cpp:461-465)
+GE_STOP_BEFORE_PUSH = 1  # CLI decode loop (src/main.cpp:140-143)
+GE_MAX_STOP_TOKENS = 64
 
 EXPORTS = (
     "ge_sampler_available",
@@ -71,6 +77,10 @@ class SampleArgs(ctypes.Structure):
         ("tokens_out", ctypes.c_void_p),
         ("probs_out", ctypes.c_void_p),
         ("flags_out", ctypes.c_void_p),
+        ("stop_tokens", ctypes.c_void_p),
+        ("n_stop", ctypes.c_int32),
+        ("stop_mode", ctypes.c_int32),
+        ("done", ctypes.c_void_p),
     ]
 
 
@@ -181,12 +191,15 @@ class Sampler:
 
     def sample(self, logits, config: SamplingConfig | Sequence[SamplingConfig], uniforms=None,
                history=None, history_offsets=None, ring=None, ring_len=None, stream=None,
-               tokens=None, probs=None, flags=None, row_params=None):
+               tokens=None, probs=None, flags=None, row_params=None, stop_tokens=None,
+               stop_mode=GE_STOP_AFTER_PUSH, done=None):
         """Sample one token per row of a [rows, vocab] (or [vocab]) device tensor.
 
         ``logits`` is float32 or bfloat16 on the GPU; ``uniforms`` float32 [rows];
         ``history`` int32 flat ids with ``history_offsets`` int32 [rows+1], or
-        ``ring``/``ring_len`` for the device ring. Returns (tokens, probs, flags).
+        ``ring``/``ring_len`` for the device ring. ``stop_tokens`` (int32 device
+        tensor) and ``done`` (int32 [rows] device tensor) enable the device-side
+        stop check (see ge_sample_args). Returns (tokens, probs, flags).
         """
         import torch
 
@@ -201,12 +214,21 @@ class Sampler:
         if dt is None:
             raise ValueError(f"unsupported logits dtype {logits.dtype}")
         dev = logits.device
-        if tokens is None:
-            tokens = torch.empty(rows, dtype=torch.int32, device=dev)
-        if probs is None:
-            probs = torch.empty(rows, dtype=torch.float32, device=dev)
-        if flags is None:
-            flags = torch.empty(rows, dtype=torch.int32, device=dev)
+        if stream is None:
+            stream = torch.cuda.current_stream(dev)
+        elif isinstance(stream, int):
+            stream = torch.cuda.ExternalStream(stream, device=dev)
+        # Buffers made here are allocated on the launch stream: the caching
+        # allocator then keeps a block that is dropped while the kernel still
+        # reads or writes it (row_params below) from being reused before the
+        # stream has passed that point.
+        with torch.cuda.stream(stream):
+            if tokens is None:
+                tokens = torch.empty(rows, dtype=torch.int32, device=dev)
+            if probs is None:
+                probs = torch.empty(rows, dtype=torch.float32, device=dev)
+            if flags is None:
+                flags = torch.empty(rows, dtype=torch.int32, device=dev)
         a = SampleArgs()
         a.logits = logits.data_ptr()
         a.dtype = dt
@@ -222,7 +244,8 @@ class Sampler:
             a.params = config[0].params()
             if row_params is None:
                 arr = (SampleParams * rows)(*[c.params() for c in config])
-                row_params = torch.frombuffer(bytearray(arr), dtype=torch.uint8).to(dev)
+                with torch.cuda.stream(stream):
+                    row_params = torch.frombuffer(bytearray(arr), dtype=torch.uint8).to(dev)
         a.row_params = _ptr(row_params)
         a.history = _ptr(history)
         a.history_offsets = _ptr(history_offsets)
@@ -233,8 +256,10 @@ class Sampler:
         a.tokens_out = _ptr(tokens)
         a.probs_out = _ptr(probs)
         a.flags_out = _ptr(flags)
-        if stream is None:
-            stream = torch.cuda.current_stream(dev)
+        a.stop_tokens = _ptr(stop_tokens)
+        a.n_stop = 0 if stop_tokens is None else stop_tokens.numel()
+        a.stop_mode = stop_mode
+        a.done = _ptr(done)
         rc = self.sample_raw(a, stream)
         if rc != GE_OK:
             raise SamplerError(rc, last_error())

@@ -50,6 +50,15 @@ extern "C" {
 /* Per-row output flags (ge_sample_args.flags_out). */
 #define GE_FLAG_NEAR_BOUNDARY 1  /* draw within 1e-6 of an adjacent CDF boundary */
 #define GE_FLAG_UNSUPPORTED 2    /* row's parameters need a path this build lacks; token = -1 */
+#define GE_FLAG_STOP 4           /* the token is one of the stop tokens; done[row] was set */
+#define GE_FLAG_DONE 8           /* done[row] was set on entry: nothing sampled, token = -1 */
+
+/* Where a sampled stop token goes (ge_sample_args.stop_mode). The reference
+ * has both orders: Gemma4Session::generate appends the token to its output
+ * and then stops (src/generation.cpp:461-465); the CLI decode loop stops
+ * before appending it (src/main.cpp:140-143). */
+#define GE_STOP_AFTER_PUSH 0     /* append the stop token to the ring, then stop */
+#define GE_STOP_BEFORE_PUSH 1    /* stop; the stop token is not appended */
 
 /* One row's sampling parameters: the reference SamplingConfig
  * (include/gemmaedge/generation.h:55-61: temperature, top_k, top_p, min_p)
@@ -85,7 +94,9 @@ typedef struct ge_sample_args {
      *      ring[r * ring_capacity + i], i < min(ring_len[r], ring_capacity);
      *      after sampling the kernel stores the row's token at
      *      ring[r * ring_capacity + ring_len[r] % ring_capacity] and
-     *      increments ring_len[r] (all on the device, no host sync).
+     *      increments ring_len[r] (all on the device, no host sync), except
+     *      for a failed row (token -1), a row that was done on entry, and a
+     *      stop token under GE_STOP_BEFORE_PUSH (see stop_tokens below).
      * Duplicates are allowed; ids outside [0, vocab) are ignored. */
     const int32_t* history;
     const int32_t* history_offsets;
@@ -103,7 +114,24 @@ typedef struct ge_sample_args {
     float* probs_out;         /* probability of the chosen token after top-k
                                  normalisation (generation.cpp:100); 1 for greedy */
     int32_t* flags_out;       /* GE_FLAG_* bits */
+
+    /* Stop check on the device, for decode loops replayed from a graph with
+     * several sessions in one batch (GenerationConfig::stop_tokens,
+     * include/gemmaedge/generation.h:66; the check at generation.cpp:463-465).
+     * All optional (NULL / 0: no stop check, no done state).
+     *  - stop_tokens: device int32[n_stop] (n_stop <= GE_MAX_STOP_TOKENS);
+     *  - done: device int32[rows]. A row whose done[r] != 0 on entry is
+     *    skipped: token -1, prob 0, GE_FLAG_DONE, its ring untouched, none of
+     *    its logits read. A row that samples a stop token gets done[r] = 1 and
+     *    GE_FLAG_STOP; stop_mode says whether that token is appended to the
+     *    row's ring first. Tokens of rows that failed (-1) are never appended. */
+    const int32_t* stop_tokens;
+    int32_t n_stop;
+    int32_t stop_mode;        /* GE_STOP_AFTER_PUSH or GE_STOP_BEFORE_PUSH */
+    int32_t* done;
 } ge_sample_args;
+
+#define GE_MAX_STOP_TOKENS 64
 
 typedef struct ge_sampler ge_sampler;
 

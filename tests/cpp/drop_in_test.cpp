@@ -7,8 +7,17 @@
 // (src/generation.cpp:456-460), printing one token per line for the Python
 // test to compare with the CPU oracle.
 //
+// It also runs the decode loop itself (generate mode): Gemma4Session::generate
+// (src/generation.cpp:452-469) or the CLI loop (src/main.cpp:138-146) with the
+// model replaced by a table of logits rows (evaluate(token) moves to the next
+// row), one mt19937_64 across greedy and sampling steps, the session history
+// (prompt + generated ids) passed to the penalty overload, and the reference's
+// stop tokens {1, 106} (include/gemmaedge/generation.h:66).
+//
 //   drop_in_test                                  (known answers only)
 //   drop_in_test ROWS.bin ROWS VOCAB T K P MINP SEED [SOFTCAP PENALTY HIST.bin H]
+//   drop_in_test generate ROWS.bin ROWS VOCAB SEED PROMPT.bin NPROMPT T0,T1,... lib|cli
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <fstream>
@@ -63,12 +72,65 @@ void test_sampling() {
     require(c() == d(), "sampling must consume exactly one generator output");
 }
 
+// The decode loop of Gemma4Session::generate (lib) or of the CLI (cli): the
+// step's temperature cycles through `temps` (0 = greedy, which draws nothing);
+// top-k 64, top-p 0.95, softcap 30, penalty 1.1 over prompt + generated.
+std::vector<gemmaedge::TokenId> generate_loop(const float* rows_f, std::size_t rows, std::size_t vocab,
+                                              std::uint64_t seed, std::vector<gemmaedge::TokenId> history,
+                                              const std::vector<float>& temps, bool cli) {
+    using namespace gemmaedge;
+    const std::vector<TokenId> stop_tokens{1, 106};
+    SamplingExtras extras;
+    extras.softcap = 30.0f;
+    extras.repetition_penalty = 1.1f;
+    std::mt19937_64 random(seed);
+    std::vector<TokenId> generated;
+    std::vector<float> logits(vocab);
+    for (std::size_t i = 0; i < rows; ++i) {  // max_new_tokens = rows
+        logits.assign(rows_f + i * vocab, rows_f + (i + 1) * vocab);
+        SamplingConfig config;
+        config.temperature = temps[i % temps.size()];
+        config.seed = seed;
+        const TokenId token = sample_token(logits, config, random, history.data(), history.size(), extras);
+        const bool stop = std::find(stop_tokens.begin(), stop_tokens.end(), token) != stop_tokens.end();
+        if (cli && stop) break;  // main.cpp:140-143: stop before the push
+        generated.push_back(token);
+        if (stop) break;  // generation.cpp:461-465: push, then stop
+        history.push_back(token);  // evaluate(token): the next row
+    }
+    return generated;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     try {
         test_sampling();
-        if (argc >= 9) {
+        if (argc >= 2 && std::string(argv[1]) == "generate") {
+            require(argc == 10, "generate ROWS.bin ROWS VOCAB SEED PROMPT.bin NPROMPT TEMPS lib|cli");
+            const auto data = read_file(argv[2]);
+            const std::size_t rows = std::stoul(argv[3]);
+            const std::size_t vocab = std::stoul(argv[4]);
+            const std::uint64_t seed = std::stoull(argv[5]);
+            require(data.size() == rows * vocab * sizeof(float), "row file size mismatch");
+            const auto pr = read_file(argv[6]);
+            const std::size_t np = std::stoul(argv[7]);
+            require(pr.size() == np * sizeof(std::int32_t), "prompt file size mismatch");
+            std::vector<gemmaedge::TokenId> prompt(np);
+            std::copy(pr.begin(), pr.end(), reinterpret_cast<char*>(prompt.data()));
+            std::vector<float> temps;
+            std::string t = argv[8];
+            for (std::size_t a = 0, b; a <= t.size(); a = b + 1) {
+                b = t.find(',', a);
+                if (b == std::string::npos) b = t.size();
+                temps.push_back(std::stof(t.substr(a, b - a)));
+            }
+            const std::string mode = argv[9];
+            require(mode == "lib" || mode == "cli", "mode must be lib or cli");
+            const auto out = generate_loop(reinterpret_cast<const float*>(data.data()), rows, vocab, seed, prompt,
+                                           temps, mode == "cli");
+            for (const auto tok : out) std::printf("%d\n", tok);
+        } else if (argc >= 9) {
             const auto data = read_file(argv[1]);
             const std::size_t rows = std::stoul(argv[2]);
             const std::size_t vocab = std::stoul(argv[3]);

@@ -58,3 +58,47 @@ def test_history_overload_matches_oracle(tmp_path):
                                  repetition_penalty=1.1),
                 history=hist.reshape(-1), offsets=(np.arange(rows + 1) * hl).astype(np.int32), uniforms=u)
     assert got == ora.tokens.tolist()
+
+
+@pytest.mark.parametrize("mode", ["lib", "cli"])
+def test_generate_loop_matches_oracle(tmp_path, mode):
+    """The decode loop through the drop-in (tests/cpp/drop_in_test.cpp
+    generate mode): Gemma4Session::generate (src/generation.cpp:452-469) or the
+    CLI loop (src/main.cpp:138-146) over a table of logits rows, one
+    mt19937_64 across greedy and sampling steps, prompt + generated ids as the
+    penalty history, stop tokens {1, 106}. The oracle replays the same loop;
+    the step that lifts token 106 ends it (mode lib keeps the stop token in the
+    output, mode cli drops it), as core_tests.cpp:473-504 checks for greedy."""
+    rng = np.random.default_rng(41)
+    rows, vocab, seed, stop_step = 30, 262144, 1234, 23
+    x = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
+    peaks = rng.choice(np.arange(200, vocab), size=12, replace=False)
+    x[:, peaks] += 7.0  # recurring candidates: the penalty history matters
+    x[stop_step, 106] = 80.0
+    prompt = rng.integers(0, vocab, size=32).astype(np.int32)
+    temps = [1.0, 0.0, 0.7, 1.3, 0.0]
+    x.tofile(tmp_path / "rows.bin")
+    prompt.tofile(tmp_path / "prompt.bin")
+    got = _run(["generate", tmp_path / "rows.bin", rows, vocab, seed, tmp_path / "prompt.bin", prompt.size,
+                ",".join(str(t) for t in temps), mode])
+    eng = W.MT19937_64(seed)
+    hist = list(prompt)
+    want = []
+    for i in range(rows):
+        t = temps[i % len(temps)]
+        u = W.canonical_float(eng()) if t > 0 else 0.0
+        h = np.array(hist, np.int32)
+        ora = O.run(x[i:i + 1], O.make_params(temperature=t, top_k=64, top_p=0.95, softcap=30.0,
+                                              repetition_penalty=1.1),
+                    history=h, offsets=np.array([0, h.size], np.int32),
+                    uniforms=np.array([u], np.float32), nthreads=1)
+        tok = int(ora.tokens[0])
+        stop = tok in (1, 106)
+        if mode == "cli" and stop:
+            break
+        want.append(tok)
+        if stop:
+            break
+        hist.append(tok)
+    assert len(want) == stop_step + (1 if mode == "lib" else 0)
+    assert got == want
