@@ -13,6 +13,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/gemmaedge_sampler.h"
@@ -172,7 +173,8 @@ void ge_sampler_destroy(ge_sampler* s) {
 
 namespace {
 
-// The workspace one call runs on (a handle's buffers).
+// The workspace one call runs on: a handle's buffers (ge_sample) or the
+// static array (ge_sample_noalloc, which has no full-order workspace).
 struct Workspace {
     int device;
     int max_rows;
@@ -300,6 +302,50 @@ int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
     return GE_OK;
 }
 
+// ---- allocation-free entry point ---------------------------------------------
+//
+// The selection path's workspace for GE_NOALLOC_MAX_ROWS rows in a file-scope
+// device array: u32 tickets (zero between calls) in the first kTicketBytes,
+// then kSlotWords u64 list words per row. Each GPU the library runs on holds
+// its own copy until the process ends. Host code uses the array only through
+// the address hipGetSymbolAddress returns for the current device (its name is
+// a host-side stand-in, not a device address).
+constexpr size_t kTicketBytes = 4096;
+static_assert(GE_NOALLOC_MAX_ROWS * sizeof(uint32_t) <= kTicketBytes, "ticket area");
+constexpr size_t kScratchBytes =
+    kTicketBytes + static_cast<size_t>(GE_NOALLOC_MAX_ROWS) * ge::kSlotWords * sizeof(uint64_t);
+static_assert(kScratchBytes == GE_NOALLOC_SCRATCH_BYTES, "GE_NOALLOC_SCRATCH_BYTES");
+static __device__ __align__(256) uint64_t scratch[kScratchBytes / sizeof(uint64_t)];
+
+constexpr int kMaxDevices = 64;
+
+__global__ void clear_words(uint32_t* p, int n) {
+    const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n) p[i] = 0u;
+}
+
+// The array's address on `device` (current), found once per device; its
+// ticket area is cleared on `stream` the first time (a kernel, not a memset).
+int scratch_on(int device, hipStream_t stream, void** out) {
+    static std::mutex mu;
+    static void* ptr[kMaxDevices] = {};
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(GE_ERR_DEVICE, "hipGetSymbolAddress(scratch) returned NULL");
+        constexpr int kWords = static_cast<int>(kTicketBytes / sizeof(uint32_t));
+        hipLaunchKernelGGL(clear_words, dim3((kWords + 255) / 256), dim3(256), 0, stream,
+                           static_cast<uint32_t*>(p), kWords);
+        const hipError_t e2 = hipGetLastError();
+        if (e2 != hipSuccess) return hip_fail(e2, "clear scratch tickets");
+        ptr[device] = p;
+    }
+    *out = ptr[device];
+    return GE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -324,6 +370,26 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     ws.fo_capacity = s->fo_capacity;
     ws.fo_extras_cap = s->fo_extras_cap;
     ws.fo_bitmap_words = s->fo_bitmap_words;
+    return sample_on(ws, stream, *args);
+}
+
+int ge_sample_noalloc(void* stream, const ge_sample_args* args) {
+    if (!args) return fail(GE_ERR_INVALID_ARG, "args is NULL");
+    if (args->rows > GE_NOALLOC_MAX_ROWS)
+        return fail(GE_ERR_CAPACITY, "rows %d above GE_NOALLOC_MAX_ROWS (%d)", args->rows, GE_NOALLOC_MAX_ROWS);
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices)
+        return fail(GE_ERR_NO_DEVICE, "no current device");
+    if (!device_is_gfx950(device)) return fail(GE_ERR_NO_DEVICE, "device %d is not gfx950", device);
+    void* p = nullptr;
+    const int rc = scratch_on(device, static_cast<hipStream_t>(stream), &p);
+    if (rc != GE_OK) return rc;
+    Workspace ws{};
+    ws.device = device;
+    ws.max_rows = GE_NOALLOC_MAX_ROWS;
+    ws.max_vocab = static_cast<int>(kMaxChunkLen * ge::kMaxChunks);
+    ws.tickets = static_cast<uint32_t*>(p);
+    ws.slots = reinterpret_cast<uint64_t*>(static_cast<char*>(p) + kTicketBytes);
     return sample_on(ws, stream, *args);
 }
 

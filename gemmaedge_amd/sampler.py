@@ -37,6 +37,7 @@ GE_FLAG_DONE = 8
 GE_STOP_AFTER_PUSH = 0   # Gemma4Session::generate (src/generation.cpp:461-465)
 GE_STOP_BEFORE_PUSH = 1  # CLI decode loop (src/main.cpp:140-143)
 GE_MAX_STOP_TOKENS = 64
+GE_NOALLOC_MAX_ROWS = 512
 
 EXPORTS = (
     "ge_sampler_available",
@@ -45,6 +46,7 @@ EXPORTS = (
     "ge_sample",
     "ge_sampler_last_error",
     "ge_sampler_max_top_k",
+    "ge_sample_noalloc",
 )
 
 
@@ -115,6 +117,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     L.ge_sampler_last_error.argtypes = []
     L.ge_sampler_max_top_k.restype = ctypes.c_int
     L.ge_sampler_max_top_k.argtypes = []
+    L.ge_sample_noalloc.restype = ctypes.c_int
+    L.ge_sample_noalloc.argtypes = [ctypes.c_void_p, ctypes.POINTER(SampleArgs)]
     _lib = L
     return L
 

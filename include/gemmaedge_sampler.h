@@ -156,6 +156,23 @@ int ge_sample(ge_sampler* sampler, void* stream, const ge_sample_args* args);
 /* Thread-local message describing the last failure on this thread. */
 const char* ge_sampler_last_error(void);
 
+/* Allocation-free variant of ge_sample. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc). It runs on the
+ * calling thread's current device without a handle: the selection path's
+ * workspace is a device array of GE_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each GPU it runs on until the process ends. Limits: rows <=
+ * GE_NOALLOC_MAX_ROWS (else GE_ERR_CAPACITY) and no full-order workspace, so
+ * a call whose shared params need it (top_k == 0 or above
+ * ge_sampler_max_top_k() with a larger vocab) returns GE_ERR_CAPACITY, and
+ * with row_params such rows get token -1 and GE_FLAG_UNSUPPORTED. Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (two
+ * streams or threads at once) race and must not be issued. Stream-ordered and
+ * asynchronous like ge_sample; it calls no allocator. */
+#define GE_NOALLOC_MAX_ROWS 512
+#define GE_NOALLOC_SCRATCH_BYTES (4096 + GE_NOALLOC_MAX_ROWS * 2048 * 8) /* tickets + chunk lists: 8 MiB + 4 KiB */
+int ge_sample_noalloc(void* stream, const ge_sample_args* args);
+
 /* Largest top_k handled by the selection path of this build. Rows whose
  * effective k exceeds it (top_k disabled or larger, generation.cpp:80) take
  * the full-order path, for bf16 and fp32 logits alike. */
