@@ -50,8 +50,8 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--extras", default="C1,C3,C4,C4f32,C5",
-                    help="comma list of extra configs to report (C1,C3,C4,C4f32,C5) or ''")
+    ap.add_argument("--extras", default="C1,C2cold,C3,C4,C4f32,C5",
+                    help="comma list of extra configs to report (C1,C2cold,C3,C4,C4f32,C5) or ''")
     ap.add_argument("--c5-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -171,63 +171,132 @@ def read_traffic():
         return None
 
 
+def _oracle():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ge_oracle as O
+
+    return O
+
+
+def host_threads() -> int:
+    n = os.cpu_count() or 1
+    return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
+
+
+def oracle_pass(w, nthreads, history=None, offsets=None):
+    """One oracle pass over the workload's rows; returns (outputs, seconds)."""
+    O = _oracle()
+    if history is None and w.history.size:
+        history, offsets = w.history, w.offsets
+    t0 = time.perf_counter()
+    ora = O.run(w.logits, O.make_params(**w.params), history=history, offsets=offsets,
+                uniforms=w.uniforms, nthreads=nthreads)
+    return ora, time.perf_counter() - t0
+
+
+def parity_of(gpu_out, ora):
+    """Same-run parity against the oracle: token mismatches (lowest-index tie
+    rule), draws within 1e-6 of a CDF boundary (counted separately), and the
+    largest relative error of the selected probability."""
+    tokens, probs, flags = gpu_out
+    rel = np.abs(probs.astype(np.float64) - ora.probs) / np.maximum(np.abs(ora.probs), 1e-30)
+    bad = tokens != ora.tokens
+    near = ora.flags != 0
+    return {"rows": int(tokens.size), "token_mismatches": int(np.sum(bad)),
+            "token_mismatches_outside_boundary": int(np.sum(bad & ~near)),
+            "near_boundary_draws": int(np.sum(near)),
+            "max_prob_rel_err": float(np.nanmax(rel)) if rel.size else 0.0}
+
+
+def cpu_rate(w, seconds, nthreads, first=None):
+    """Oracle rows/s on `nthreads` host threads: passes over the workload's
+    rows repeated for about `seconds` (one pass at least)."""
+    if first is None:
+        _, first = oracle_pass(w, nthreads)
+    reps = max(1, int(seconds / max(first, 1e-3)))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        oracle_pass(w, nthreads)
+    dt = time.perf_counter() - t0
+    rows = reps * w.rows
+    return {"rows_per_s": rows / dt, "us_per_row": dt / rows * 1e6, "threads": nthreads,
+            "sample": f"{reps} pass(es) over the {w.rows}-row {w.name} batch ({rows} rows, {dt:.2f} s)"}
+
+
 def cpu_baseline_leg(w, seconds: float, gpu_out):
     """CPU baseline: the oracle over the same C2 rows, one row per thread on
     the host's cores (capped by OMP_NUM_THREADS), repeated for about `seconds`.
     Its outputs are also the same-run parity reference."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import ge_oracle as O
-
-    nthreads = os.cpu_count() or 1
-    nthreads = max(1, min(nthreads, int(os.environ.get("OMP_NUM_THREADS", nthreads))))
-    params = O.make_params(**w.params)
-    hist = w.history if w.history.size else None
-    offs = w.offsets if w.history.size else None
-    t0 = time.perf_counter()
-    ora = O.run(w.logits, params, history=hist, offsets=offs, uniforms=w.uniforms, nthreads=nthreads)
-    first = time.perf_counter() - t0
-    reps = max(1, int(seconds / max(first, 1e-3)))
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        O.run(w.logits, params, history=hist, offsets=offs, uniforms=w.uniforms, nthreads=nthreads)
-    dt = time.perf_counter() - t0
-    rows = reps * w.rows
-    base = {"value": rows / dt, "unit": "rows/s", "cores": nthreads, "kind": "port",
-            "sample": f"{reps} passes over the {w.rows}-row {w.name} batch ({rows} rows, "
-                      f"{dt:.1f} s wall), oracle/ge_oracle.cpp, one row per thread"}
-    tokens, probs, flags = gpu_out
-    rel = np.abs(probs.astype(np.float64) - ora.probs) / np.maximum(np.abs(ora.probs), 1e-30)
-    par = {"rows": int(w.rows), "token_mismatches": int(np.sum(tokens != ora.tokens)),
-           "near_boundary_draws": int(np.sum(ora.flags)),
-           "max_prob_rel_err": float(np.nanmax(rel)) if rel.size else 0.0}
-    return base, par
+    nthreads = host_threads()
+    ora, first = oracle_pass(w, nthreads)
+    r = cpu_rate(w, seconds, nthreads, first)
+    base = {"value": r["rows_per_s"], "unit": "rows/s", "cores": nthreads, "kind": "port",
+            "sample": r["sample"] + ", oracle/ge_oracle.cpp, one row per thread"}
+    return base, parity_of(gpu_out, ora)
 
 
 def bench_c1(torch, sampler, W):
-    out = {}
+    """Batch-1 latency (C1 and its greedy run). Returns (extras, {name: (workload, outputs)})."""
+    out, runs = {}, {}
     for greedy in (False, True):
         w = W.c1(greedy=greedy)
         b = Bound(sampler, w, torch)
+        gpu_out = b.run_once()
         d = kernel_durations_us(torch, b, 200)
         g, _ = timed_graph(torch, b, 200, 10)
-        out["C1_greedy" if greedy else "C1"] = {
+        name = "C1_greedy" if greedy else "C1"
+        out[name] = {
             "us_per_token_kernel_p50": float(np.median(d)),
             "us_per_token_kernel_p99": float(np.percentile(d, 99)),
             "us_per_token_graph_back_to_back": g / 200 * 1e6,
             "bytes_per_launch": w.bytes_per_row()}
-    return out
+        runs[name] = (w, gpu_out)
+    return out, runs
 
 
 def bench_throughput(torch, sampler, w, name):
+    """Rows/s of one config. Returns (extras, {name: (workload, outputs)})."""
     b = Bound(sampler, w, torch)
-    tok, _, flags = b.run_once()
-    if np.any(flags & 2):
-        return {name: {"status": "unsupported in this build (rows flagged GE_FLAG_UNSUPPORTED)"}}
+    gpu_out = b.run_once()
+    if np.any(gpu_out[2] & 2):
+        return {name: {"status": "unsupported in this build (rows flagged GE_FLAG_UNSUPPORTED)"}}, {}
     d = kernel_durations_us(torch, b, 30)
     bytes_launch = w.bytes_per_row() * w.rows
     gbs = bytes_launch / (np.mean(d) * 1e-6) / 1e9
-    return {name: {"rows": w.rows, "rows_per_s": w.rows / (np.mean(d) * 1e-6),
-                   "kernel_us": float(np.mean(d)), "GBps": gbs, "frac_peak": gbs / HBM_PEAK_GBS}}
+    return ({name: {"rows": w.rows, "rows_per_s": w.rows / (np.mean(d) * 1e-6),
+                    "kernel_us": float(np.mean(d)), "GBps": gbs, "frac_peak": gbs / HBM_PEAK_GBS}},
+            {name: (w, gpu_out)})
+
+
+def bench_c2_cold(torch, sampler, w, copies=5, steps=100):
+    """C2 with inputs that do not fit the 256 MB Infinity Cache: `copies`
+    distinct copies of the batch (5 x 67.6 MB), launch i reading copy i %
+    copies, all captured in one graph; average launch time from HIP events."""
+    b = Bound(sampler, w, torch)
+    bufs = [b.logits] + [b.logits.clone() for _ in range(copies - 1)]
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            cs = torch.cuda.current_stream().cuda_stream
+            for i in range(steps):
+                b.args.logits = bufs[i % copies].data_ptr()
+                b.launch(cs)
+    b.args.logits = bufs[0].data_ptr()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / steps
+    gbs = w.bytes_per_row() * w.rows / (us * 1e-6) / 1e9
+    return {"C2_cold": {"copies": copies, "resident_bytes": int(copies * b.logits.numel() * 4),
+                        "kernel_us": us, "GBps": gbs, "frac_peak": gbs / HBM_PEAK_GBS}}
 
 
 def c5_sweep(torch, sampler, W, steps):
@@ -277,6 +346,8 @@ def c5_sweep(torch, sampler, W, steps):
     stream = torch.cuda.current_stream()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     step_tokens = torch.empty(steps, dtype=torch.int32, device="cuda")
+    step_probs = torch.empty(steps, dtype=torch.float32, device="cuda")
+    step_flags = torch.empty(steps, dtype=torch.int32, device="cuda")
     torch.cuda.synchronize()
     for i in range(steps):
         logits.copy_(all_logits[i])
@@ -285,7 +356,10 @@ def c5_sweep(torch, sampler, W, steps):
         g.replay()
         ev[i][1].record(stream)
         step_tokens[i:i + 1].copy_(tokens)
+        step_probs[i:i + 1].copy_(probs)
+        step_flags[i:i + 1].copy_(flags)
     torch.cuda.synchronize()
+    gpu_out = (step_tokens.cpu().numpy(), step_probs.cpu().numpy(), step_flags.cpu().numpy())
     us = np.array([e0.elapsed_time(e1) * 1000.0 for e0, e1 in ev])
     out = {"steps": steps, "p50_us": float(np.median(us)), "p99_us": float(np.percentile(us, 99)),
            "mean_us": float(np.mean(us)), "history_len_final": int(ring_len.item())}
@@ -319,7 +393,13 @@ def c5_sweep(torch, sampler, W, steps):
         torch.cuda.synchronize()
     out["one_graph_us_per_step"] = e0.elapsed_time(e1) * 1000.0 / steps
     out["one_graph_tokens_match"] = bool(torch.equal(graph_tokens, step_tokens))
-    return out
+    # For the oracle: step i's history is the tokens sampled before it (the
+    # window never wraps: steps <= ring capacity).
+    toks = gpu_out[0]
+    lens = np.array([min(i, cap) for i in range(steps)], np.int64)
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    hist = np.concatenate([toks[max(0, i - cap):i] for i in range(steps)]).astype(np.int32)
+    return out, (w, gpu_out, hist, offs)
 
 
 def main():
@@ -369,29 +449,58 @@ def main():
     gpu_out = b.run_once()
 
     extras = {}
+    runs = {}  # name -> (workload, gpu outputs[, history, offsets]) for the same-run parity
     for name in [x for x in args.extras.split(",") if x]:
         log(f"extra {name}")
         try:
             if name == "C1":
-                extras.update(bench_c1(torch, sampler, W))
+                e, r = bench_c1(torch, sampler, W)
+            elif name == "C2cold":
+                e, r = bench_c2_cold(torch, sampler, w), {}
             elif name == "C3":
-                extras.update(bench_throughput(torch, sampler, W.c3(), "C3"))
+                e, r = bench_throughput(torch, sampler, W.c3(), "C3")
             elif name == "C4":
-                extras.update(bench_throughput(torch, sampler, W.c4(), "C4"))
+                e, r = bench_throughput(torch, sampler, W.c4(), "C4")
             elif name == "C4f32":
                 # not a BASELINE config: C4's rows kept in f32 (the f32 full-order path)
-                extras.update(bench_throughput(torch, sampler, W.c4(f32=True), "C4_f32"))
+                e, r = bench_throughput(torch, sampler, W.c4(f32=True), "C4_f32")
             elif name == "C5":
-                extras["C5"] = c5_sweep(torch, sampler, W, args.c5_steps)
-        except Exception as e:  # report, do not hide
-            extras[name] = {"error": repr(e)}
+                c5, run = c5_sweep(torch, sampler, W, args.c5_steps)
+                e, r = {"C5": c5}, {"C5": run}
+            else:
+                raise ValueError(f"unknown extra {name}")
+            extras.update(e)
+            runs.update(r)
+        except Exception as ex:  # report, do not hide
+            extras[name] = {"error": repr(ex)}
         torch.cuda.empty_cache()
 
-    cpu, par = None, None
+    cpu, parity = None, {}
     if not args.no_cpu_baseline:
         log("CPU baseline leg (oracle) ...")
-        cpu, par = cpu_baseline_leg(w, args.cpu_seconds, gpu_out)
-        log(f"C2 parity: {par}")
+        cpu, parity["C2"] = cpu_baseline_leg(w, args.cpu_seconds, gpu_out)
+        log(f"C2 parity: {parity['C2']}")
+        nthreads = host_threads()
+        per_config = {}
+        for name, run in runs.items():
+            rw, rout = run[0], run[1]
+            hist, offs = (run[2], run[3]) if len(run) > 2 else (None, None)
+            ora, first = oracle_pass(rw, nthreads, hist, offs)
+            parity[name] = parity_of(rout, ora)
+            log(f"{name} parity: {parity[name]}")
+            if hist is None:
+                per_config[name] = cpu_rate(rw, min(args.cpu_seconds / 4, 4.0), nthreads, first)
+            else:  # the decode sweep: its rows have growing histories
+                per_config[name] = {"rows_per_s": rw.rows / first, "us_per_row": first / rw.rows * 1e6,
+                                    "threads": nthreads,
+                                    "sample": f"one pass over the {rw.rows} decode steps ({first:.2f} s)"}
+        if "C1" in runs:
+            # The reference samples one row per token on one thread (its
+            # softcap loop alone is OpenMP-parallel): batch 1, single thread.
+            r1 = cpu_rate(runs["C1"][0], 2.0, 1)
+            per_config["C1_single_thread"] = {"us_per_token": r1["us_per_row"], "threads": 1,
+                                              "sample": r1["sample"]}
+        cpu["per_config"] = per_config
 
     result = {
         "metric": "sampler rows/s at V=262144, batch 64 (C2)",
@@ -413,7 +522,7 @@ def main():
                      "kernel": "select_kernel<float,64>", "kernel_us_mean": launch_us,
                      "kernel_us_isolated_p50": float(np.median(d)), "bytes_per_launch": bytes_launch},
         "cpu_baseline": cpu,
-        "parity": {"C2": par},
+        "parity": parity,
         "extras": extras,
     }
     print(json.dumps(result))
