@@ -57,7 +57,9 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target wall time of the oracle baseline sample")
     ap.add_argument("--profile-pass", action="store_true",
-                    help="short run for rocprofv3: C2 launches plus a copy-kernel calibration")
+                    help="short run for rocprofv3: --steps launches of one config plus a copy-kernel calibration")
+    ap.add_argument("--profile-config", default="C2", choices=["C1", "C1g", "C2", "C3", "C4", "C4f32", "C5"],
+                    help="config of the profile pass (C5: --steps consecutive decode steps on the device ring)")
     return ap.parse_args()
 
 
@@ -425,16 +427,23 @@ def main():
 
     if args.profile_pass:
         stream = torch.cuda.current_stream()
-        for _ in range(args.steps):
-            b.launch(stream.cuda_stream)
+        pc = args.profile_config
+        if pc == "C5":
+            c5_sweep(torch, sampler, W, args.steps)
+        else:
+            pw = {"C1": lambda: W.c1(), "C1g": lambda: W.c1(greedy=True), "C2": lambda: w, "C3": W.c3,
+                  "C4": W.c4, "C4f32": lambda: W.c4(f32=True)}[pc]()
+            pb = b if pc == "C2" else Bound(sampler, pw, torch)
+            for _ in range(args.steps):
+                pb.launch(stream.cuda_stream)
         torch.cuda.synchronize()
         src = torch.empty(256 * 2**20 // 4, dtype=torch.float32, device="cuda").fill_(1.0)
         dst = torch.empty_like(src)
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
-        log(f"profile pass: {args.steps} C2 launches, 5 copies of {src.numel() * 4} bytes")
-        print(json.dumps({"profile_pass": True, "c2_launches": args.steps, "copy_bytes": src.numel() * 4}))
+        log(f"profile pass: {args.steps} {pc} launches, 5 copies of {src.numel() * 4} bytes")
+        print(json.dumps({"profile_pass": True, "config": pc, "launches": args.steps, "copy_bytes": src.numel() * 4}))
         return
 
     log(f"timing {args.steps} steps (warmup {args.warmup})")

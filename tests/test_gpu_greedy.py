@@ -1,0 +1,113 @@
+"""GPU parity of the greedy path (temperature <= 0; the argmax kernel): the
+reference's std::max_element over the final logits (src/generation.cpp:66-70),
+first maximum, index 0 when logit 0 is NaN. Every case is compared with the
+oracle on the same logits and histories. The cases aim at what the kernel
+decides without evaluating the softcap on every token: equal final values
+from distinct raw values (the softcap's tie classes, common for large
+logits), penalised maxima (r > 1 lowers, r < 1 raises), NaN, bf16, batches,
+and chunks that hold several tokens of the winning tie class (rescanned)."""
+import numpy as np
+import pytest
+
+from gemmaedge_amd import workloads as W
+from gpu_util import assert_parity, run_gpu, run_oracle, small_workload
+
+pytestmark = pytest.mark.gpu
+
+V = 262144
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    import torch
+
+    from gemmaedge_amd import Sampler
+
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    s = Sampler(max_rows=64, max_vocab=V, max_history=8192)
+    yield s
+    s.close()
+
+
+def _check(sampler, w, label):
+    print(f"[greedy] {label} rows={w.rows} V={w.vocab} {w.dtype} {w.params}", flush=True)
+    gpu = run_gpu(sampler, w)
+    ora = run_oracle(w)
+    assert_parity(w, gpu, ora, label)
+    return gpu, ora
+
+
+def _rng(seed):
+    return np.random.Generator(np.random.Philox(seed))
+
+
+@pytest.mark.parametrize("center", [12.0, 45.0, 90.0, 400.0])
+def test_softcap_tie_classes(sampler, center):
+    """Large logits: neighbouring raw values cap to the same final value, so
+    the first maximum is the lowest index of a class of distinct raw values.
+    The class members are spread over several chunks, and some chunks hold
+    more than two of them (rescanned)."""
+    rng = _rng(int(center))
+    x = (rng.standard_normal(V, dtype=np.float32) * np.float32(2.0)).astype(np.float32)
+    top = np.float32(center)
+    idx = rng.choice(V, size=40, replace=False)
+    # members one to a few ulps below the top, several in one chunk of 1024
+    x[idx] = top - rng.integers(0, 6, size=idx.size).astype(np.float32) * np.spacing(top)
+    x[5000:5006] = top - np.arange(6, dtype=np.float32) * np.spacing(top)
+    x[300000 % V] = top
+    w = small_workload(f"ties{center}", x, dict(temperature=0.0, softcap=30.0))
+    _check(sampler, w, f"softcap ties at {center}")
+
+
+@pytest.mark.parametrize("r", [1.3, 0.7])
+def test_penalised_maximum(sampler, r):
+    """The largest raw logits are in the history: with r > 1 they fall below
+    unpenalised ones, with r < 1 a penalised token wins."""
+    rng = _rng(7)
+    x = (rng.standard_normal(V, dtype=np.float32) * np.float32(3.0)).astype(np.float32)
+    peaks = rng.choice(V, size=8, replace=False)
+    x[peaks] = np.float32(20.0) + np.arange(8, dtype=np.float32)
+    x[peaks[:3]] = -np.float32(25.0)  # negative penalised values move the other way
+    hist = np.concatenate([peaks[:6], peaks[:2], rng.integers(0, V, 100)]).astype(np.int32)
+    w = small_workload(f"pen{r}", x, dict(temperature=0.0, softcap=30.0, repetition_penalty=r),
+                       history=hist, offsets=np.array([0, hist.size], np.int32))
+    _check(sampler, w, f"penalised r={r}")
+
+
+def test_nan_rules(sampler):
+    rng = _rng(11)
+    base = (rng.standard_normal(V, dtype=np.float32)).astype(np.float32)
+    rows = np.stack([base.copy() for _ in range(4)])
+    rows[0, 0] = np.nan                       # logit 0 NaN: index 0
+    rows[1, 12345] = np.nan                   # NaN elsewhere never wins
+    rows[2, :] = np.nan                       # all NaN: index 0
+    rows[3, 7] = np.inf
+    rows[3, 9] = np.inf                       # first of two +inf
+    w = small_workload("nan", rows, dict(temperature=0.0, softcap=30.0))
+    _check(sampler, w, "NaN and inf rows")
+    # NaN penalty on token 0 makes its final value NaN
+    w = small_workload("nanpen", base, dict(temperature=0.0, repetition_penalty=float("nan")),
+                       history=np.array([0, 3], np.int32), offsets=np.array([0, 2], np.int32))
+    gpu, _ = _check(sampler, w, "NaN penalty on token 0")
+    assert gpu[0][0] == 0
+
+
+def test_batch_and_bf16(sampler):
+    w = W.c2(rows=64)
+    w.params = dict(w.params, temperature=0.0)
+    _check(sampler, w, "C2 rows greedy")
+    wb = W.c2(rows=16, seed=5)
+    wb.logits = W.f32_to_bf16_bits(wb.logits * np.float32(8.0))  # bf16: many equal values
+    wb.dtype = "bf16"
+    wb.params = dict(wb.params, temperature=0.0)
+    _check(sampler, wb, "bf16 rows greedy")
+
+
+@pytest.mark.parametrize("vocab", [1, 3, 1000, 4097, 70001])
+def test_small_and_ragged_vocab(sampler, vocab):
+    rng = _rng(vocab)
+    x = np.round(rng.standard_normal((3, vocab)) * 2.0).astype(np.float32)  # many exact ties
+    w = small_workload(f"v{vocab}", x, dict(temperature=0.0, softcap=30.0, repetition_penalty=1.2),
+                       history=rng.integers(0, vocab, 9).astype(np.int32),
+                       offsets=np.array([0, 3, 6, 9], np.int32))
+    _check(sampler, w, f"vocab {vocab}")
