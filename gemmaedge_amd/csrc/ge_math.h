@@ -29,6 +29,24 @@
 //
 // Every function here is evaluated with floating-point contraction off; the
 // fused operations are explicit fma() calls.
+//
+// Notices of the published sources whose algorithms and constants the
+// tanhf / expm1f and expf restatements follow:
+//
+//   fdlibm s_tanhf.c, s_expm1f.c (float conversion by Ian Lance Taylor,
+//   Cygnus Support):
+//   ====================================================
+//   Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//
+//   Developed at SunPro, a Sun Microsystems, Inc. business.
+//   Permission to use, copy, modify, and distribute this
+//   software is freely granted, provided that this notice
+//   is preserved.
+//   ====================================================
+//
+//   ARM optimized-routines math/expf.c:
+//   Copyright (c) 2017-2019, Arm Limited.
+//   SPDX-License-Identifier: MIT
 #pragma once
 
 #include <hip/hip_runtime.h>
