@@ -18,6 +18,11 @@
 
 #include "../../include/gemmaedge_sampler.h"
 #include "sampler_internal.h"
+#include "sampler_validate.h"
+
+static_assert(ge::kPlanBlock == ge::kBlock && ge::kPlanMaxTopK == ge::kMaxTopK &&
+                  ge::kPlanMaxChunks == ge::kMaxChunks && ge::kPlanMaxChunkLen == ge::kBlock * ge::kMaxEpt,
+              "plan and kernel geometry");
 
 struct ge_sampler {
     int device;
@@ -196,62 +201,17 @@ struct Workspace {
 // Validates the arguments against the workspace and launches the kernels on
 // `stream` (the caller has made ws.device current).
 int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
-    if (x.vocab < 1) return fail(GE_ERR_INVALID_ARG, "cannot sample empty logits");  // generation.cpp:63
-    if (!x.logits || !x.tokens_out) return fail(GE_ERR_INVALID_ARG, "logits or tokens_out is NULL");
-    if (x.dtype != GE_DTYPE_F32 && x.dtype != GE_DTYPE_BF16)
-        return fail(GE_ERR_INVALID_ARG, "dtype %d", x.dtype);
-    if (x.rows < 1) return fail(GE_ERR_INVALID_ARG, "rows %d", x.rows);
-    if (x.rows > ws.max_rows || x.vocab > ws.max_vocab)
-        return fail(GE_ERR_CAPACITY, "rows %d / vocab %d above capacity %d / %d", x.rows, x.vocab,
-                    ws.max_rows, ws.max_vocab);
-    if (x.row_stride < x.vocab) return fail(GE_ERR_INVALID_ARG, "row_stride %lld < vocab %d",
-                                            static_cast<long long>(x.row_stride), x.vocab);
-    if (x.ring) {
-        if (!x.ring_len || x.ring_capacity < 1)
-            return fail(GE_ERR_INVALID_ARG, "ring needs ring_len and ring_capacity >= 1");
-        if (x.history) return fail(GE_ERR_INVALID_ARG, "history and ring are exclusive");
-    }
-    if (x.history && !x.history_offsets) return fail(GE_ERR_INVALID_ARG, "history without offsets");
-    if (x.n_stop < 0 || x.n_stop > GE_MAX_STOP_TOKENS || (x.n_stop > 0 && !x.stop_tokens))
-        return fail(GE_ERR_INVALID_ARG, "n_stop %d (at most %d, with stop_tokens)", x.n_stop, GE_MAX_STOP_TOKENS);
-    if (x.stop_mode != GE_STOP_AFTER_PUSH && x.stop_mode != GE_STOP_BEFORE_PUSH)
-        return fail(GE_ERR_INVALID_ARG, "stop_mode %d", x.stop_mode);
-    const bool maybe_sampling = x.row_params != nullptr || !(x.params.temperature <= 0.0f);
-    if (maybe_sampling && !x.uniforms) return fail(GE_ERR_INVALID_ARG, "uniforms required when sampling");
-
-    // Rows with k > kMaxTopK (top-k disabled or large) take the full-order
-    // kernels.
-    bool run_select = true;
-    bool run_full = false;
-    if (!x.row_params) {
-        const ge_sample_params& p = x.params;
-        const uint32_t v = static_cast<uint32_t>(x.vocab);
-        const uint32_t k = p.temperature <= 0.0f ? 1u : (p.top_k ? (p.top_k < v ? p.top_k : v) : v);
-        if (k > static_cast<uint32_t>(ge::kMaxTopK)) {
-            run_select = false;
-            run_full = true;
-        }
-    } else {
-        run_full = x.vocab > ge::kMaxTopK;
-    }
-    if (run_full && !ws.fo_items) {
-        // With per-row parameters (on the device) the select kernel flags
-        // each row that needs the full-order path instead.
-        if (!x.row_params) return fail(GE_ERR_CAPACITY, "top_k %u needs the full-order workspace", x.params.top_k);
-        run_full = false;
-    }
-
-    // Launch geometry: 64 logits per thread when there are enough rows to fill
-    // the chip, else 16 so a single row still spreads over 64+ workgroups.
-    const int64_t chunks64 = (x.vocab + kMaxChunkLen - 1) / kMaxChunkLen;
-    const int64_t chunks16 = (x.vocab + ge::kBlock * 16 - 1) / (ge::kBlock * 16);
-    int ept = (static_cast<int64_t>(x.rows) * chunks64 >= 16 || chunks16 > ge::kMaxChunks) ? 64 : 16;
+    ge::CallPlan plan{};
+    char msg[256];
+    const int rc = ge::plan_call(x, ge::CallCapacity{ws.max_rows, ws.max_vocab, ws.fo_items != nullptr}, plan, msg,
+                                 sizeof(msg));
+    if (rc != GE_OK) return fail(rc, "%s", msg);
+    const bool run_select = plan.run_select;
+    const bool run_full = plan.run_full;
+    const int ept = plan.ept;
     const int chunk_len = ge::kBlock * ept;
-    const int cpr = static_cast<int>((x.vocab + chunk_len - 1) / chunk_len);
-
-    const size_t esize = x.dtype == GE_DTYPE_BF16 ? 2 : 4;
-    const bool vec_ok = (reinterpret_cast<uintptr_t>(x.logits) % 16 == 0) &&
-                        ((static_cast<uint64_t>(x.row_stride) * esize) % 16 == 0);
+    const int cpr = plan.cpr;
+    const bool vec_ok = plan.vec_ok;
 
     ge::DevArgs a{};
     a.logits = x.logits;
