@@ -251,6 +251,10 @@ int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
     a.fo_capacity = ws.fo_capacity;
 
     const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (plan.run_greedy) {
+        const hipError_t e = ge::launch_greedy(a, st, ept);
+        if (e != hipSuccess) return hip_fail(e, "launch (greedy)");
+    }
     if (run_select) {
         const hipError_t e = ge::launch_select(a, st, ept);
         if (e != hipSuccess) return hip_fail(e, "launch");

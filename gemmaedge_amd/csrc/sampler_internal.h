@@ -77,6 +77,24 @@ inline int64_t fo_items_stride(int max_history) {
 // boundary; the sort also uses the aux and pre arrays as two V-entry buffers.
 inline int64_t fo_items_stride_f32(int vocab) { return (static_cast<int64_t>(vocab) + 2 + 63) / 64 * 64; }
 
+// The row's parameters: the shared ones, or its entry of row_params.
+__device__ __forceinline__ ge_sample_params row_params(const DevArgs& a, int row) {
+    return a.row_params ? a.row_params[row] : a.params;
+}
+
+__device__ __forceinline__ void row_history(const DevArgs& a, int row, const int32_t*& h, int& n) {
+    h = nullptr;
+    n = 0;
+    if (a.ring) {
+        h = a.ring + static_cast<int64_t>(row) * a.ring_capacity;
+        n = min(max(a.ring_len[row], 0), a.ring_capacity);
+    } else if (a.history && a.history_offsets) {
+        const int s = a.history_offsets[row];
+        h = a.history + s;
+        n = max(a.history_offsets[row + 1] - s, 0);
+    }
+}
+
 // True when the row was finished by an earlier call (done[row] != 0): every
 // kernel skips it, and the one that owns the row reports it (skipped_row).
 __device__ __forceinline__ bool row_done(const DevArgs& a, int row) { return a.done && a.done[row] != 0; }
@@ -114,6 +132,10 @@ __device__ __forceinline__ void emit_row(const DevArgs& a, int row, int32_t toke
 // Launches the fused select/sample kernel for rows whose k <= kMaxTopK.
 // ept in {16, 64}. Returns a hipError_t.
 hipError_t launch_select(const DevArgs& a, hipStream_t stream, int ept);
+
+// Launches the greedy kernel (every row greedy, shared parameters): one pass,
+// ept in {16, 64}. Returns a hipError_t.
+hipError_t launch_greedy(const DevArgs& a, hipStream_t stream, int ept);
 
 // Launches the full-order kernels (rows with k > kMaxTopK; other rows are
 // skipped): one pair for bf16, one pair per slice of rows for f32. Returns a

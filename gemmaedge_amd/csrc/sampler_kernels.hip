@@ -47,6 +47,7 @@
 
 #include "ge_math.h"
 #include "sampler_internal.h"
+#include "tie_class.h"
 #include "wave_ops.h"
 
 #pragma clang fp contract(off)
@@ -150,23 +151,6 @@ __device__ __forceinline__ int opaque_tid() {
 
 __device__ __forceinline__ float load_one(const float* rowp, int i) { return rowp[i]; }
 __device__ __forceinline__ float load_one(const uint16_t* rowp, int i) { return bf16_to_f32(rowp[i]); }
-
-__device__ __forceinline__ ge_sample_params row_params(const DevArgs& a, int row) {
-    return a.row_params ? a.row_params[row] : a.params;
-}
-
-__device__ __forceinline__ void row_history(const DevArgs& a, int row, const int32_t*& h, int& n) {
-    h = nullptr;
-    n = 0;
-    if (a.ring) {
-        h = a.ring + static_cast<int64_t>(row) * a.ring_capacity;
-        n = min(max(a.ring_len[row], 0), a.ring_capacity);
-    } else if (a.history && a.history_offsets) {
-        const int s = a.history_offsets[row];
-        h = a.history + s;
-        n = max(a.history_offsets[row + 1] - s, 0);
-    }
-}
 
 // Exponent of the lowest set bit of a positive finite float.
 __device__ __forceinline__ int lsb_exponent(float e) {
@@ -369,108 +353,6 @@ __device__ __forceinline__ uint32_t block_kth_exact(uint32_t lo, uint32_t hi, ui
         width = shift - ns;
         shift = ns;
     }
-}
-
-// Called by one whole wave; every lane returns the same value: the smallest
-// raw key x <= tau with softcap(x) == softcap(tau). softcap is monotone
-// non-decreasing (glibc tanhf is monotone on all floats), so the keys with
-// equal capped value form an interval. Usually tau-1 already caps lower and
-// one evaluation round decides; otherwise a 64-way search finds the floor.
-// tie_floor with its first evaluation supplied: target = softcap(tau),
-// below = softcap(tau - 1) (both wave-uniform).
-__device__ __forceinline__ uint32_t tie_floor_given(uint32_t tau, float cap, float target, float below) {
-    if (!(cap > 0.0f) || tau <= kKeyNegInf) return tau;
-    if (below != target) return tau;
-    const int lane = __lane_id();
-    uint32_t hi = tau - 1;  // lowest key known to map to target
-    uint32_t lo;            // a key known to map below target
-    uint64_t step = 1;
-    for (;;) {
-        const uint64_t off = static_cast<uint64_t>(lane + 1) * step;
-        const uint32_t x = (static_cast<uint64_t>(hi - kKeyNegInf) > off)
-                               ? hi - static_cast<uint32_t>(off)
-                               : kKeyNegInf;
-        const bool eq = softcap(key_value(x), cap) == target;
-        const uint64_t ne = __ballot(!eq);
-        if (ne) {
-            const int j = __ffsll(static_cast<unsigned long long>(ne)) - 1;
-            const uint32_t xj = wave::readlane(x, j);
-            const uint32_t xp = wave::readlane(x, j > 0 ? j - 1 : 0);
-            lo = xj;
-            hi = j > 0 ? xp : hi;
-            break;
-        }
-        hi = wave::readlane(x, 63);
-        if (hi == kKeyNegInf) return kKeyNegInf;
-        step *= 64;
-    }
-    while (hi - lo > 1) {
-        const uint32_t span = hi - lo;
-        const uint32_t s = (span + 63u) / 64u;
-        const uint64_t off = static_cast<uint64_t>(lane + 1) * s;
-        const uint32_t x = off < span ? lo + static_cast<uint32_t>(off) : hi;
-        const bool eq = softcap(key_value(x), cap) == target;
-        const uint64_t m = __ballot(eq);  // non-empty: lanes probing hi match
-        const int j = __ffsll(static_cast<unsigned long long>(m)) - 1;
-        const uint32_t xj = wave::readlane(x, j);
-        const uint32_t xp = wave::readlane(x, j > 0 ? j - 1 : 0);
-        lo = j > 0 ? xp : lo;
-        hi = xj;
-    }
-    return hi;
-}
-
-__device__ __forceinline__ uint32_t tie_floor(uint32_t tau, float cap) {
-    if (!(cap > 0.0f) || tau <= kKeyNegInf) return tau;
-    const int lane = __lane_id();
-    const float s01 = softcap(key_value(tau - static_cast<uint32_t>(lane & 1)), cap);
-    return tie_floor_given(tau, cap, u2f(wave::readlane(f2u(s01), 0)), u2f(wave::readlane(f2u(s01), 1)));
-}
-
-// Mirror of tie_floor: the largest raw key x >= r with softcap(x) ==
-// softcap(r). One whole wave; every lane returns the same value.
-__device__ __forceinline__ uint32_t tie_ceil(uint32_t r, float cap) {
-    if (!(cap > 0.0f) || r < kKeyNegInf || r >= kKeyPosInf) return r;
-    const int lane = __lane_id();
-    const float s01 = softcap(key_value(r + static_cast<uint32_t>(lane & 1)), cap);
-    const float target = u2f(wave::readlane(f2u(s01), 0));
-    if (u2f(wave::readlane(f2u(s01), 1)) != target) return r;
-    uint32_t lo = r + 1;  // highest key known to map to target
-    uint32_t hi;          // a key known to map above target
-    uint64_t step = 1;
-    for (;;) {
-        const uint64_t off = static_cast<uint64_t>(lane + 1) * step;
-        const uint32_t x = (static_cast<uint64_t>(kKeyPosInf - lo) > off)
-                               ? lo + static_cast<uint32_t>(off)
-                               : kKeyPosInf;
-        const bool eq = softcap(key_value(x), cap) == target;
-        const uint64_t ne = __ballot(!eq);
-        if (ne) {
-            const int j = __ffsll(static_cast<unsigned long long>(ne)) - 1;
-            const uint32_t xj = wave::readlane(x, j);
-            const uint32_t xp = wave::readlane(x, j > 0 ? j - 1 : 0);
-            hi = xj;
-            lo = j > 0 ? xp : lo;
-            break;
-        }
-        lo = wave::readlane(x, 63);
-        if (lo == kKeyPosInf) return kKeyPosInf;
-        step *= 64;
-    }
-    while (hi - lo > 1) {
-        const uint32_t span = hi - lo;
-        const uint32_t s = (span + 63u) / 64u;
-        const uint64_t off = static_cast<uint64_t>(lane + 1) * s;
-        const uint32_t x = off < span ? lo + static_cast<uint32_t>(off) : hi;
-        const bool eq = softcap(key_value(x), cap) == target;
-        const uint64_t nm = __ballot(!eq);  // non-empty: lanes probing hi differ
-        const int j = __ffsll(static_cast<unsigned long long>(nm)) - 1;
-        const uint32_t xj = wave::readlane(x, j);
-        const uint32_t xp = wave::readlane(x, j > 0 ? j - 1 : 0);
-        lo = j > 0 ? xp : lo;
-        hi = xj;
-    }
-    return lo;
 }
 
 // Descending bitonic sort of s[0, n), n a power of two <= kStage, by the

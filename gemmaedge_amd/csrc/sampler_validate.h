@@ -32,7 +32,8 @@ struct CallCapacity {
 struct CallPlan {
     bool run_select;
     bool run_full;
-    int ept;        // logits per thread of the selection pass (16 or 64)
+    bool run_greedy;  // every row greedy (shared parameters, temperature <= 0)
+    int ept;        // logits per thread of the selection or greedy pass (16 or 64)
     int cpr;        // chunks per row
     bool vec_ok;    // rows 16-byte aligned: vector loads
 };
@@ -82,6 +83,8 @@ inline int plan_call(const ge_sample_args& x, const CallCapacity& cap, CallPlan&
     // both kernels run and each serves its own rows.
     plan.run_select = true;
     plan.run_full = false;
+    plan.run_greedy = !x.row_params && x.params.temperature <= 0.0f;
+    if (plan.run_greedy) plan.run_select = false;
     if (!x.row_params) {
         const ge_sample_params& p = x.params;
         const uint32_t v = static_cast<uint32_t>(x.vocab);
@@ -106,6 +109,9 @@ inline int plan_call(const ge_sample_args& x, const CallCapacity& cap, CallPlan&
     const int64_t chunks64 = (x.vocab + kPlanMaxChunkLen - 1) / kPlanMaxChunkLen;
     const int64_t chunks16 = (x.vocab + kPlanBlock * 16 - 1) / (kPlanBlock * 16);
     plan.ept = (static_cast<int64_t>(x.rows) * chunks64 >= 16 || chunks16 > kPlanMaxChunks) ? 64 : 16;
+    // The greedy pass has no list merge: its cost per chunk is a round trip,
+    // so smaller chunks (more workgroups) pay while the grid stays resident.
+    if (plan.run_greedy) plan.ept = (static_cast<int64_t>(x.rows) * chunks16 <= 2048 && chunks16 <= kPlanMaxChunks) ? 16 : 64;
     const int64_t chunk_len = static_cast<int64_t>(kPlanBlock) * plan.ept;
     plan.cpr = static_cast<int>((x.vocab + chunk_len - 1) / chunk_len);
     if (plan.cpr > kPlanMaxChunks)

@@ -118,6 +118,10 @@ void check_validation() {
     expect(run(a, cap) == GE_ERR_INVALID_ARG, "sampling without uniforms");
     a.params.temperature = 0.0f;
     expect(run(a, cap) == GE_OK, "greedy without uniforms");
+    expect(plan.run_greedy && !plan.run_select && !plan.run_full, "shared greedy parameters take the greedy pass");
+    a.row_params = reinterpret_cast<const ge_sample_params*>(logits);
+    a.uniforms = reinterpret_cast<const float*>(logits);
+    expect(run(a, cap) == GE_OK && !plan.run_greedy && plan.run_select, "per-row parameters take the selection pass");
     a = base();
     a.vocab = 2000;
     a.row_stride = 2000;
