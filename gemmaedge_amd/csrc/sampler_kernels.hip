@@ -480,6 +480,17 @@ struct RowCtx {
     float cap;
 };
 
+// Slot layout extension of the lean rows (see merge_lean): the list's final
+// keys at words [fin, fin + L) and the capped value key of the j1-th entry
+// at word `bound`, next to [guarantee, count, raw entries (at most L)].
+struct LeanList {
+    bool on;
+    uint32_t j1;     // merge level 1
+    uint32_t cap;    // L: entries a lean list may hold
+    uint32_t fin;    // word of the first final key
+    uint32_t bound;  // word of the capped j1-th entry
+};
+
 // Builds the chunk's penalty bitmap in pbits (one bit per element of
 // [c0, c0 + CHUNK)) from the row's history. Block-uniform (barriers).
 template <int CHUNK>
@@ -854,7 +865,7 @@ __device__ __forceinline__ void seg_gather(uint64_t* stage, const uint32_t (&cnt
 // so the top m of the staged entries is the chunk's top m.
 template <typename T, int EPT>
 __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_t m, uint32_t* pbits,
-                                               SelShared& sh, uint64_t* slot, uint32_t stride,
+                                               SelShared& sh, uint64_t* slot, uint32_t stride, const LeanList& ll,
                                                uint32_t& n_top, uint32_t& n_out, bool& direct, bool& ok) {
     constexpr int W = sizeof(T) == 4 ? 4 : 8;  // elements per 16-byte load
     constexpr int NV = EPT / W;                 // 16-byte loads per thread
@@ -1090,6 +1101,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
         n_out = n_top;
         direct = true;
         uint64_t g = 0ull;
+        uint32_t rank = 0xffffffffu;
         if (wave == 0) {
             const uint32_t b1 = cnt[0], b2 = b1 + cnt[1], b3 = b2 + cnt[2];
             const uint32_t i = static_cast<uint32_t>(lane);
@@ -1108,6 +1120,27 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
             if (i < n_c && r < m) store_shared(&slot[2u + r], x);
             const uint64_t hm = __ballot(i < n_c && r == m - 1u);
             if (hm) g = wave::readlane64(x, __ffsll(static_cast<unsigned long long>(hm)) - 1);
+            rank = r;
+        } else if (ll.on && wave == 1) {
+            // The candidates' final keys and capped raw keys, while wave 0
+            // ranks them (same candidate order as wave 0's lanes).
+            const uint32_t b1 = cnt[0], b2 = b1 + cnt[1], b3 = b2 + cnt[2];
+            const uint32_t i = static_cast<uint32_t>(lane);
+            if (i < n_c) {
+                const int w = (i >= b1 ? 1 : 0) + (i >= b2 ? 1 : 0) + (i >= b3 ? 1 : 0);
+                const uint32_t base = w == 0 ? 0u : (w == 1 ? b1 : (w == 2 ? b2 : b3));
+                const uint64_t e = entry_of(sh.stage[w * kSeg + (i - base)]);
+                const float f = softcap(key_value(static_cast<uint32_t>(e >> 32)), rc.cap);
+                sh.hist[i] = order_key((rc.pen && raw_entry_pen(e)) ? penalize(f, rc.r) : f);
+                sh.hist[64u + i] = order_key(f);
+            }
+        }
+        if (ll.on) {
+            __syncthreads();
+            if (wave == 0 && static_cast<uint32_t>(lane) < n_c) {
+                if (rank < m) store_shared(&slot[ll.fin + rank], static_cast<uint64_t>(sh.hist[lane]));
+                if (rank == ll.j1 - 1u) store_shared(&slot[ll.bound], static_cast<uint64_t>(sh.hist[64 + lane]));
+            }
         }
         return g;  // meaningful in wave 0, which publishes it
     }
@@ -1493,6 +1526,40 @@ __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge
     if (pos + 1 < keep && fabs(static_cast<double>(choice0) - c_at) < 1e-6) near = true;
     pos_out = pos;
     near_out = near;
+}
+
+// Rank by counting over per-wave segments, each padded with zero keys to a
+// multiple of 8 (four 16-byte broadcast reads per step); also stores term(x),
+// computed alongside the count, at ex[rank] for ranks below m.
+template <typename Term>
+__device__ __forceinline__ void seg_rank_expf(const uint64_t* stage, const uint32_t (&cnt)[kBlock / 64], uint32_t n,
+                                              uint32_t m, uint64_t* dst, Term&& term, float* ex) {
+    const int tid = threadIdx.x;
+    if (static_cast<uint32_t>(tid) < n) {
+        int w = 0;
+        uint32_t i = static_cast<uint32_t>(tid);
+        while (i >= cnt[w]) {
+            i -= cnt[w];
+            ++w;
+        }
+        const uint64_t x = stage[w * kSeg + i];
+        const float t = term(x);  // independent of the rank: overlaps it
+        uint32_t rk = 0;
+#pragma unroll
+        for (int v = 0; v < kBlock / 64; ++v) {
+            const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(stage + v * kSeg);
+            for (uint32_t j = 0; j < (cnt[v] + 7u) / 8u; ++j) {
+                const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
+                rk = add_greater4(rk, q0.x, q0.y, q1.x, q1.y, x);
+                rk = add_greater4(rk, q2.x, q2.y, q3.x, q3.y, x);
+            }
+        }
+        if (rk < m) {
+            dst[rk] = x;
+            ex[rk] = t;
+        }
+    }
+    __syncthreads();
 }
 
 // sh.top[0, nt) := the largest k distinct keys of sh.top[0, nt) and
@@ -1993,6 +2060,156 @@ __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, co
 }
 
 // A rescan of chunk c with m = k for the merge's fallback.
+// Lean merge for the common rows (LeanList::on: k <= 64, not greedy, no
+// penalty below 1), level j1 only and without a softcap: the chunks
+// published their entries' final keys and the capped value of their j1-th
+// entry. Every wave loads the chunks' counts, j1-th entries and capped bounds
+// and reduces the row bound G1 (the largest j1-th entry) and its capped value
+// B in registers; every thread loads one entry slot (chunk, position < j1)
+// with its final key. Each wave compacts its entries above G1 (every element
+// outside them ends at or below B) into its LDS segment as final composite
+// keys; after the first barrier every thread ranks one entry over all
+// segments by counting and stores it and its expf term at its rank when
+// below k; after the second the top k is certified (its k-th final value
+// above B, so nothing outside can reach or tie it) and wave 0 runs the
+// reference's normalisation, min-p / top-p and draw (generation.cpp:89-126).
+// Returns false (block-uniform, nothing written) when the lists do not
+// certify; the caller then runs the full merge, which reloads them.
+template <typename T>
+__device__ __forceinline__ bool merge_lean(const DevArgs& a, SelShared& sh, const RowCtx& rc,
+                                           const ge_sample_params& p, uint32_t k, const LeanList& ll,
+                                           uint32_t stride, float u, uint32_t ej, uint32_t ec) {
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const int wave = tid >> 6;
+    const uint32_t cpr = static_cast<uint32_t>(a.cpr);
+    const uint32_t j1 = ll.j1;
+    const uint64_t* slot_row = a.slots + static_cast<int64_t>(rc.row) * kSlotWords;
+
+    // 1. One round trip: per wave the chunks' headers (lane c: chunk c), per
+    //    thread one entry slot (chunk t % cpr, position t / cpr < j1) with its
+    //    chunk's count and its final key, and the expf table.
+    const bool hl = static_cast<uint32_t>(lane) < cpr;
+    const uint32_t hbase = static_cast<uint32_t>(lane) * stride;
+    const uint64_t hg = hl ? load_shared(&slot_row[hbase]) : 0ull;
+    const uint64_t hc = hl ? load_shared(&slot_row[hbase + 1u]) : 0ull;
+    const uint64_t hj = hl ? load_shared(&slot_row[hbase + 1u + j1]) : 0ull;
+    const uint64_t hb = hl ? load_shared(&slot_row[hbase + ll.bound]) : 0ull;
+    const bool es = ej < j1;
+    const uint32_t ebase = ec * stride;
+    const uint64_t er = es ? load_shared(&slot_row[ebase + 2u + ej]) : 0ull;
+    const uint64_t ef = es ? load_shared(&slot_row[ebase + ll.fin + ej]) : 0ull;
+    const uint64_t en = es ? load_shared(&slot_row[ebase + 1u]) : 0ull;
+    const uint64_t et = tid < 32 ? exp2_table(static_cast<uint32_t>(tid)) : 0ull;
+    const float inv_temp = 1.0f / p.temperature;
+    if (tid < 32) sh.exp_tab[tid] = et;
+    // 2. G1 and B: over the chunks that listed j1 or more (a chunk that
+    //    listed fewer listed everything). A failed chunk needs the full merge.
+    if (__any(hl && hg == kGuaranteeFailed)) return false;  // every wave alike
+    const bool lv = hl && static_cast<uint32_t>(hc) >= j1;
+    const uint64_t vj = lv ? hj : 0ull;
+    const uint32_t ghi = wave::max_u32(static_cast<uint32_t>(vj >> 32));
+    const uint32_t glo = wave::max_u32(static_cast<uint32_t>(vj >> 32) == ghi ? static_cast<uint32_t>(vj) : 0u);
+    const uint64_t g1 = (static_cast<uint64_t>(ghi) << 32) | glo;
+    const uint32_t bkey = wave::max_u32(lv ? static_cast<uint32_t>(hb) : 0u);
+    // 3. The entries above G1, as final composite keys, into stage[0, n):
+    //    each wave takes its range with one LDS atomic (the counter and the
+    //    maximum were cleared before the ticket's barrier); the row's largest
+    //    final key by an LDS atomic maximum.
+    const bool in = es && ej < static_cast<uint32_t>(en) && er > g1;
+    const uint32_t fk = static_cast<uint32_t>(ef);
+    const uint64_t mk = __ballot(in);
+    const uint32_t n_w = static_cast<uint32_t>(__popcll(mk));
+    const uint32_t kmax = wave::max_u32(in ? fk : 0u);
+    uint32_t base = 0u;
+    if (lane == 0 && n_w != 0u) {
+        base = atomicAdd(&sh.u32[kSegCount], n_w);
+        atomicMax(&sh.u32[8], kmax);
+    }
+    base = wave::readlane(base, 0);
+    if (in) sh.stage[base + lanes_below(mk)] = composite(fk, raw_entry_index(er));
+    __syncthreads();
+    // 4. Rank over stage[0, n); the top k and their expf terms by rank.
+    const uint32_t n = sh.u32[kSegCount];
+    if (n < k) return false;  // block-uniform
+    const float maximum = key_value(sh.u32[8]);
+    float* ex = reinterpret_cast<float*>(sh.list);
+    if (static_cast<uint32_t>(tid) < n) {
+        const uint64_t x = sh.stage[tid];
+        const float t = expf_glibc_tab((key_value(composite_key(x)) - maximum) * inv_temp,
+                                       [&](uint32_t i) { return sh.exp_tab[i]; });
+        // Four independent carry chains; blocks of 8 keys by 16-byte
+        // broadcast reads, the last block masked (words past n are stale).
+        const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(sh.stage);
+        uint32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+        const uint32_t full = n / 8u;
+        uint32_t j = 0;
+        for (; j + 2u <= full; j += 2u) {
+            const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
+            const ulonglong2 q4 = p2[4 * j + 4], q5 = p2[4 * j + 5], q6 = p2[4 * j + 6], q7 = p2[4 * j + 7];
+            r0 = add_greater4(r0, q0.x, q0.y, q1.x, q1.y, x);
+            r1 = add_greater4(r1, q2.x, q2.y, q3.x, q3.y, x);
+            r2 = add_greater4(r2, q4.x, q4.y, q5.x, q5.y, x);
+            r3 = add_greater4(r3, q6.x, q6.y, q7.x, q7.y, x);
+        }
+        if (j < full) {
+            const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
+            r0 = add_greater4(r0, q0.x, q0.y, q1.x, q1.y, x);
+            r1 = add_greater4(r1, q2.x, q2.y, q3.x, q3.y, x);
+            ++j;
+        }
+        if (8u * j < n) {
+            const uint32_t b = 8u * j;
+            uint64_t q[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[i] = b + static_cast<uint32_t>(i) < n ? sh.stage[b + static_cast<uint32_t>(i)] : 0ull;
+            r2 = add_greater4(r2, q[0], q[1], q[2], q[3], x);
+            r3 = add_greater4(r3, q[4], q[5], q[6], q[7], x);
+        }
+        const uint32_t rk = (r0 + r1) + (r2 + r3);
+        if (rk < k) {
+            sh.top[rk] = x;
+            ex[rk] = t;
+        }
+    }
+    __syncthreads();
+    // 5. Certified when the k-th final value is above B.
+    if (!(composite_key(sh.top[k - 1u]) > bkey)) return false;  // block-uniform
+    if (wave != 0) return true;
+    // 6. generation.cpp:89-126 over the k terms (wave 0).
+    const bool live = static_cast<uint32_t>(lane) < k;
+    const float e = live ? ex[lane] : 0.0f;
+    const bool bad = live && (!(e >= 0.0f) || __builtin_isinf(e));
+    const int lsb = (live && e > 0.0f && !bad) ? lsb_exponent(e) : INT_MAX;
+    const double s = wave_sum(static_cast<double>(e));
+    const int mn = wave_min_i(lsb);
+    const int ex2 = static_cast<int>((d2u(s) >> 52) & 0x7ffu) - 1023;
+    double den;
+    // Exact when every term is a multiple of 2^mn and the sum fits 53 bits
+    // above it: any order then equals the sequential sum.
+    if (!__any(bad) && s > 0.0 && !__builtin_isinf(s) && mn >= ex2 - 51) {
+        den = s;
+    } else {
+        den = 0.0;
+        for (uint32_t i = 0; i < k; ++i) den += static_cast<double>(readlane_f(e, static_cast<int>(i)));
+    }
+    const float inv_denom = static_cast<float>(1.0 / den);
+    const float pr = e * inv_denom;
+    float* scratch = ex + 64;  // 128 floats for the sequential chains
+    uint32_t pos;
+    bool near;
+    if (!__any(live && __builtin_isnan(pr))) {
+        scan_walk_wave(pr, k, p, u, scratch, pos, near);
+    } else {
+        scan_and_walk([&](uint32_t g) { return g == 0 ? pr : 0.0f; }, k, p, u, pos, near);
+    }
+    const float ppos = readlane_f(pr, static_cast<int>(pos));
+    if (lane == 0)
+        write_row(a, rc.row, static_cast<int32_t>(composite_index(sh.top[pos])), ppos,
+                  near ? GE_FLAG_NEAR_BOUNDARY : 0);
+    return true;
+}
+
 template <typename T, int EPT>
 __device__ __forceinline__ uint32_t rescan_chunk(const RowCtx& rc, int c, uint32_t k, uint32_t* pbits,
                                                  SelShared& sh, bool& ok) {
@@ -2061,10 +2278,25 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
                                     : min(static_cast<uint32_t>(kSlotWords / a.cpr), 2u * m + 24u);
     uint64_t* slot = a.slots + static_cast<int64_t>(row) * kSlotWords + static_cast<int64_t>(chunk) * stride;
 
+    // Lean rows (merge_lean): small k, no penalty below 1, every chunk's
+    // first j1 entries within one word per thread; the chunks also publish
+    // their entries' final keys.
+    LeanList ll;
+    ll.j1 = spec_level1(k, a.cpr, m);
+    ll.cap = (stride - 3u) / 2u;
+    ll.fin = 2u + ll.cap;
+    ll.bound = 2u + 2u * ll.cap;
+    ll.on = !greedy && k <= 64u && !pen_all && a.cpr <= 64 && m <= ll.cap &&
+            static_cast<uint32_t>(a.cpr) * ll.j1 <= static_cast<uint32_t>(kBlock);
+    // The entry slot this thread loads if its workgroup merges (chunk
+    // tid % cpr, position tid / cpr): the division runs while the logits load.
+    const uint32_t lean_j = static_cast<uint32_t>(tid) / static_cast<uint32_t>(a.cpr);
+    const uint32_t lean_c = static_cast<uint32_t>(tid) - lean_j * static_cast<uint32_t>(a.cpr);
+
     uint32_t n_top, n_out;
     bool direct, ok;
     const uint64_t gamma =
-        chunk_topm<T, EPT>(rc, chunk * CHUNK, m, s_pbits, sh, slot, stride, n_top, n_out, direct, ok);
+        chunk_topm<T, EPT>(rc, chunk * CHUNK, m, s_pbits, sh, slot, stride, ll, n_top, n_out, direct, ok);
 
     // Publish [guarantee, count, sorted entries] (a list ranked by one wave
     // or with appended penalised entries is already written), wait for the
@@ -2072,16 +2304,28 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
     // merges.
     if (tid == 0) {
         store_shared(&slot[0], gamma);
-        store_shared(&slot[1], static_cast<uint64_t>(min(n_out, stride - 2u)));
+        store_shared(&slot[1], static_cast<uint64_t>(min(n_out, ll.on ? ll.cap : stride - 2u)));
     }
-    if (!direct)
-        for (uint32_t i = tid; i < n_top; i += kBlock) store_shared(&slot[2u + i], sh.list[i]);
+    if (!direct) {
+        for (uint32_t i = tid; i < n_top; i += kBlock) {
+            const uint64_t e = sh.list[i];
+            store_shared(&slot[2u + i], e);
+            if (ll.on) {
+                const float f = softcap(key_value(static_cast<uint32_t>(e >> 32)), rc.cap);
+                store_shared(&slot[ll.fin + i],
+                             static_cast<uint64_t>(order_key((rc.pen && raw_entry_pen(e)) ? penalize(f, rc.r) : f)));
+                if (i == ll.j1 - 1u) store_shared(&slot[ll.bound], static_cast<uint64_t>(order_key(f)));
+            }
+        }
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
         const uint32_t ticket =
             __hip_atomic_fetch_add(&a.tickets[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         sh.u32[0] = ticket == static_cast<uint32_t>(a.cpr - 1) ? 1u : 0u;
+        sh.u32[kSegCount] = 0u;  // merge_lean's entry counter and maximum
+        sh.u32[8] = 0u;
     }
     __syncthreads();
     if (sh.u32[0] == 0u) return;
@@ -2090,6 +2334,10 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
     // their latency overlaps the collection.
     const float u = greedy ? 0.0f : a.uniforms[row];
     const float x0 = greedy ? load_one(static_cast<const T*>(rc.rowp), 0) : 0.0f;
+    if (ll.on) {
+        if (merge_lean<T>(a, sh, rc, p, k, ll, stride, u, lean_j, lean_c)) return;
+        __syncthreads();  // not certified: the full merge below reloads the lists
+    }
     uint32_t nt;
     const bool collected = static_cast<uint32_t>(a.cpr) * stride <= static_cast<uint32_t>(kBlock * kSmallWords)
                                ? merge_collect_small(a, sh, rc, k, spec_level1(k, a.cpr, m), stride, nt)
