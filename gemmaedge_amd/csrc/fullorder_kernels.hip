@@ -58,7 +58,9 @@ constexpr int kSpillCap = 512;
 constexpr uint64_t kSat = static_cast<uint64_t>(1) << 62;
 
 enum : uint32_t { kMetaItems = 0, kMetaExtras = 1, kMetaNan = 2, kMetaStatus = 3 };
-enum : uint32_t { kStatusOk = 0, kStatusTooManyPenalised = 1 };
+// kStatusFallback: items of a flagged bf16 row, made by the fallback sort;
+// kStatusSkip: a row the fallback pass leaves as the first pass wrote it.
+enum : uint32_t { kStatusOk = 0, kStatusTooManyPenalised = 1, kStatusFallback = 2, kStatusSkip = 3 };
 
 // ---- bf16 order-key bins ---------------------------------------------------
 
@@ -81,6 +83,9 @@ __device__ __forceinline__ uint32_t bin_word(uint32_t bin) { return bin & (kWord
 __device__ __forceinline__ uint32_t bin_shift(uint32_t bin) { return (bin >> 15) << 4; }
 
 // ---- small helpers ---------------------------------------------------------
+
+__device__ __forceinline__ float load_value(const float* rowp, int i) { return rowp[i]; }
+__device__ __forceinline__ float load_value(const uint16_t* rowp, int i) { return bf16_to_f32(rowp[i]); }
 
 __device__ __forceinline__ ge_sample_params params_of(const DevArgs& a, int row) {
     return a.row_params ? a.row_params[row] : a.params;
@@ -618,7 +623,8 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t act) {
     return m;
 }
 
-__global__ __launch_bounds__(kThreads) void fo_sort_f32_kernel(DevArgs a) {
+template <typename T>
+__global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
     __shared__ SortShared sh;
     const int tid = threadIdx.x;
     const int lane = __lane_id();
@@ -628,8 +634,18 @@ __global__ __launch_bounds__(kThreads) void fo_sort_f32_kernel(DevArgs a) {
     const ge_sample_params p = params_of(a, row);
     uint32_t k;
     if (!full_order_row(p, V, k) || row_done(a, row)) return;  // done rows: fo_decide_kernel reports them
+    if (a.fo_fallback) {
+        // Only rows the first pass flagged (its status word, at the call
+        // row); the decide kernel of this pass skips the others.
+        const uint32_t st = a.fo_meta[static_cast<int64_t>(a.fo_row0 + row) * 4 + kMetaStatus];
+        __syncthreads();  // every thread has read it before thread 0 may rewrite it below
+        if (st != kStatusTooManyPenalised) {
+            if (tid == 0) a.fo_meta[static_cast<int64_t>(row) * 4 + kMetaStatus] = kStatusSkip;
+            return;
+        }
+    }
 
-    const float* rowp = static_cast<const float*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
+    const T* rowp = static_cast<const T*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
     const int32_t* hist;
     int H;
     history_of(a, row, hist, H);
@@ -669,7 +685,7 @@ __global__ __launch_bounds__(kThreads) void fo_sort_f32_kernel(DevArgs a) {
 #pragma unroll
             for (int u = 0; u < kSortUnroll; ++u) {
                 const int i = base + 64 * u + lane;
-                x[u] = i < whi ? rowp[i] : 0.0f;
+                x[u] = i < whi ? load_value(rowp, i) : 0.0f;
                 bw[u] = (pen && i < whi) ? ld_l2(bitmap + (i >> 5)) : 0u;
             }
 #pragma unroll
@@ -789,7 +805,7 @@ __global__ __launch_bounds__(kThreads) void fo_sort_f32_kernel(DevArgs a) {
         meta[kMetaItems] = G;
         meta[kMetaExtras] = 0;
         meta[kMetaNan] = last_nan ? static_cast<uint32_t>(V) - ld_l2(istart + G - 1) : 0u;
-        meta[kMetaStatus] = kStatusOk;
+        meta[kMetaStatus] = a.fo_fallback ? kStatusFallback : kStatusOk;
     }
 }
 
@@ -1131,9 +1147,13 @@ __device__ uint32_t wave_partition_point(uint32_t lo, uint32_t hi, Pred pred) {
     return lo;
 }
 
-template <typename T>
+// T: the logits' type. kSorted: the items come from the sort kernel (every
+// token in them, penalised ones at their final values; raw keys are f32
+// order keys), else from the bf16 histogram (penalised tokens in the
+// extras, raw keys are bf16 bins).
+template <typename T, bool kSorted>
 __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
-    constexpr bool kF32 = sizeof(T) == 4;
+    constexpr bool kF32 = kSorted;
     __shared__ DecideShared sh;
     const int tid = threadIdx.x;
     const int lane = __lane_id();
@@ -1144,9 +1164,10 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     uint32_t k;
     if (!full_order_row(p, V, k)) return;
     if (row_done(a, row)) {  // finished by an earlier call: the first kernel skipped it too
-        if (tid == 0) skipped_row(a, row);
+        if (tid == 0 && !a.fo_fallback) skipped_row(a, row);
         return;
     }
+    if (a.fo_fallback && a.fo_meta[static_cast<int64_t>(row) * 4 + kMetaStatus] != kStatusFallback) return;
 
     const int32_t* hist;
     int H;
@@ -1169,7 +1190,10 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         }
         if (tid == 0) emit_row(a, row, token, prob, flags);
     };
-    if (meta[kMetaStatus] != kStatusOk) {
+    if (meta[kMetaStatus] != (a.fo_fallback ? kStatusFallback : kStatusOk)) {
+        // Too many unique penalised ids for the extras: the fallback pass
+        // re-samples the row (the caller launches it whenever a history may
+        // be that long).
         finish(-1, 0.0f, GE_FLAG_UNSUPPORTED);
         return;
     }
@@ -1468,7 +1492,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                 for (int h = 0; h < kW; ++h) w[h] = 0;
                 for (int h = 0; h < kPer; ++h) {
                     if (lo + h < V) {
-                        if constexpr (kF32) w[h] = f2u(rowp[lo + h]);
+                        if constexpr (sizeof(T) == 4) w[h] = f2u(rowp[lo + h]);
                         else w[h >> 1] |= static_cast<uint32_t>(rowp[lo + h]) << ((h & 1) * 16);
                         valid |= 1u << h;
                     }
@@ -1484,7 +1508,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             if constexpr (kF32) {
 #pragma unroll
                 for (int h = 0; h < kPer; ++h) {
-                    const float x = u2f(w[h]);
+                    const float x = sizeof(T) == 4 ? u2f(w[h]) : u2f(((w[h >> 1] >> ((h & 1) * 16)) & 0xFFFFu) << 16);
                     const uint32_t rk = order_key(x);
                     const bool m = nan_group ? (x != x) : (!((pw >> h) & 1u) && rk >= blo && rk <= bhi);
                     if (((valid >> h) & 1u) && m) mm |= 1u << h;
@@ -1492,7 +1516,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                 if (!nan_group) {
                     for (uint32_t b = pw; b; b &= b - 1u) {
                         const int h = __builtin_ctz(b);
-                        const float f = penalize(softcap(rowp[lo + h], cap), rpen);
+                        const float f = penalize(softcap(load_value(rowp, lo + h), cap), rpen);
                         if (order_key(f) == gkey) mm |= 1u << h;
                     }
                 }
@@ -1575,36 +1599,54 @@ DevArgs slice_rows(const DevArgs& a, int r0, int n) {
     s.tokens = a.tokens + r0;
     if (a.probs) s.probs = a.probs + r0;
     if (a.flags) s.flags = a.flags + r0;
+    if (a.done) s.done = a.done + r0;
+    s.fo_row0 = a.fo_row0 + r0;
     return s;
 }
 
 }  // namespace
 
-hipError_t launch_full_order(const DevArgs& a, hipStream_t stream) {
+namespace {
+
+// Rows [0, a.rows) through the sort-based kernels, as many per launch pair as
+// the workspace holds at the f32 stride (at least one, by construction).
+template <typename T>
+hipError_t sorted_pass(const DevArgs& a, hipStream_t stream) {
+    const int64_t stride = fo_items_stride_f32(a.vocab);
+    if (a.fo_capacity < stride) return hipErrorInvalidValue;
+    const int per = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.fo_capacity / stride, a.rows)));
+    for (int r0 = 0; r0 < a.rows; r0 += per) {
+        DevArgs s = slice_rows(a, r0, std::min(per, a.rows - r0));
+        s.fo_items_stride = stride;
+        hipLaunchKernelGGL(fo_sort_kernel<T>, dim3(s.rows), dim3(kThreads), 0, stream, s);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((fo_decide_kernel<T, true>), dim3(s.rows), dim3(kDThreads), 0, stream, s);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_full_order(const DevArgs& a, hipStream_t stream, bool penalised_overflow) {
     if (!a.fo_items) return hipErrorInvalidValue;
     if (a.dtype == GE_DTYPE_BF16) {
         hipLaunchKernelGGL(fo_hist_kernel, dim3(a.rows), dim3(kThreads), 0, stream, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(fo_decide_kernel<uint16_t>, dim3(a.rows), dim3(kDThreads), 0, stream, a);
-        return hipGetLastError();
-    }
-    // f32 rows need up to V items each: as many rows per launch pair as the
-    // workspace holds at that stride (at least one, by construction).
-    const int64_t stride = fo_items_stride_f32(a.vocab);
-    const int per = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.fo_capacity / stride, a.rows)));
-    if (a.fo_capacity < stride) return hipErrorInvalidValue;
-    for (int r0 = 0; r0 < a.rows; r0 += per) {
-        DevArgs s = slice_rows(a, r0, std::min(per, a.rows - r0));
-        s.fo_items_stride = stride;
-        hipLaunchKernelGGL(fo_sort_f32_kernel, dim3(s.rows), dim3(kThreads), 0, stream, s);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(fo_decide_kernel<float>, dim3(s.rows), dim3(kDThreads), 0, stream, s);
+        hipLaunchKernelGGL((fo_decide_kernel<uint16_t, false>), dim3(a.rows), dim3(kDThreads), 0, stream, a);
         e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        if (e != hipSuccess || !penalised_overflow) return e;
+        // Rows flagged for too many unique penalised ids: sorted items, as
+        // for f32 rows, then their draw again (the first pass wrote token -1
+        // and left their ring and done state alone).
+        DevArgs f = a;
+        f.fo_fallback = 1;
+        return sorted_pass<uint16_t>(f, stream);
     }
-    return hipSuccess;
+    return sorted_pass<float>(a, stream);
 }
 
 }  // namespace ge

@@ -184,6 +184,7 @@ struct Workspace {
     int device;
     int max_rows;
     int max_vocab;
+    int max_history;
     uint32_t* tickets;
     uint64_t* slots;
     uint64_t* fo_items;
@@ -260,7 +261,12 @@ int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
         if (e != hipSuccess) return hip_fail(e, "launch");
     }
     if (run_full) {
-        const hipError_t e = ge::launch_full_order(a, st);
+        // A bf16 row may hold more unique penalised ids than the extras
+        // workspace when its history can be that long: a device ring's
+        // capacity, else the handle's max_history.
+        const int64_t hmax = x.ring ? std::max<int64_t>(x.ring_capacity, ws.max_history) : ws.max_history;
+        const bool overflow = x.dtype == GE_DTYPE_BF16 && hmax > ws.fo_extras_cap;
+        const hipError_t e = ge::launch_full_order(a, st, overflow);
         if (e != hipSuccess) return hip_fail(e, "launch (full order)");
     }
     return GE_OK;
@@ -322,6 +328,7 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     ws.device = s->device;
     ws.max_rows = s->max_rows;
     ws.max_vocab = s->max_vocab;
+    ws.max_history = s->max_history;
     ws.tickets = s->tickets;
     ws.slots = s->slots;
     ws.fo_items = s->fo_items;

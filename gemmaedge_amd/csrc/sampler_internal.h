@@ -61,6 +61,11 @@ struct DevArgs {
     int32_t fo_extras_cap;        // <= kFoExtrasCap
     int64_t fo_bitmap_words;
     int64_t fo_capacity;          // items (and aux, pre entries) in the workspace
+    // Full-order fallback pass (bf16 rows with more unique penalised ids than
+    // fo_extras_cap): the sort-based kernels serve only the rows the first
+    // pass flagged. fo_row0: the first call row of a slice of rows.
+    int32_t fo_fallback;
+    int32_t fo_row0;
 };
 
 // Full-order path sizes.
@@ -140,6 +145,8 @@ hipError_t launch_greedy(const DevArgs& a, hipStream_t stream, int ept);
 // Launches the full-order kernels (rows with k > kMaxTopK; other rows are
 // skipped): one pair for bf16, one pair per slice of rows for f32. Returns a
 // hipError_t.
-hipError_t launch_full_order(const DevArgs& a, hipStream_t stream);
+// penalised_overflow: some bf16 row may hold more unique penalised ids than
+// fo_extras_cap (then a fallback pass re-samples exactly the rows that do).
+hipError_t launch_full_order(const DevArgs& a, hipStream_t stream, bool penalised_overflow);
 
 }  // namespace ge

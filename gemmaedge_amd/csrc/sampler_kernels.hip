@@ -533,7 +533,6 @@ __device__ __forceinline__ uint64_t chunk_slow(const RowCtx& rc, int c0, uint32_
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const T* rowp = static_cast<const T*>(rc.rowp);
     const int cend = min(c0 + CHUNK, rc.V);
-    const bool pen_all = !(rc.r >= 1.0f);
     ok = true;
     if (rc.pen) build_penalty_bitmap<CHUNK>(rc, c0, cend, tid, pbits);
     auto is_pen = [&](int e) -> bool {
@@ -577,9 +576,37 @@ __device__ __forceinline__ uint64_t chunk_slow(const RowCtx& rc, int c0, uint32_
         above = block_sum(above, sh);
     }
     const uint32_t q = R != 0u ? m - above : 0xffffffffu;  // class members to take
+    // Penalised tokens leave the raw order (a penalty below 1 can even lift
+    // one above every bound taken from raw values), so the penalised
+    // candidates are the top m penalised tokens by final value (ties at the
+    // m-th taken in index order): the chunk's top m lies in the union of
+    // that set and the unpenalised candidates above, at most 2m <= kStage
+    // entries, so this routine always completes.
+    auto pen_key = [&](float x) { return order_key(penalize(softcap(x, rc.cap), rc.r)); };
+    uint32_t pk = 0u;             // m-th largest penalised final key (0: fewer than m, all)
+    uint32_t pq = 0xffffffffu;    // penalised tokens of key pk to take
+    if (rc.pen) {
+        auto visit_pen = [&](auto&& f) {
+#pragma unroll 1
+            for (int v = 0; v < NV; ++v) {
+                float x[W];
+                load_group(v, x);
+                const int e0 = c0 + (v * kBlock + tid) * W;
+#pragma unroll
+                for (int j = 0; j < W; ++j)
+                    if (e0 + j < cend && is_pen(e0 + j)) f(pen_key(x[j]));
+            }
+        };
+        pk = block_kth_exact(1u, 0xffffffffu, m, visit_pen, sh);
+        if (pk != 0u) {
+            uint32_t pabove = 0;
+            visit_pen([&](uint32_t key) { pabove += key > pk ? 1u : 0u; });
+            pq = m - block_sum(pabove, sh);
+        }
+    }
     // Stage in index order: per group, the class ranks and the candidates'
     // positions are exclusive scans over the threads.
-    uint32_t cls_before = 0, n_c = 0;
+    uint32_t cls_before = 0, pcls_before = 0, n_c = 0;
 #pragma unroll 1
     for (int v = 0; v < NV; ++v) {
         float x[W];
@@ -598,13 +625,30 @@ __device__ __forceinline__ uint64_t chunk_slow(const RowCtx& rc, int c0, uint32_
         uint32_t cls_total;
         const uint32_t cbase = cls_before + block_excl_scan(static_cast<uint32_t>(__popc(cls)), cls_total, sh);
         cls_before += cls_total;
+        uint32_t pcls = 0, pbig = 0;  // penalised: final key == pk / > pk
+        if (pen != 0u && pk != 0u) {
+#pragma unroll
+            for (int j = 0; j < W; ++j) {
+                if (!((pen >> j) & 1u)) continue;
+                const uint32_t fk = pen_key(x[j]);
+                pcls |= static_cast<uint32_t>(fk == pk) << j;
+                pbig |= static_cast<uint32_t>(fk > pk) << j;
+            }
+        }
+        uint32_t pbase = 0;
+        if (pk != 0u) {
+            uint32_t pcls_total;
+            pbase = pcls_before + block_excl_scan(static_cast<uint32_t>(__popc(pcls)), pcls_total, sh);
+            pcls_before += pcls_total;
+        }
         uint32_t cand = 0;
 #pragma unroll
         for (int j = 0; j < W; ++j) {
             const uint32_t key = order_key(x[j]);
             bool c;
             if ((pen >> j) & 1u) {
-                c = pen_all || key >= lo;
+                c = pk == 0u || ((pbig >> j) & 1u) ||
+                    (((pcls >> j) & 1u) && pbase + static_cast<uint32_t>(__popc(pcls & ((1u << j) - 1u))) < pq);
             } else if ((cls >> j) & 1u) {
                 c = cbase + static_cast<uint32_t>(__popc(cls & ((1u << j) - 1u))) < q;
             } else {

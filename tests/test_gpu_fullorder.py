@@ -202,16 +202,52 @@ def test_per_row_params_mix_paths(sampler):
     assert np.array_equal(flags.cpu().numpy() & 1, ora.flags)
 
 
-def test_too_many_penalised_tokens_is_flagged(sampler):
+def test_more_penalised_tokens_than_extras(sampler):
+    # 9000 unique history ids exceed the histogram pass's 8192 extras: the
+    # row is re-sampled by the fallback pass (sorted items, as for f32 rows)
+    # and matches the oracle; nothing is flagged unsupported.
+    from gemmaedge_amd import sampler as S
+
     rng = np.random.default_rng(11)
     V = 40000
     x = _bf16(rng.standard_normal((1, V)).astype(np.float32))
     hist = rng.permutation(V)[:9000].astype(np.int32)  # 9000 unique ids > 8192
     w = small_workload("many-penalised", x, dict(temperature=1.0, top_k=0, repetition_penalty=1.2),
                        history=hist, offsets=np.array([0, hist.size], np.int32), dtype="bf16")
-    tokens, probs, flags = run_gpu(sampler, w)
-    assert tokens[0] == -1 and (flags[0] & 2)
+    gpu, _ = _check(sampler, w)
+    assert not (gpu[2][0] & S.GE_FLAG_UNSUPPORTED)
     # the history bitmap was restored: the next call on the same rows is exact
     w2 = small_workload("after-many", x, dict(temperature=1.0, top_k=0, repetition_penalty=1.2),
                         history=hist[:100], offsets=np.array([0, 100], np.int32), dtype="bf16")
     _check(sampler, w2)
+
+
+def test_penalised_overflow_rows_in_slices():
+    # A handle whose workspace holds one f32-stride row at a time: the
+    # fallback pass runs three slices. Rows 0 and 2 overflow the extras (10000
+    # unique ids), row 1 does not and keeps the first pass's result; row 2
+    # with penalty below 1.
+    import torch
+
+    from gemmaedge_amd import Sampler
+    from gemmaedge_amd import sampler as S
+
+    rng = np.random.default_rng(12)
+    V = W.VOCAB
+    x = _bf16((rng.standard_normal((3, V)) * 0.5).astype(np.float32))
+    lens = [10000, 300, 10000]
+    hist = np.concatenate([rng.permutation(V)[:n] for n in lens]).astype(np.int32)
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    for r in (1.3, 0.85):
+        w = small_workload(f"overflow-slices-r{r}", x, dict(temperature=1.0, top_k=0, top_p=0.95,
+                                                           softcap=30.0, repetition_penalty=r),
+                           history=hist, offsets=offs, uniforms=W.mt_uniforms(77, 3), dtype="bf16")
+        s = Sampler(max_rows=4, max_vocab=V, max_history=12000)
+        try:
+            gpu = run_gpu(s, w)
+            torch.cuda.synchronize()
+        finally:
+            s.close()
+        ora = run_oracle(w)
+        assert_parity(w, gpu, ora, w.name)
+        assert not np.any(gpu[2] & S.GE_FLAG_UNSUPPORTED), gpu[2]

@@ -249,3 +249,49 @@ def test_penalty_below_one_with_long_histories(sampler):
                                                      repetition_penalty=0.8),
                            history=hist, offsets=offs, uniforms=W.mt_uniforms(H, rows))
         _check(sampler, w)
+
+
+@pytest.mark.parametrize("k", [40, 1024])
+def test_penalty_below_one_dense_history(sampler, k):
+    # r < 1 with thousands of unique history ids inside one chunk: more
+    # penalised tokens than the exact chunk routine can stage. It keeps the
+    # chunk's top k penalised tokens by final value besides its top k
+    # unpenalised ones, so no row is refused (no GE_FLAG_UNSUPPORTED).
+    from gemmaedge_amd import sampler as S
+
+    rng = np.random.default_rng(1000 + k)
+    rows, V = 4, W.VOCAB
+    x = (rng.standard_normal((rows, V)) * 3).astype(np.float32)
+    H = 6000
+    hist = np.concatenate([
+        np.concatenate([16384 * (r + 1) + 500 + np.arange(5000), rng.integers(0, V, size=H - 5000)])
+        for r in range(rows)]).astype(np.int32)
+    offs = (np.arange(rows + 1) * H).astype(np.int32)
+    w = small_workload(f"pen0.8-dense-k{k}", x, dict(temperature=1.0 if k > 64 else 0.7, top_k=k,
+                                                      top_p=0.99 if k > 64 else 0.9, softcap=30.0,
+                                                      repetition_penalty=0.8),
+                       history=hist, offsets=offs, uniforms=W.mt_uniforms(k + 7, rows))
+    gpu, _ = _check(sampler, w)
+    assert not np.any(gpu[2] & S.GE_FLAG_UNSUPPORTED), gpu[2]
+
+
+def test_rescan_with_penalised_top_tokens(sampler):
+    # Sorted rows put the whole top k in the first chunk, so the merge
+    # rescans it with m = k; the history holds its 3000 largest tokens
+    # (r > 1 lowers them). The rescan keeps the top k penalised tokens by
+    # final value besides the top k unpenalised ones instead of every
+    # penalised token above the bound, so it fits and matches the oracle.
+    from gemmaedge_amd import sampler as S
+
+    rng = np.random.default_rng(4242)
+    rows, V = 2, W.VOCAB
+    x = np.ascontiguousarray(-np.sort((rng.standard_normal((rows, V)) * 3).astype(np.float32), axis=1))
+    H = 3000
+    hist = np.concatenate([np.arange(H), rng.integers(0, V, size=H)]).astype(np.int32)
+    offs = np.array([0, H, 2 * H], np.int32)
+    for k, r in ((1024, 1.2), (40, 1.5), (256, 0.9)):
+        w = small_workload(f"rescan-pen-k{k}-r{r}", x, dict(temperature=1.0, top_k=k, top_p=0.99, softcap=30.0,
+                                                             repetition_penalty=r),
+                           history=hist, offsets=offs, uniforms=W.mt_uniforms(k, rows))
+        gpu, _ = _check(sampler, w)
+        assert not np.any(gpu[2] & S.GE_FLAG_UNSUPPORTED), gpu[2]
