@@ -12,7 +12,11 @@ std::invalid_argument at :63).
 from __future__ import annotations
 
 import ctypes
+import dataclasses
+import math
 import os
+import re
+import struct
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
@@ -135,6 +139,10 @@ def max_top_k() -> int:
     return int(load_library().ge_sampler_max_top_k())
 
 
+# A decimal floating-point literal (what strtof reads, without hex, inf or nan).
+_DECIMAL = re.compile(r"[+-]?(?:[0-9]+\.?[0-9]*|\.[0-9]+)(?:[eE][+-]?[0-9]+)?")
+
+
 @dataclass
 class SamplingConfig:
     """include/gemmaedge/generation.h:55-61, plus softcap / penalty (defaults = reference)."""
@@ -150,6 +158,46 @@ class SamplingConfig:
     def params(self) -> SampleParams:
         return SampleParams(self.temperature, self.top_k, self.top_p, self.min_p, self.softcap,
                             self.repetition_penalty)
+
+    # Environment variables of include/gemmaedge/sampling_env.h (field, type).
+    ENV = {
+        "GEMMAEDGE_TEMPERATURE": ("temperature", float),
+        "GEMMAEDGE_TOP_K": ("top_k", int),
+        "GEMMAEDGE_TOP_P": ("top_p", float),
+        "GEMMAEDGE_MIN_P": ("min_p", float),
+        "GEMMAEDGE_SEED": ("seed", int),
+        "GEMMAEDGE_SOFTCAP": ("softcap", float),
+        "GEMMAEDGE_REPETITION_PENALTY": ("repetition_penalty", float),
+    }
+
+    @classmethod
+    def from_env(cls, base: "SamplingConfig | None" = None, environ=None) -> "SamplingConfig":
+        """A copy of ``base`` (default: the reference defaults) with the fields
+        the environment sets; unset, empty or malformed values are ignored,
+        as the reference's CLI ignores a malformed GEMMAEDGE_EXPERT_CACHE_GB
+        (src/main.cpp:109-115). Same rules as sampling_env.h: decimal floats
+        that are finite as float32, top_k within uint32, seed within uint64,
+        integers without sign; spaces and tabs around a value are allowed."""
+        env = os.environ if environ is None else environ
+        out = dataclasses.replace(base) if base is not None else cls()
+        for name, (field, typ) in cls.ENV.items():
+            text = (env.get(name) or "").strip(" \t")
+            if not text:
+                continue
+            if typ is float:
+                if not _DECIMAL.fullmatch(text):
+                    continue
+                try:
+                    v = struct.unpack("<f", struct.pack("<f", float(text)))[0]
+                except OverflowError:
+                    continue
+                if math.isfinite(v):
+                    setattr(out, field, v)
+            elif text.isascii() and text.isdigit():
+                v = int(text)
+                if v <= (2**32 - 1 if field == "top_k" else 2**64 - 1):
+                    setattr(out, field, v)
+        return out
 
 
 def _ptr(t) -> Optional[int]:

@@ -9,6 +9,9 @@
 //     over a stride of all float bit patterns, against the host's glibc;
 //   - the closed-form accumulation replay of chain_math.h against plain loops
 //     (tests/cpp/chain_check.hip, compiled here as host C++);
+//   - the drop-in's configuration from the environment
+//     (include/gemmaedge/sampling_env.h): defaults kept when unset or
+//     malformed, values taken when well formed;
 //   - the CPU oracle (oracle/ge_oracle.cpp) on random and edge-case batches:
 //     f32 and bf16, per-row parameters, histories with duplicates and
 //     out-of-range ids, NaN / inf rows, greedy, tiny vocabularies.
@@ -21,6 +24,7 @@
 
 #include "../../gemmaedge_amd/csrc/ge_math.h"
 #include "../../gemmaedge_amd/csrc/sampler_validate.h"
+#include "../../include/gemmaedge/sampling_env.h"
 #include "../../oracle/ge_oracle.h"
 
 extern "C" long long ge_test_chain_random(int which, unsigned long long seed, int trials);
@@ -216,10 +220,48 @@ void check_oracle() {
     expect(ge_oracle_sample_final(nullptr, 0, &p, 0.5f, nullptr) == -1, "empty logits rejected");
 }
 
+void check_env() {
+    const char* names[] = {"GEMMAEDGE_TEMPERATURE", "GEMMAEDGE_TOP_K", "GEMMAEDGE_TOP_P", "GEMMAEDGE_MIN_P",
+                           "GEMMAEDGE_SEED", "GEMMAEDGE_SOFTCAP", "GEMMAEDGE_REPETITION_PENALTY"};
+    for (const char* n : names) unsetenv(n);
+    const gemmaedge::SamplingConfig d{};
+    gemmaedge::SamplingConfig c = gemmaedge::sampling_config_from_env(d);
+    expect(c.temperature == d.temperature && c.top_k == d.top_k && c.top_p == d.top_p && c.min_p == d.min_p &&
+               c.seed == d.seed,
+           "env: defaults when unset");
+    setenv("GEMMAEDGE_TEMPERATURE", " 0.7 ", 1);
+    setenv("GEMMAEDGE_TOP_K", "40", 1);
+    setenv("GEMMAEDGE_TOP_P", "0.9", 1);
+    setenv("GEMMAEDGE_MIN_P", "0.05", 1);
+    setenv("GEMMAEDGE_SEED", "18446744073709551615", 1);
+    setenv("GEMMAEDGE_SOFTCAP", "30", 1);
+    setenv("GEMMAEDGE_REPETITION_PENALTY", "1.15", 1);
+    c = gemmaedge::sampling_config_from_env(d);
+    expect(c.temperature == 0.7f && c.top_k == 40u && c.top_p == 0.9f && c.min_p == 0.05f &&
+               c.seed == UINT64_MAX,
+           "env: values taken");
+    gemmaedge::SamplingExtras e = gemmaedge::sampling_extras_from_env(gemmaedge::SamplingExtras{});
+    expect(e.softcap == 30.0f && e.repetition_penalty == 1.15f, "env: extras taken");
+    const char* bad_float[] = {"", "  ", "abc", "0.5x", "nan", "inf", "1e99", "0.5 7"};
+    for (const char* v : bad_float) {
+        setenv("GEMMAEDGE_TOP_P", v, 1);
+        expect(gemmaedge::sampling_config_from_env(d).top_p == d.top_p, "env: malformed float ignored");
+    }
+    const char* bad_int[] = {"-1", "+3", "4294967296", "12.5", "0x10", "99999999999999999999", ""};
+    for (const char* v : bad_int) {
+        setenv("GEMMAEDGE_TOP_K", v, 1);
+        expect(gemmaedge::sampling_config_from_env(d).top_k == d.top_k, "env: malformed integer ignored");
+    }
+    setenv("GEMMAEDGE_TOP_K", "0", 1);
+    expect(gemmaedge::sampling_config_from_env(d).top_k == 0u, "env: top_k 0 (disabled) taken");
+    for (const char* n : names) unsetenv(n);
+}
+
 }  // namespace
 
 int main() {
     check_validation();
+    check_env();
     check_math();
     check_chains();
     check_oracle();
