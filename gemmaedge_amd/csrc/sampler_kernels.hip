@@ -43,6 +43,7 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <cstddef>
 #include <type_traits>
 
 #include "ge_math.h"
@@ -489,6 +490,12 @@ struct LeanList {
     uint32_t cap;    // L: entries a lean list may hold
     uint32_t fin;    // word of the first final key
     uint32_t bound;  // word of the capped j1-th entry
+    // Final-order lists (merge_fs, k above 64): the chunk publishes its top m
+    // by raw order as final composite keys sorted by final value, with the
+    // capped values of its m-th (word 0) and j1-th (last word of the slot)
+    // raw entries as bounds. The chunk's list then comes from LDS, not from
+    // the one-wave direct rank.
+    bool fs;
 };
 
 // Builds the chunk's penalty bitmap in pbits (one bit per element of
@@ -1136,7 +1143,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
         // Massive ties or a loose bound: the exact routine.
         return chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
     }
-    if (n_c <= 64u && !pen_all) {
+    if (n_c <= 64u && !pen_all && !ll.fs) {
         // 5. The usual case: wave 0 ranks the candidates by counting (exact
         //    64-bit keys read in pairs from LDS broadcasts, four pairs per
         //    step) and writes the sorted top m straight to the slot; the
@@ -1970,11 +1977,13 @@ __device__ __forceinline__ int next_rescan(const SelShared& sh, int c, int cpr, 
     return -1;
 }
 
-// Merge, second part: softmax / min-p / top-p / draw over sh.top[0, keff).
+// Merge, second part: softmax / min-p / top-p / draw over top[0, keff)
+// (composite final keys, sorted descending); prob: keff floats of LDS
+// scratch (at least 128) that do not overlap top.
 template <typename T>
 __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, const RowCtx& rc,
                                              const ge_sample_params& p, bool greedy, uint32_t keff,
-                                             float u, float x0) {
+                                             float u, float x0, const uint64_t* top, float* prob) {
     const int tid = threadIdx.x;
     const int lane = __lane_id();
     const int wave = tid >> 6;
@@ -1989,7 +1998,7 @@ __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, co
             // value is NaN (NaN < x is false). Token 0's final value is NaN
             // iff its raw value is, unless the penalty itself is NaN and 0
             // is in the history.
-            int32_t token = static_cast<int32_t>(composite_index(sh.top[0]));
+            int32_t token = static_cast<int32_t>(composite_index(top[0]));
             bool nan0 = __builtin_isnan(softcap(x0, rc.cap));
             if (!nan0 && rc.pen && __builtin_isnan(rc.r))
                 for (int j = 0; j < rc.H && !nan0; ++j) nan0 = rc.hist[j] == 0;
@@ -2000,18 +2009,17 @@ __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, co
     }
 
     // generation.cpp:89-101 — p_i = expf((v_i - max) * (1/T)); double denominator.
-    const float maximum = key_value(composite_key(sh.top[0]));
+    const float maximum = key_value(composite_key(top[0]));
     const float inv_temp = 1.0f / p.temperature;
     auto expf_lds = [&](float x) { return expf_glibc_tab(x, [&](uint32_t i) { return sh.exp_tab[i]; }); };
     const bool one_wave = keff <= 64u;
-    float* prob = reinterpret_cast<float*>(sh.stage);
     float pr_reg = 0.0f;  // one-wave path: this lane's probability
     bool any_nan;
     if (one_wave) {
         // One wave, probabilities in registers, no barriers.
         if (wave != 0) return;
         const bool live = lane < static_cast<int>(keff);
-        const uint64_t c = live ? sh.top[lane] : 0ull;
+        const uint64_t c = live ? top[lane] : 0ull;
         const float e = live ? expf_lds((key_value(composite_key(c)) - maximum) * inv_temp) : 0.0f;
         const bool bad = live && (!(e >= 0.0f) || __builtin_isinf(e));
         const int lsb = (live && e > 0.0f && !bad) ? lsb_exponent(e) : INT_MAX;
@@ -2034,7 +2042,7 @@ __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, co
         int lmin = INT_MAX;
         int bad = 0;
         for (uint32_t i = tid; i < keff; i += kBlock) {
-            const float v = key_value(composite_key(sh.top[i]));
+            const float v = key_value(composite_key(top[i]));
             const float e = expf_lds((v - maximum) * inv_temp);
             prob[i] = e;
             lsum += static_cast<double>(e);
@@ -2100,7 +2108,7 @@ __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, co
     else scan_and_walk(seg_prob, keff, p, u, pos, near);
     const float ppos = one_wave ? readlane_f(pr_reg, static_cast<int>(pos)) : prob[pos];
     if (lane == 0)
-        write_row(a, row, static_cast<int32_t>(composite_index(sh.top[pos])), ppos, near ? GE_FLAG_NEAR_BOUNDARY : 0);
+        write_row(a, row, static_cast<int32_t>(composite_index(top[pos])), ppos, near ? GE_FLAG_NEAR_BOUNDARY : 0);
 }
 
 // A rescan of chunk c with m = k for the merge's fallback.
@@ -2254,6 +2262,183 @@ __device__ __forceinline__ bool merge_lean(const DevArgs& a, SelShared& sh, cons
     return true;
 }
 
+// Merge for final-order lists (LeanList::fs: k above 64, no penalty below 1).
+// Each chunk listed its top m by raw order as final composite keys sorted by
+// final value, with B_c(m) and B_c(j1), the capped values of its m-th and
+// j1-th raw entries: every element it left out (or left out of its first j1)
+// ends at or below them. With B the largest bound of a level, the listed
+// entries above B are a prefix of every list and hold every element above B;
+// a 16-way merge of those prefixes (pairwise merge-path levels, each thread a
+// run of outputs after one co-rank search) sorts them, and the top k is
+// certified when its k-th final value is above B. Level j1 first, then level
+// m. Returns false (block-uniform, nothing written) when neither certifies or
+// a chunk failed.
+template <typename T>
+__device__ __forceinline__ bool merge_fs(const DevArgs& a, SelShared& sh, const RowCtx& rc,
+                                         const ge_sample_params& p, uint32_t k, const LeanList& ll,
+                                         uint32_t stride, float u) {
+    static_assert(offsetof(SelShared, top) == offsetof(SelShared, list) + kListCap * sizeof(uint64_t) &&
+                      kListCap + kMaxTopK >= kSlotWords + 2,
+                  "list and top form the merge's second buffer");
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const uint32_t cpr = static_cast<uint32_t>(a.cpr);
+    const uint32_t words = cpr * stride;  // <= kSlotWords
+    const uint32_t j1 = ll.j1;
+    const uint64_t* slot_row = a.slots + static_cast<int64_t>(rc.row) * kSlotWords;
+    constexpr int kPer = kSlotWords / kBlock;
+
+    // 1. One round trip: every slot word, mirrored into stage at its own
+    //    position (list c at c * stride + 2); per wave the chunks' headers
+    //    (lane c: chunk c); the expf table.
+    uint64_t w[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t g = static_cast<uint32_t>(i * kBlock + tid);
+        w[i] = g < words ? load_shared(&slot_row[g]) : 0ull;
+    }
+    const bool hl = static_cast<uint32_t>(lane) < cpr;
+    const uint32_t hbase = static_cast<uint32_t>(lane) * stride;
+    const uint64_t hg = hl ? load_shared(&slot_row[hbase]) : 0ull;
+    const uint64_t hc = hl ? load_shared(&slot_row[hbase + 1u]) : 0ull;
+    const uint64_t h1 = hl ? load_shared(&slot_row[hbase + stride - 1u]) : 0ull;
+    const uint64_t et = tid < 32 ? exp2_table(static_cast<uint32_t>(tid)) : 0ull;
+    if (tid < 32) sh.exp_tab[tid] = et;
+    auto mirror = [&]() {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const uint32_t g = static_cast<uint32_t>(i * kBlock + tid);
+            if (g < words) sh.stage[g] = w[i];
+        }
+    };
+    mirror();
+    if (__any(hl && hg == kGuaranteeFailed)) return false;  // every wave alike
+    // 2. The level bounds, in every wave: B(j1) over the chunks that listed
+    //    j1 or more (the others listed everything), B(m) over all.
+    const uint32_t cnt_c = hl ? static_cast<uint32_t>(hc) : 0u;
+    const uint32_t b1 = wave::max_u32((hl && cnt_c >= j1) ? static_cast<uint32_t>(h1) : 0u);
+    const uint32_t bm = wave::max_u32(hl ? static_cast<uint32_t>(hg) : 0u);
+    uint32_t levels = 0;
+    while ((1u << levels) < cpr) ++levels;
+    for (int lv = 0; lv < 2; ++lv) {
+        const uint32_t B = lv == 0 ? b1 : bm;
+        if (lv == 1) {
+            if (bm == b1) break;  // the same bound again
+            __syncthreads();      // the first try's reads are done
+            mirror();
+        }
+        __syncthreads();
+        // Prefix of list c above B (lists are in final order, keys distinct).
+        uint32_t s_c = 0;
+        if (hl) {
+            const uint64_t* lst = sh.stage + hbase + 2u;
+            uint32_t lo = 0, hi = cnt_c;
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (composite_key(lst[mid]) > B) lo = mid + 1;
+                else hi = mid;
+            }
+            s_c = lo;
+        }
+        const uint32_t incl = wave::incl_add(s_c);
+        const uint32_t n = wave::readlane(incl, 63);
+        if (n < k) continue;  // block-uniform
+        if (tid < 64 && hl) sh.cnt[lane] = incl - s_c;  // exclusive prefix
+        if (tid == 0) sh.cnt[cpr] = n;
+        __syncthreads();
+        // 3. Pairwise merge levels; the merge of chunks [c0, c2) lands at
+        //    c0 * stride + 2 of the other buffer.
+        const uint64_t* src = sh.stage;
+        uint64_t* dst = sh.list;
+        const uint32_t q = (n + kBlock - 1u) / kBlock;
+        for (uint32_t l = 0; l < levels; ++l) {
+            const uint32_t G = 1u << l;
+            const uint32_t nout = (cpr + 2u * G - 1u) / (2u * G);
+            uint32_t g = static_cast<uint32_t>(tid) * q;
+            const uint32_t gend = min(g + q, n);
+            while (g < gend) {
+                // the output list holding g: the largest i with start(i) <= g
+                uint32_t lo = 0, hi = nout;
+                while (hi - lo > 1u) {
+                    const uint32_t mid = (lo + hi) >> 1;
+                    if (sh.cnt[mid * 2u * G] <= g) lo = mid;
+                    else hi = mid;
+                }
+                const uint32_t c0 = lo * 2u * G, c1 = min(c0 + G, cpr), c2 = min(c0 + 2u * G, cpr);
+                const uint32_t base = sh.cnt[c0];
+                const uint32_t lenA = sh.cnt[c1] - base, lenB = sh.cnt[c2] - sh.cnt[c1];
+                const uint64_t* A = src + c0 * stride + 2u;
+                const uint64_t* Bp = src + c1 * stride + 2u;
+                uint64_t* out = dst + c0 * stride + 2u;
+                uint32_t o = g - base;
+                const uint32_t oend = min(gend - base, lenA + lenB);
+                uint32_t ca = o > lenB ? o - lenB : 0u, cb = min(o, lenA);
+                while (ca < cb) {  // co-rank: A's share of the first o outputs
+                    const uint32_t mid = (ca + cb) >> 1;
+                    if (A[mid] > Bp[o - mid - 1u]) ca = mid + 1u;
+                    else cb = mid;
+                }
+                uint32_t ia = ca, ib = o - ca;
+                uint64_t va = ia < lenA ? A[ia] : 0ull, vb = ib < lenB ? Bp[ib] : 0ull;
+                for (; o < oend; ++o) {
+                    if (va > vb) {
+                        out[o] = va;
+                        ++ia;
+                        va = ia < lenA ? A[ia] : 0ull;
+                    } else {
+                        out[o] = vb;
+                        ++ib;
+                        vb = ib < lenB ? Bp[ib] : 0ull;
+                    }
+                }
+                g = base + oend;
+            }
+            __syncthreads();
+            const uint64_t* t = src;
+            src = dst;
+            dst = const_cast<uint64_t*>(t);
+        }
+        // 4. Certified when the k-th final value is above B.
+        const uint64_t* top = src + 2;
+        if (!(composite_key(top[k - 1u]) > B)) continue;  // block-uniform
+        merge_finish<T>(a, sh, rc, p, false, k, u, 0.0f, top, reinterpret_cast<float*>(dst));
+        return true;
+    }
+    return false;
+}
+
+// Merge fallback for final-order lists: the top k of every listed entry into
+// sh.top[0, nt), and in sh.gam[c] a bound for chunk c as merge_all_lists
+// leaves it (a final composite key no element the chunk left out exceeds).
+__device__ __forceinline__ void merge_all_fs(const DevArgs& a, SelShared& sh, const RowCtx& rc, uint32_t k,
+                                             uint32_t stride, uint32_t& nt) {
+    const int tid = threadIdx.x;
+    constexpr int kPer = kSlotWords / kBlock;
+    uint64_t w[kPer];
+    uint32_t wp[kPer], wc[kPer];
+    load_slots(a, sh, rc.row, stride, w, wp, wc);
+    __syncthreads();
+    bool ent[kPer];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        ent[i] = slot_entry(sh, wp[i], wc[i]);
+        cnt += ent[i] ? 1u : 0u;
+    }
+    uint32_t n;
+    uint32_t pos = block_excl_scan(cnt, n, sh);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (ent[i]) sh.stage[pos++] = w[i];
+    __syncthreads();
+    for (int c = tid; c < a.cpr; c += kBlock) {
+        const uint64_t g = sh.gam[c];
+        if (g != 0ull && g != kGuaranteeFailed) sh.gam[c] = (g << 32) | 0xffffffffull;
+    }
+    __syncthreads();
+    nt = select_top(sh.stage, n, k, sh.top);
+}
+
 template <typename T, int EPT>
 __device__ __forceinline__ uint32_t rescan_chunk(const RowCtx& rc, int c, uint32_t k, uint32_t* pbits,
                                                  SelShared& sh, bool& ok) {
@@ -2332,6 +2517,8 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
     ll.bound = 2u + 2u * ll.cap;
     ll.on = !greedy && k <= 64u && !pen_all && a.cpr <= 64 && m <= ll.cap &&
             static_cast<uint32_t>(a.cpr) * ll.j1 <= static_cast<uint32_t>(kBlock);
+    ll.fs = !greedy && !ll.on && k > 64u && !pen_all && a.cpr <= 64 && m + 3u <= stride &&
+            m <= static_cast<uint32_t>(kBlock);
     // The entry slot this thread loads if its workgroup merges (chunk
     // tid % cpr, position tid / cpr): the division runs while the logits load.
     const uint32_t lean_j = static_cast<uint32_t>(tid) / static_cast<uint32_t>(a.cpr);
@@ -2346,11 +2533,43 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
     // or with appended penalised entries is already written), wait for the
     // stores, then one ticket per workgroup; the last workgroup of the row
     // merges.
-    if (tid == 0) {
+    if (ll.fs) {
+        // The list's final composite keys, ranked by final value; the capped
+        // values of the m-th and j1-th raw entries as the bounds.
+        const uint32_t i = static_cast<uint32_t>(tid);
+        uint64_t fc = 0ull;
+        if (i < n_top) {
+            const uint64_t e = sh.list[i];
+            const float f = softcap(key_value(static_cast<uint32_t>(e >> 32)), rc.cap);
+            const uint32_t kc = order_key(f);
+            fc = composite(order_key((rc.pen && raw_entry_pen(e)) ? penalize(f, rc.r) : f), raw_entry_index(e));
+            if (i == m - 1u) sh.u32[24] = kc;
+            if (i == ll.j1 - 1u) sh.u32[25] = kc;
+        }
+        sh.stage[i] = fc;  // zeros past n_top pad the rank's reads
+        __syncthreads();
+        if (i < n_top) {
+            const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(sh.stage);
+            uint32_t r0 = 0, r1 = 0;
+            for (uint32_t j = 0; j < (n_top + 7u) / 8u; ++j) {
+                const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
+                r0 = add_greater4(r0, q0.x, q0.y, q1.x, q1.y, fc);
+                r1 = add_greater4(r1, q2.x, q2.y, q3.x, q3.y, fc);
+            }
+            store_shared(&slot[2u + r0 + r1], fc);
+        }
+        if (tid == 0) {
+            const uint64_t g0 = gamma == kGuaranteeFailed ? kGuaranteeFailed
+                                                          : (gamma == 0ull ? 0ull : static_cast<uint64_t>(sh.u32[24]));
+            store_shared(&slot[0], g0);
+            store_shared(&slot[1], static_cast<uint64_t>(n_top));
+            store_shared(&slot[stride - 1u], static_cast<uint64_t>(n_top >= ll.j1 ? sh.u32[25] : 0u));
+        }
+    } else if (tid == 0) {
         store_shared(&slot[0], gamma);
         store_shared(&slot[1], static_cast<uint64_t>(min(n_out, ll.on ? ll.cap : stride - 2u)));
     }
-    if (!direct) {
+    if (!direct && !ll.fs) {
         for (uint32_t i = tid; i < n_top; i += kBlock) {
             const uint64_t e = sh.list[i];
             store_shared(&slot[2u + i], e);
@@ -2382,6 +2601,24 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
         if (merge_lean<T>(a, sh, rc, p, k, ll, stride, u, lean_j, lean_c)) return;
         __syncthreads();  // not certified: the full merge below reloads the lists
     }
+    if (ll.fs) {
+        if (merge_fs<T>(a, sh, rc, p, k, ll, stride, u)) return;
+        // Not certified: every listed entry, then exact rescans.
+        __syncthreads();
+        uint32_t nt;
+        merge_all_fs(a, sh, rc, k, stride, nt);
+        for (int c = next_rescan(sh, 0, a.cpr, nt, k); c >= 0; c = next_rescan(sh, c + 1, a.cpr, nt, k)) {
+            bool rok;
+            const uint32_t nl = rescan_chunk<T, EPT>(rc, c, k, s_pbits, sh, rok);
+            if (!rok) {
+                if (tid == 0) write_row(a, row, -1, 0.0f, GE_FLAG_UNSUPPORTED);
+                return;
+            }
+            nt = absorb_list(sh, nt, nl, k);
+        }
+        merge_finish<T>(a, sh, rc, p, false, min(nt, k), u, x0, sh.top, reinterpret_cast<float*>(sh.stage));
+        return;
+    }
     uint32_t nt;
     const bool collected = static_cast<uint32_t>(a.cpr) * stride <= static_cast<uint32_t>(kBlock * kSmallWords)
                                ? merge_collect_small(a, sh, rc, k, spec_level1(k, a.cpr, m), stride, nt)
@@ -2400,7 +2637,7 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
             nt = absorb_list(sh, nt, nl, k);
         }
     }
-    merge_finish<T>(a, sh, rc, p, greedy, min(nt, k), u, x0);
+    merge_finish<T>(a, sh, rc, p, greedy, min(nt, k), u, x0, sh.top, reinterpret_cast<float*>(sh.stage));
 }
 
 template <typename T, int EPT>
