@@ -38,6 +38,7 @@
 #include <climits>
 
 #include "chain_math.h"
+#include "chain_wave.h"
 #include "ge_math.h"
 #include "sampler_internal.h"
 
@@ -811,22 +812,20 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
 
 // ---- kernel 2: probabilities, exact chains, token ----------------------------
 
-struct ChainPos {
-    int item;       // item holding element `elem`
-    uint32_t elem;  // global element index (next to consume, or the event element)
-};
 
 // Item boundaries and addends: start(i) is the index of item i's first
 // element, start(G) the element count. One view reads LDS copies (rows whose
 // items fit), the other the global arrays; each is a single address space,
 // so the compiler emits ds_read or global_load rather than flat loads.
 struct LdsView {
+    static constexpr int kPerLane = 2;  // mostly binade crossings: shorter steps
     const uint32_t* pre;
     const float* add;
     __device__ __forceinline__ uint32_t start(int i) const { return pre[i]; }
     __device__ __forceinline__ float addend(int i) const { return add[i]; }
 };
 struct GlobalView {
+    static constexpr int kPerLane = 4;  // mostly plain steps: longer ones
     const uint32_t* pre;
     const float* add;
     __device__ __forceinline__ uint32_t start(int i) const { return pre[i]; }
@@ -942,124 +941,6 @@ __device__ bool wave_chain(const View& iv, int G, ChainPos& cp, uint32_t L, doub
         if (cp.elem >= L) return false;
         cp.item += 1;
     }
-    return false;
-}
-
-// The same walk for a float accumulator, in 32-bit integer arithmetic: the
-// accumulator is carried as its float bits, each item's increment comes from
-// the bit fields of its addend (chain_math.h step_bits), increments are capped
-// at 2^24 (more than any binade holds, so the cap never hides an exit) and
-// scanned as u32 with DPP. Each lane takes kPerLane consecutive items, so one
-// step covers 64 * kPerLane items.
-template <bool kDesc, typename View>
-__device__ bool wave_chain_f32(const View& iv, int G, ChainPos& cp, uint32_t L, double& s, double thr) {
-    // LDS rows (at most kStage items) are mostly binade crossings: shorter
-    // steps; global rows (up to V items) are mostly plain steps: longer ones.
-    constexpr int kPerLane = __is_same(View, LdsView) ? 2 : 4;
-    constexpr uint32_t kCap = 0x1000000u;
-    const int lane = __lane_id();
-    const uint32_t tb = f2u(static_cast<float>(thr));
-    uint32_t sb = f2u(static_cast<float>(s));
-    while (cp.elem < L && cp.item < G) {
-        const int i0 = cp.item + lane * kPerLane;
-        uint32_t bound[kPerLane + 1];
-#pragma unroll
-        for (int j = 0; j <= kPerLane; ++j) bound[j] = iv.start(min(i0 + j, G));
-        uint32_t ab[kPerLane];
-#pragma unroll
-        for (int j = 0; j < kPerLane; ++j) {  // G >= 1: the clamped read is in range
-            const uint32_t v = f2u(iv.addend(min(i0 + j, G - 1)));
-            ab[j] = i0 + j < G ? v : 0u;
-        }
-        const chain::StepBits bb = chain::binade_bits(sb);
-        const uint32_t tm = kDesc ? 0u : chain::threshold_bits(tb, bb.uexp);
-        uint32_t nt[kPerLane], lo_e[kPerLane], pre_in[kPerLane + 1];
-        bool evj[kPerLane];
-        pre_in[0] = 0;
-#pragma unroll
-        for (int j = 0; j < kPerLane; ++j) {
-            lo_e[j] = max(bound[j], cp.elem);
-            const uint32_t hi_e = min(bound[j + 1], L);
-            nt[j] = hi_e > lo_e[j] ? hi_e - lo_e[j] : 0u;
-            uint32_t D;
-            bool tie, big;
-            chain::step_bits(ab[j], bb.uexp, D, tie, big);
-            const uint32_t lo32 = nt[j] * D;
-            const uint32_t capped = (__umulhi(nt[j], D) != 0u || lo32 > kCap) ? kCap : lo32;
-            const uint32_t tot = big ? 0u : capped;  // nt = 0 gives 0
-            pre_in[j + 1] = pre_in[j] + tot;  // <= 4 * 2^24
-            evj[j] = nt[j] && (big || tie);
-        }
-        const uint32_t lane_tot = min(pre_in[kPerLane], kCap);
-        const uint32_t excl = wave_incl_u32(lane_tot) - lane_tot;  // <= 2^30
-        int jf = kPerLane;
-#pragma unroll
-        for (int j = kPerLane - 1; j >= 0; --j) {
-            const uint32_t after = excl + pre_in[j + 1];
-            bool e = evj[j];
-            if (nt[j]) e = e || (kDesc ? bb.m < bb.lo + after : (bb.m + after > chain::kHiF || bb.m + after >= tm));
-            if (e) jf = j;
-        }
-        const uint64_t evmask = __ballot(jf < kPerLane);
-        const int f = evmask ? static_cast<int>(__builtin_ctzll(evmask)) : 64;
-        if (f == 64) {
-            const uint32_t total = rl32(excl + lane_tot, 63);
-            const uint32_t m2 = kDesc ? bb.m - total : bb.m + total;
-            sb = (sb >> 23) <= 1u ? m2 : ((sb & 0x7F800000u) | (m2 & 0x7FFFFFu));
-            const int next = cp.item + 64 * kPerLane;
-            const uint32_t tile_end = iv.start(next < G ? next : G);
-            if (tile_end >= L) {  // the last element lies in this step
-                int where = -1;
-#pragma unroll
-                for (int j = 0; j < kPerLane; ++j)
-                    if (nt[j] && lo_e[j] + nt[j] == L) where = i0 + j;
-                const uint64_t lm = __ballot(where >= 0);
-                cp.item = static_cast<int>(rl32(static_cast<uint32_t>(where), static_cast<int>(__builtin_ctzll(lm))));
-                cp.elem = L;
-                s = static_cast<double>(u2f(sb));
-                return false;
-            }
-            cp.elem = tile_end;
-            cp.item = next;
-            continue;
-        }
-        // lanes before f, and items of lane f before its event item, in one step
-        const int jfu = static_cast<int>(rl32(static_cast<uint32_t>(jf), f));
-        uint32_t before_in = 0, lo_f = 0, n_f = 0, a_f = 0;
-#pragma unroll
-        for (int j = 0; j < kPerLane; ++j) {
-            if (j == jfu) {
-                before_in = pre_in[j];
-                lo_f = lo_e[j];
-                n_f = nt[j];
-                a_f = ab[j];
-            }
-        }
-        const uint32_t before = rl32(excl + before_in, f);
-        const uint32_t m2 = kDesc ? bb.m - before : bb.m + before;
-        sb = (sb >> 23) <= 1u ? m2 : ((sb & 0x7F800000u) | (m2 & 0x7FFFFFu));
-        cp.item = cp.item + f * kPerLane + jfu;
-        cp.elem = rl32(lo_f, f);
-        const uint32_t nf = rl32(n_f, f);
-        const double af = static_cast<double>(u2f(rl32(a_f, f)));
-        double sd = static_cast<double>(u2f(sb));
-        bool evt = false;
-        const uint64_t used = kDesc ? chain::desc_run_f32(sd, af, nf, evt)
-                                    : chain::asc_run_f32(sd, af, nf, thr, evt);
-        sb = f2u(static_cast<float>(sd));
-        if (evt) {
-            cp.elem += static_cast<uint32_t>(kDesc ? used : used - 1);
-            s = sd;
-            return true;
-        }
-        cp.elem += nf;
-        if (cp.elem >= L) {
-            s = sd;
-            return false;
-        }
-        cp.item += 1;
-    }
-    s = static_cast<double>(u2f(sb));
     return false;
 }
 

@@ -1368,11 +1368,19 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, const float* pr
     for (uint32_t g = 0; g * 64 < limit && !stopped; ++g) {
         const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
         const float pl = idx < limit ? seg_prob(g) : 0.0f;
+        // A whole segment below the limit: its 64 probabilities are read
+        // together (sixteen broadcast 16-byte reads in flight), so the chain
+        // waits for LDS once per 64 steps.
+        const bool whole = g * 64 + 64 <= limit;
+        F16 qs[4];
+        if (whole) static_for<0, 4>([&](auto B) { qs[decltype(B)::value] = lds16(probs + g * 64 + decltype(B)::value * 16); });
         static_for<0, 4>([&](auto B) {
             constexpr int b = decltype(B)::value * 16;
             if (stopped) return;
             const float before = cum;
-            if (g * 64 + b + 16 <= limit) {
+            if (whole) {
+                static_for<0, 16>([&](auto J) { cum = cum + qs[decltype(B)::value].v[decltype(J)::value]; });
+            } else if (g * 64 + b + 16 <= limit) {
                 const F16 q = lds16(probs + g * 64 + b);  // whole block below the limit
                 static_for<0, 16>([&](auto J) { cum = cum + q.v[decltype(J)::value]; });
             } else {
@@ -1405,11 +1413,16 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, const float* pr
     for (uint32_t g = 0; g * 64 < keep && !found; ++g) {
         const uint32_t idx = g * 64 + static_cast<uint32_t>(lane);
         const float pl = idx < keep ? seg_prob(g) : 0.0f;
+        const bool whole = g * 64 + 64 <= keep;
+        F16 qs[4];
+        if (whole) static_for<0, 4>([&](auto B) { qs[decltype(B)::value] = lds16(probs + g * 64 + decltype(B)::value * 16); });
         static_for<0, 4>([&](auto B) {
             constexpr int b = decltype(B)::value * 16;
             if (found) return;
             const float before = choice;
-            if (g * 64 + b + 16 <= keep) {
+            if (whole) {
+                static_for<0, 16>([&](auto J) { choice = choice - qs[decltype(B)::value].v[decltype(J)::value]; });
+            } else if (g * 64 + b + 16 <= keep) {
                 const F16 q = lds16(probs + g * 64 + b);
                 static_for<0, 16>([&](auto J) { choice = choice - q.v[decltype(J)::value]; });
             } else {
