@@ -36,6 +36,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 
 #include "chain_math.h"
 #include "chain_wave.h"
@@ -79,10 +80,6 @@ __device__ __forceinline__ float bin_value(uint32_t bin, float cap) {
 // [kLowBin, kHighBin]: widening is monotone and glibc tanhf is monotone.
 __device__ __forceinline__ uint32_t bin_key(uint32_t bin, float cap) { return order_key(bin_value(bin, cap)); }
 
-// Histogram word and field of a bin: bins b and b + 32768 share a word.
-__device__ __forceinline__ uint32_t bin_word(uint32_t bin) { return bin & (kWords - 1); }
-__device__ __forceinline__ uint32_t bin_shift(uint32_t bin) { return (bin >> 15) << 4; }
-
 // ---- small helpers ---------------------------------------------------------
 
 __device__ __forceinline__ float load_value(const float* rowp, int i) { return rowp[i]; }
@@ -119,6 +116,27 @@ __device__ __forceinline__ uint64_t rl64(uint64_t v, int lane) {
     const uint32_t lo = rl32(static_cast<uint32_t>(v), lane);
     const uint32_t hi = rl32(static_cast<uint32_t>(v >> 32), lane);
     return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+// v with lane kLane replaced by the wave-uniform x (v_writelane_b32; gfx950
+// reads one SGPR per VALU instruction, so the lane is an immediate).
+template <int kLane>
+__device__ __forceinline__ uint64_t writelane64(uint64_t v, uint64_t x) {
+    uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(lo) : "s"(static_cast<uint32_t>(x)), "n"(kLane));
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(hi) : "s"(static_cast<uint32_t>(x >> 32)), "n"(kLane));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+// f(std::integral_constant<int, J>) for J = J0 .. N - 1.
+template <int J0, int N, typename F>
+__device__ __forceinline__ void unroll_for(F&& f) {
+    if constexpr (J0 < N) {
+        f(std::integral_constant<int, J0>{});
+        unroll_for<J0 + 1, N>(f);
+    }
+}
+// Set bits of m below this lane.
+__device__ __forceinline__ uint32_t lanes_below_u64(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
 }
 __device__ __forceinline__ double rld(double v, int lane) {
     return __builtin_bit_cast(double, rl64(__builtin_bit_cast(uint64_t, v), lane));
@@ -183,26 +201,6 @@ __device__ __forceinline__ uint64_t sat_mul(uint64_t n, uint64_t d) {
     return (__umul64hi(n, d) != 0 || lo > kSat) ? kSat : lo;
 }
 
-// Block-wide exclusive scan of one u32 per thread; returns the total too.
-// `scratch` holds kWaves entries. Contains barriers: every thread must call.
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* scratch, uint32_t& total) {
-    const int lane = __lane_id();
-    const int wave = threadIdx.x >> 6;
-    const uint32_t incl = wave_incl_u32(v);
-    if (lane == 63) scratch[wave] = incl;
-    __syncthreads();
-    uint32_t before = 0;
-    total = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-        const uint32_t x = scratch[w];
-        if (w < wave) before += x;
-        total += x;
-    }
-    __syncthreads();
-    return before + incl - v;
-}
-
 __device__ __forceinline__ int lsb_exp(float x) {  // exponent of the lowest set bit, x > 0 finite
     const uint32_t b = f2u(x);
     const uint32_t ex = b >> 23;
@@ -223,24 +221,18 @@ struct HistShared {
         uint32_t hist[kWords];            // two 16-bit counters per word
     };
     uint16_t thr_bin[kFoExtrasCap];       // lowest bin whose final value is >= the token's
-    uint32_t off[kThreads];               // items before each thread's bins
-    uint64_t mask[kThreads];              // each thread's non-empty, non-NaN bins
+    uint32_t off[kThreads];               // items before each group of 64 bins
+    uint64_t mask[kThreads];              // each group's non-empty, non-NaN bins
     uint32_t spill[kSpillCap];            // bins that moved 32768 counts out of LDS
     uint32_t scan[kWaves];
     uint32_t counters[4];                 // [0] penalised tokens, [1] spills, [2] NaN tokens
 };
 
-// Count of bin `bin` after streaming: the LDS field plus 32768 per spill.
-__device__ __forceinline__ uint32_t bin_field(const HistShared& sh, uint32_t bin) {
-    return (sh.hist[bin_word(bin)] >> bin_shift(bin)) & 0xFFFFu;
-}
+// After streaming, a bin's count is its LDS field plus 32768 per spill-list entry.
 __device__ __forceinline__ uint32_t bin_spilled(const HistShared& sh, uint32_t bin, uint32_t nspill) {
     uint32_t c = 0;
     for (uint32_t i = 0; i < nspill; ++i) c += sh.spill[i] == bin ? 32768u : 0u;
     return c;
-}
-__device__ __forceinline__ uint32_t bin_count(const HistShared& sh, uint32_t bin, uint32_t nspill) {
-    return bin_field(sh, bin) + (nspill ? bin_spilled(sh, bin, nspill) : 0u);
 }
 
 // Counts two bf16 tokens (one 32-bit word) without branches: a token with
@@ -474,92 +466,141 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
     else stream_row<false>(sh, rowp, V, a.vec_ok != 0, bitmap, tid);
     const uint32_t nspill = min(sh.counters[1], static_cast<uint32_t>(kSpillCap));
 
-    // 3. Items in descending order. Wave w owns bins 65535 - 4096 w - 64 j - l
-    //    for j = 0..63 (step) and l = 0..63 (lane): each step reads 64
-    //    consecutive histogram words. Group g = 64 w + j has mask sh.mask[g]
-    //    (bit l: non-empty, non-NaN) and sh.off[g] items before it.
+    // 3. Items in descending order. After the last sweep every field is below
+    //    0x8000, so bit 15 can mark the bins of the spill list: a spilled bin
+    //    whose field is 0 then still reads as non-empty.
+    for (uint32_t i = tid; i < nspill; i += kThreads) {
+        const uint32_t e = sh.spill[i];
+        atomicOr(&sh.hist[e & (kWords - 1)], 0x8000u << ((e / kWords) * 16u));
+    }
+    __syncthreads();
+    //    Wave w owns histogram words kWords - 1 - 2048 w - 64 j - l for
+    //    j = 0..31 (group) and l = 0..63 (lane); word x holds the "high" bin
+    //    x + kWords (upper field) and the "low" bin x (lower field). Bins in
+    //    descending order are the high bins by descending word, then the low
+    //    bins by descending word, i.e. (wave, group, lane) order in each half.
+    //    Lane j keeps group j's two ballots; sh.mask / sh.off hold them with
+    //    the items before each group, high groups at [0, 512), low at [512, 1024).
     const int lane = __lane_id();
     const int wave = tid >> 6;
-    const uint32_t wtop = 65535u - 4096u * static_cast<uint32_t>(wave);
-    uint32_t wcount = 0;
+    const uint32_t wtop = (kWords - 1u) - 2048u * static_cast<uint32_t>(wave);
+    uint32_t words[32];  // this lane's histogram words
+#pragma unroll
+    for (int j = 0; j < 32; ++j) words[j] = sh.hist[wtop - 64u * j - lane];
+    auto field_count = [&](uint32_t f, uint32_t bin) {
+        return (f & 0x7FFFu) + ((f & 0x8000u) ? bin_spilled(sh, bin, nspill) : 0u);
+    };
+    uint64_t mhi = 0, mlo = 0;
     uint32_t nan_local = 0;
-    for (int j0 = 0; j0 < 64; j0 += 8) {  // eight independent LDS reads per round
-        uint32_t c[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) c[u] = bin_field(sh, wtop - 64u * (j0 + u) - lane);
-        if (nspill) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) c[u] += bin_spilled(sh, wtop - 64u * (j0 + u) - lane, nspill);
+    unroll_for<0, 32>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const uint32_t x = words[j];
+        bool nh = (x >> 16) != 0u;
+        bool nl = (x & 0xFFFFu) != 0u;
+        if ((wave == 0 && j < 2) || (wave == kWaves - 1 && j >= 30)) {  // the groups holding NaN bins
+            const uint32_t w = wtop - 64u * j - lane;
+            if (nh && bin_is_nan(w + kWords)) {
+                nan_local += field_count(x >> 16, w + kWords);
+                nh = false;
+            }
+            if (nl && bin_is_nan(w)) {
+                nan_local += field_count(x & 0xFFFFu, w);
+                nl = false;
+            }
         }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const bool isn = bin_is_nan(wtop - 64u * (j0 + u) - lane);
-            if (c[u] && isn) nan_local += c[u];
-            const uint64_t m = __ballot(c[u] != 0u && !isn);
-            if (lane == 0) sh.mask[wave * 64 + j0 + u] = m;
-            wcount += static_cast<uint32_t>(__popcll(m));
-        }
-    }
-    if (lane == 0) sh.scan[wave] = wcount;
+        const uint64_t bh = __ballot(nh);
+        const uint64_t bl = __ballot(nl);
+        mhi = writelane64<j>(mhi, bh);
+        mlo = writelane64<j>(mlo, bl);
+    });
+    const uint32_t ph = static_cast<uint32_t>(__popcll(mhi));  // lanes past 31: 0
+    const uint32_t pl = static_cast<uint32_t>(__popcll(mlo));
+    const uint32_t ih = wave_incl_u32(ph);
+    const uint32_t il = wave_incl_u32(pl);
+    if (lane == 63) sh.scan[wave] = (ih << 16) | il;  // each at most 2048
     if (nan_local) atomicAdd(&sh.counters[2], nan_local);
-    __syncthreads();
-    uint32_t nbins_total = 0;
-    uint32_t wbefore = 0;
+    __syncthreads();  // also: every histogram word is read
+    uint32_t tot_hi = 0, tot_lo = 0, before_hi = 0, before_lo = 0;
     for (int w = 0; w < kWaves; ++w) {
         const uint32_t x = sh.scan[w];
-        if (w < wave) wbefore += x;
-        nbins_total += x;
+        if (w < wave) {
+            before_hi += x >> 16;
+            before_lo += x & 0xFFFFu;
+        }
+        tot_hi += x >> 16;
+        tot_lo += x & 0xFFFFu;
     }
-    {  // group offsets: lane j takes group 64 * wave + j
-        const uint32_t cj = static_cast<uint32_t>(__popcll(sh.mask[wave * 64 + lane]));
-        sh.off[wave * 64 + lane] = wbefore + wave_incl_u32(cj) - cj;
+    const uint32_t nbins_total = tot_hi + tot_lo;
+    const uint32_t ohi = before_hi + ih - ph;
+    const uint32_t olo = tot_hi + before_lo + il - pl;
+    if (lane < 32) {
+        sh.mask[wave * 32 + lane] = mhi;
+        sh.mask[512 + wave * 32 + lane] = mlo;
+        sh.off[wave * 32 + lane] = ohi;
+        sh.off[512 + wave * 32 + lane] = olo;
     }
     __syncthreads();
 
-    // Bin items, in two passes: first (bin, count) pairs at their rank among
-    // the bins, staged in the decide kernel's per-item arrays (unused until
-    // then); then, densely over all threads, the final value of each and its
-    // place among the penalised items.
-    uint32_t* stage_bin = reinterpret_cast<uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
-    uint32_t* stage_cnt = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
-    const uint64_t below_me = (1ull << lane) - 1;
-    for (int j0 = 0; j0 < 64; j0 += 8) {
-        uint64_t m[8];
-        uint32_t o[8];
+    // Bin items, spread over the waves by group (group g goes to wave g % 16,
+    // so the few dense groups of a typical row land on different waves): a
+    // lane with a non-empty bin writes its final value and count at its rank
+    // among the bins plus the penalised tokens above it. Lane i of a wave
+    // prefetches the wave's i-th group; four groups are taken per round so
+    // that their softcap chains overlap.
+    {
+        const uint32_t gl = static_cast<uint32_t>(wave) + 16u * static_cast<uint32_t>(lane);
+        const uint64_t gm = sh.mask[gl];
+        const uint32_t go = sh.off[gl];
+        uint64_t todo = __ballot(gm != 0ull);
+        while (todo) {
+            constexpr int kRound = 4;
+            uint32_t bin[kRound], cnt[kRound], r[kRound];
+            bool on[kRound];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            m[u] = sh.mask[wave * 64 + j0 + u];
-            o[u] = sh.off[wave * 64 + j0 + u];
-        }
+            for (int u = 0; u < kRound; ++u) {
+                on[u] = false;
+                bin[u] = kLowBin;
+                cnt[u] = 0;
+                r[u] = 0;
+                if (todo == 0ull) continue;  // wave-uniform
+                const int i = __builtin_ctzll(todo);
+                todo &= todo - 1ull;
+                const uint64_t m = wave::readlane64(gm, i);
+                on[u] = ((m >> lane) & 1u) != 0u;
+                const uint32_t g = static_cast<uint32_t>(wave) + 16u * static_cast<uint32_t>(i);
+                const bool high = g < 512u;
+                const uint32_t word = (kWords - 1u) - 2048u * ((g & 511u) >> 5) - 64u * (g & 31u) - lane;
+                bin[u] = high ? word + kWords : word;
+                if (on[u]) {
+                    const uint32_t x = sh.hist[word];
+                    cnt[u] = field_count(high ? (x >> 16) : (x & 0xFFFFu), bin[u]);
+                }
+                r[u] = rl32(go, i) + lanes_below_u64(m);
+            }
+            float v[kRound];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            if (!((m[u] >> lane) & 1u)) continue;
-            const uint32_t bin = wtop - 64u * (j0 + u) - lane;
-            const uint32_t r = o[u] + static_cast<uint32_t>(__popcll(m[u] & below_me));
-            stage_bin[r] = bin;
-            stage_cnt[r] = bin_count(sh, bin, nspill);
+            for (int u = 0; u < kRound; ++u) v[u] = bin_value(bin[u], cap);
+#pragma unroll
+            for (int u = 0; u < kRound; ++u) {
+                if (!on[u]) continue;
+                uint32_t lo = 0, hi = E;  // penalised tokens with thr_bin > bin (thr_bin is non-increasing)
+                while (lo < hi) {
+                    const uint32_t mid = (lo + hi) >> 1;
+                    if (sh.thr_bin[mid] > bin[u]) lo = mid + 1;
+                    else hi = mid;
+                }
+                items[r[u] + lo] = (static_cast<uint64_t>(f2u(v[u])) << 32) | cnt[u];
+            }
         }
-    }
-    __syncthreads();
-    for (uint32_t r = tid; r < nbins_total; r += kThreads) {
-        const uint32_t bin = stage_bin[r];
-        uint32_t c = 0;  // penalised tokens with thr_bin > bin (thr_bin is non-increasing)
-        uint32_t lo = 0, hi = E;
-        while (lo < hi) {
-            const uint32_t mid = (lo + hi) >> 1;
-            if (sh.thr_bin[mid] > bin) lo = mid + 1;
-            else hi = mid;
-        }
-        c = lo;
-        items[r + c] = (static_cast<uint64_t>(f2u(bin_value(bin, cap))) << 32) | stage_cnt[r];
     }
     // Penalised items: position = own rank + bins with a final value >= its own.
     for (uint32_t e = tid; e < E; e += kThreads) {
         const uint32_t tb = sh.thr_bin[e];
         uint32_t nb = 0;
-        if (tb <= kHighBin) {
-            const uint32_t g = (65535u - tb) >> 6;        // group holding bin tb
-            const uint32_t l = (65535u - tb) & 63u;       // its lane: bins >= tb are lanes 0..l
+        if (tb <= kHighBin) {  // bins >= tb: in tb's half, the words >= tb's word
+            const uint32_t d = (kWords - 1u) - (tb & (kWords - 1u));
+            const uint32_t g = (tb >= kWords ? 0u : 512u) + (d >> 6);  // group holding tb
+            const uint32_t l = d & 63u;                                // its lane
             const uint64_t upto = l == 63 ? ~0ull : ((2ull << l) - 1);
             nb = sh.off[g] + static_cast<uint32_t>(__popcll(sh.mask[g] & upto));
         }

@@ -251,3 +251,22 @@ def test_penalised_overflow_rows_in_slices():
         ora = run_oracle(w)
         assert_parity(w, gpu, ora, w.name)
         assert not np.any(gpu[2] & S.GE_FLAG_UNSUPPORTED), gpu[2]
+
+
+def test_values_with_more_than_32768_tokens(sampler):
+    """Bins whose count passes the LDS counters' 16-bit fields (moved to the
+    spill list every 32768 tokens), including one whose remaining field is
+    exactly 0 and a NaN bin that spills."""
+    V = 100003
+    rng = np.random.default_rng(21)
+    base = (rng.standard_normal(V) * 0.5).astype(np.float32)
+    rows = [np.zeros(V, np.float32)]                                         # one value, 3 spills
+    r = base.copy(); r[: 2 * 32768] = 0.25; rows.append(r)                   # field 0 after 2 spills
+    r = base.copy(); r[5:5 + 32768] = -1.5; r[40000:40000 + 40000] = np.nan; rows.append(r)
+    r = base.copy(); r[::2] = -np.inf; rows.append(r)                         # -inf bin with 50002 tokens
+    r = np.full(V, 0.125, np.float32); r[7::3] = 0.5; rows.append(r)          # two heavy values
+    x = _bf16(np.stack(rows))
+    for T, p in ((1.0, 0.9), (0.7, 1.0)):
+        w = small_workload(f"spill-T{T}-p{p}", x, dict(temperature=T, top_k=0, top_p=p, softcap=30.0),
+                           uniforms=W.mt_uniforms(int(T * 10), x.shape[0]), dtype="bf16")
+        _check(sampler, w)
