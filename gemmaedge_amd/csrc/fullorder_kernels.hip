@@ -1378,9 +1378,9 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     // penalised tokens of the group are the extras run (bf16) or are
     // evaluated where the bitmap marks them (f32).
     {
-        constexpr int kPer = 16;
+        constexpr int kPer = sizeof(T) == 2 ? 32 : 16;  // 64 bytes per thread per batch
         constexpr int kBatch = kDThreads * kPer;
-        constexpr int kW = kPer * static_cast<int>(sizeof(T)) / 4;  // 32-bit words per 16 tokens
+        constexpr int kW = kPer * static_cast<int>(sizeof(T)) / 4;  // 32-bit words per kPer tokens
         constexpr int kPerVec = 16 / static_cast<int>(sizeof(T));   // tokens per 16-byte load
         const bool fwd = sh.forward != 0;
         uint32_t want = fwd ? sh.group_rank : sh.group_total - 1 - sh.group_rank;
@@ -1409,7 +1409,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                     const uint4 v = *reinterpret_cast<const uint4*>(rowp + lo + q * kPerVec);
                     w[4 * q + 0] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
                 }
-                valid = 0xFFFFu;
+                valid = kPer == 32 ? 0xFFFFFFFFu : 0xFFFFu;
             } else {
                 for (int h = 0; h < kW; ++h) w[h] = 0;
                 for (int h = 0; h < kPer; ++h) {
@@ -1425,7 +1425,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         // penalised ones, which the extras run supplies).
         auto match16 = [&](int lo, const uint32_t* w, uint32_t valid) -> uint32_t {
             uint32_t mm = 0;
-            // 16 tokens at a multiple of 16 lie in one bitmap word
+            // kPer (<= 32) tokens at a multiple of kPer lie in one bitmap word
             const uint32_t pw = (pen && valid) ? (bitmap[lo >> 5] >> (lo & 31)) & valid : 0u;
             if constexpr (kF32) {
 #pragma unroll
