@@ -1199,6 +1199,49 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     //    segment to its place in stage[0, n_c) (inside segment 0's area past
     //    wave 0's entries, so no wave overwrites another's unread entries),
     //    then rank by counting. More: gather and sort.
+    if (ll.fs && n_c <= static_cast<uint32_t>(kBlock)) {
+        // Final-order list straight from the candidates: their final
+        // composite keys, each ranked among all of them, the top m written to
+        // the slot. The bounds are the m-th and j1-th final keys, raised to
+        // the capped value of tau, which bounds every element below it (a
+        // penalised candidate's final can fall below those). The softcap is
+        // monotone, so without penalties these are the capped values of the
+        // m-th and j1-th raw entries.
+        uint32_t base = 0;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) base += w < wave ? cnt[w] : 0u;
+        for (uint32_t i = lane; i < cnt[wave]; i += 64) {
+            const uint64_t e = entry_of(seg[i]);
+            const float f = softcap(key_value(static_cast<uint32_t>(e >> 32)), rc.cap);
+            sh.stage[base + i] =
+                composite(order_key((rc.pen && raw_entry_pen(e)) ? penalize(f, rc.r) : f), raw_entry_index(e));
+        }
+        if (static_cast<uint32_t>(tid) >= n_c && static_cast<uint32_t>(tid) < ((n_c + 7u) & ~7u))
+            sh.stage[tid] = 0ull;
+        __syncthreads();
+        const bool all_listed = allpass && n_c <= m;
+        const uint32_t listed = all_listed ? n_c : m;
+        const uint32_t ktau = allpass ? 0u : order_key(softcap(floor_v, rc.cap));
+        if (static_cast<uint32_t>(tid) < n_c) {
+            const uint64_t fc = sh.stage[tid];
+            const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(sh.stage);
+            uint32_t r0 = 0, r1 = 0;
+            for (uint32_t j = 0; j < (n_c + 7u) / 8u; ++j) {
+                const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
+                r0 = add_greater4(r0, q0.x, q0.y, q1.x, q1.y, fc);
+                r1 = add_greater4(r1, q2.x, q2.y, q3.x, q3.y, fc);
+            }
+            const uint32_t r = r0 + r1;
+            if (r < m) store_shared(&slot[2u + r], fc);
+            if (r == m - 1u) sh.u32[24] = max(composite_key(fc), ktau);
+            if (r == ll.j1 - 1u) sh.u32[25] = max(composite_key(fc), ktau);
+        }
+        if (tid == 0 && n_c < ll.j1) sh.u32[25] = 0u;  // (all listed; the header then writes 0)
+        n_top = listed;
+        n_out = listed;
+        direct = true;
+        return all_listed ? 0ull : 1ull;  // 1: a nonzero guarantee, the bounds are in sh.u32[24], [25]
+    }
     if (n_c <= static_cast<uint32_t>(kBlock)) {
         uint32_t base = 0;
 #pragma unroll
@@ -2547,29 +2590,33 @@ __global__ __launch_bounds__(kBlock, 4) void select_kernel(DevArgs a) {
     // stores, then one ticket per workgroup; the last workgroup of the row
     // merges.
     if (ll.fs) {
-        // The list's final composite keys, ranked by final value; the capped
-        // values of the m-th and j1-th raw entries as the bounds.
-        const uint32_t i = static_cast<uint32_t>(tid);
-        uint64_t fc = 0ull;
-        if (i < n_top) {
-            const uint64_t e = sh.list[i];
-            const float f = softcap(key_value(static_cast<uint32_t>(e >> 32)), rc.cap);
-            const uint32_t kc = order_key(f);
-            fc = composite(order_key((rc.pen && raw_entry_pen(e)) ? penalize(f, rc.r) : f), raw_entry_index(e));
-            if (i == m - 1u) sh.u32[24] = kc;
-            if (i == ll.j1 - 1u) sh.u32[25] = kc;
-        }
-        sh.stage[i] = fc;  // zeros past n_top pad the rank's reads
-        __syncthreads();
-        if (i < n_top) {
-            const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(sh.stage);
-            uint32_t r0 = 0, r1 = 0;
-            for (uint32_t j = 0; j < (n_top + 7u) / 8u; ++j) {
-                const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
-                r0 = add_greater4(r0, q0.x, q0.y, q1.x, q1.y, fc);
-                r1 = add_greater4(r1, q2.x, q2.y, q3.x, q3.y, fc);
+        if (direct) {
+            __syncthreads();  // the list is written, the bounds are in sh.u32[24], [25]
+        } else {
+            // The list's final composite keys, ranked by final value; the capped
+            // values of the m-th and j1-th raw entries as the bounds.
+            const uint32_t i = static_cast<uint32_t>(tid);
+            uint64_t fc = 0ull;
+            if (i < n_top) {
+                const uint64_t e = sh.list[i];
+                const float f = softcap(key_value(static_cast<uint32_t>(e >> 32)), rc.cap);
+                const uint32_t kc = order_key(f);
+                fc = composite(order_key((rc.pen && raw_entry_pen(e)) ? penalize(f, rc.r) : f), raw_entry_index(e));
+                if (i == m - 1u) sh.u32[24] = kc;
+                if (i == ll.j1 - 1u) sh.u32[25] = kc;
             }
-            store_shared(&slot[2u + r0 + r1], fc);
+            sh.stage[i] = fc;  // zeros past n_top pad the rank's reads
+            __syncthreads();
+            if (i < n_top) {
+                const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(sh.stage);
+                uint32_t r0 = 0, r1 = 0;
+                for (uint32_t j = 0; j < (n_top + 7u) / 8u; ++j) {
+                    const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
+                    r0 = add_greater4(r0, q0.x, q0.y, q1.x, q1.y, fc);
+                    r1 = add_greater4(r1, q2.x, q2.y, q3.x, q3.y, fc);
+                }
+                store_shared(&slot[2u + r0 + r1], fc);
+            }
         }
         if (tid == 0) {
             const uint64_t g0 = gamma == kGuaranteeFailed ? kGuaranteeFailed
