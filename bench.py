@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import dataclasses
 import json
 import os
 import sys
@@ -253,6 +254,16 @@ def bench_c1(torch, sampler, W):
             "us_per_token_graph_back_to_back": g / 200 * 1e6,
             "bytes_per_launch": w.bytes_per_row()}
         runs[name] = (w, gpu_out)
+    # The reference's own dtype with top-k disabled (k = V): the f32 full-order
+    # path for one row (not a BASELINE config; its latency is reported).
+    w = dataclasses.replace(W.c1(), name="C1-f32-full-order", params=dict(W.c1().params, top_k=0))
+    b = Bound(sampler, w, torch)
+    gpu_out = b.run_once()
+    d = kernel_durations_us(torch, b, 10)
+    out["C1_f32_full_order"] = {"us_per_token_kernel_p50": float(np.median(d)),
+                                "us_per_token_kernel_max": float(np.max(d)),
+                                "bytes_per_launch": w.bytes_per_row()}
+    runs["C1_f32_full_order"] = (w, gpu_out)
     return out, runs
 
 
