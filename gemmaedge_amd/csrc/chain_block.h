@@ -1,0 +1,306 @@
+// The whole workgroup replays a float or double accumulation over a long list
+// of items (runs of equal addends, item i being elements [start(i),
+// start(i + 1)) of one addend): the reference's softmax denominator (double),
+// top-p cumulative and draw walk (float) over probabilities in sorted order
+// (src/generation.cpp:96-97, 105-113, 120-124), for rows whose items number
+// up to the vocabulary (f32 logits, where nearly every token is an item of
+// its own).
+//
+// Inside one binade of the accumulator each item is a map of the
+// accumulator's parity (chain_math.h ParityMap): ties to even are the only
+// steps that depend on the accumulator, and only through its parity. The
+// block takes the items in tiles of kThreads * kPer; each thread folds its kPer
+// consecutive items into one map, a DPP scan composes the maps across the
+// wave, and the waves' totals are composed through LDS. The magnitudes only
+// grow along the list, so the first item that would leave the binade, or
+// reach the threshold, is found by comparing scanned magnitudes; that item is
+// replayed in closed form (chain_math.h asc_run / desc_run) by the thread
+// that holds it, and the scan resumes after it in the new binade. A tile thus
+// costs one pass per binade crossing in it, and ties cost nothing extra.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <climits>
+#include <cmath>
+
+#include "chain_math.h"
+#include "chain_wave.h"
+#include "ge_math.h"
+#include "wave_ops.h"
+
+#pragma clang fp contract(off)
+
+namespace ge {
+namespace bchain {
+
+constexpr int kPer = 8;  // consecutive items per thread per tile
+
+// Float accumulator (the top-p cumulative and the draw walk).
+struct F32Acc {
+    using U = uint32_t;
+    static constexpr U kCap = 1u << 28;
+    struct Bin {
+        U m, lo, hi, tm;
+        int uexp;
+    };
+    __device__ static Bin binade(double s, double thr) {
+        const chain::StepBits b = chain::binade_bits(f2u(static_cast<float>(s)));
+        return Bin{b.m, b.lo, chain::kHiF, chain::threshold_bits(f2u(static_cast<float>(thr)), b.uexp), b.uexp};
+    }
+    __device__ static void step(uint32_t ab, int uexp, U& D, bool& tie, bool& odd0, bool& big) {
+        chain::step_bits_p(ab, uexp, D, tie, odd0, big);
+    }
+    __device__ static double rebuild(double s, const Bin&, U m) {
+        return static_cast<double>(u2f(chain::rebuild_bits(f2u(static_cast<float>(s)), m)));
+    }
+    __device__ static uint64_t asc(double& s, double a, uint64_t n, double thr, bool& hit) {
+        return chain::asc_run_f32(s, a, n, thr, hit);
+    }
+    __device__ static uint64_t desc(double& c, double a, uint64_t n, bool& stop) {
+        return chain::desc_run_f32(c, a, n, stop);
+    }
+};
+
+// Double accumulator with float addends (the softmax denominator and the
+// near-boundary sums).
+struct F64Acc {
+    using U = uint64_t;
+    static constexpr U kCap = 1ull << 62;
+    struct Bin {
+        U m, lo, hi, tm;
+        int uexp;
+    };
+    __device__ static Bin binade(double s, double thr) {
+        const chain::Binade b = chain::binade_of<double>(s);
+        U tm = ~0ull;  // never reached: m + magnitude < 2^63
+        if (thr == thr) {
+            if (!(thr > 0.0)) tm = 0;
+            else if (thr < std::ldexp(1.0, b.uexp + 53)) tm = chain::threshold_m(thr, b.uexp);
+        }
+        return Bin{b.m, b.lo, b.hi, tm, b.uexp};
+    }
+    __device__ static void step(uint32_t ab, int uexp, U& D, bool& tie, bool& odd0, bool& big) {
+        chain::step_bits64(ab, uexp, D, tie, odd0, big);
+    }
+    __device__ static double rebuild(double, const Bin& b, U m) {
+        return std::ldexp(static_cast<double>(m), b.uexp);
+    }
+    __device__ static uint64_t asc(double& s, double a, uint64_t n, double thr, bool& hit) {
+        return chain::asc_run<double>(s, a, n, thr, hit);
+    }
+    __device__ static uint64_t desc(double& c, double a, uint64_t n, bool& stop) {
+        return chain::desc_run<double>(c, a, n, stop);
+    }
+};
+
+template <int kWaves>
+struct Shared {
+    uint64_t me[kWaves];  // per-wave maps (magnitudes from an even / odd start)
+    uint64_t mo[kWaves];
+    int ev[kWaves];       // per-wave first event item, INT_MAX for none
+    int last;             // item holding element L - 1, when it lies in the tile
+    double rs;            // the event item's replay: accumulator after it,
+    uint32_t relem;       // next (or event) element,
+    int rhit;             // whether the threshold / stop fired
+};
+
+template <int kCtrl, int kRowMask, typename U>
+__device__ __forceinline__ U dpp_any(U x) {
+    if constexpr (sizeof(U) == 4) return wave::dpp<kCtrl, kRowMask>(x, 0u);
+    else return wave::dpp64<kCtrl, kRowMask>(x, 0ull);
+}
+
+template <typename A, int kCtrl, int kRowMask>
+__device__ __forceinline__ chain::ParityMap<typename A::U> scan_step(chain::ParityMap<typename A::U> v) {
+    using U = typename A::U;
+    // lanes without a source read the identity map (0, 0)
+    const chain::ParityMap<U> t{dpp_any<kCtrl, kRowMask>(v.e), dpp_any<kCtrl, kRowMask>(v.o)};
+    return chain::compose<U, A::kCap>(t, v);
+}
+
+// Exclusive scan of the lanes' maps in lane order (lane 0: the identity).
+template <typename A>
+__device__ __forceinline__ chain::ParityMap<typename A::U> wave_excl(chain::ParityMap<typename A::U> f) {
+    constexpr int kWaveShr1 = 0x138;
+    chain::ParityMap<typename A::U> v{dpp_any<kWaveShr1, 0xf>(f.e), dpp_any<kWaveShr1, 0xf>(f.o)};
+    v = scan_step<A, wave::kRowShr1, 0xf>(v);
+    v = scan_step<A, wave::kRowShr2, 0xf>(v);
+    v = scan_step<A, wave::kRowShr4, 0xf>(v);
+    v = scan_step<A, wave::kRowShr8, 0xf>(v);
+    v = scan_step<A, wave::kRowBcast15, 0xa>(v);
+    v = scan_step<A, wave::kRowBcast31, 0xc>(v);
+    return v;
+}
+
+// Items i .. i + kPer - 1: boundaries pb[0..kPer] (clamped to start(G), so
+// items past G hold no element) and addend bits ab.
+__device__ __forceinline__ void load_tile(const uint32_t* pre, const float* add, int G, int i, uint32_t* pb,
+                                          uint32_t* ab) {
+    if (i + kPer <= G) {  // pre has G + 1 entries; i is a multiple of kPer
+        const uint4 p0 = *reinterpret_cast<const uint4*>(pre + i);
+        const uint4 p1 = *reinterpret_cast<const uint4*>(pre + i + 4);
+        pb[0] = p0.x; pb[1] = p0.y; pb[2] = p0.z; pb[3] = p0.w;
+        pb[4] = p1.x; pb[5] = p1.y; pb[6] = p1.z; pb[7] = p1.w;
+        pb[8] = pre[i + 8];
+        const uint4 a0 = *reinterpret_cast<const uint4*>(add + i);
+        const uint4 a1 = *reinterpret_cast<const uint4*>(add + i + 4);
+        ab[0] = a0.x; ab[1] = a0.y; ab[2] = a0.z; ab[3] = a0.w;
+        ab[4] = a1.x; ab[5] = a1.y; ab[6] = a1.z; ab[7] = a1.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j <= kPer; ++j) pb[j] = pre[min(i + j, G)];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) ab[j] = i + j < G ? f2u(add[i + j]) : 0u;
+    }
+}
+
+template <bool kDesc, typename Bin, typename U>
+__device__ __forceinline__ bool exceeds(const Bin& b, U r) {
+    if (kDesc) return b.m < b.lo + r;             // m - r below the binade's exact range
+    return b.m + r > b.hi || b.m + r >= b.tm;     // above it, or at the threshold
+}
+
+// Replays elements [cp.elem, L) with the whole workgroup (every thread calls
+// it with the same arguments; it holds barriers). Semantics as wave_chain_f32
+// (chain_wave.h): ascending sums stop at the first element whose sum is >=
+// thr (NaN: never), descending ones before the first element with c <= a.
+// Returns true on a stop with cp at the stop element; otherwise false with
+// cp.elem == L and cp.item holding element L - 1. Requires L <= start(G);
+// pre and add 16-byte aligned.
+template <typename A, bool kDesc, int kThreads>
+__device__ bool block_chain(const uint32_t* pre, const float* add, int G, ChainPos& cp, uint32_t L, double& s,
+                            double thr, Shared<kThreads / 64>& sh) {
+    using U = typename A::U;
+    using Map = chain::ParityMap<U>;
+    constexpr int kWaves = kThreads / 64;
+    constexpr int kTile = kThreads * kPer;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    if (!(cp.elem < L && cp.item < G)) return false;
+    int t0 = cp.item / kTile * kTile;
+    uint32_t pb[kPer + 1], ab[kPer];
+    load_tile(pre, add, G, t0 + tid * kPer, pb, ab);
+    for (;;) {
+        // the next tile's loads are in flight while this one is scanned
+        uint32_t npb[kPer + 1], nab[kPer];
+        const bool more = t0 + kTile < G;
+        if (more) load_tile(pre, add, G, t0 + kTile + tid * kPer, npb, nab);
+        const uint32_t tile_end = pre[min(t0 + kTile, G)];
+        const int ibase = t0 + tid * kPer;
+        for (;;) {  // one pass per binade the tile's remaining items start in
+            const typename A::Bin b = A::binade(s, thr);
+            const uint32_t e0 = cp.elem;
+            Map f{0, 0};
+            int last = -1;
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                const uint32_t lo = max(pb[j], e0);
+                const uint32_t hi = min(pb[j + 1], L);
+                const uint32_t nt = hi > lo ? hi - lo : 0u;
+                U D;
+                bool tie, odd0, big;
+                A::step(ab[j], b.uexp, D, tie, odd0, big);
+                f = chain::compose<U, A::kCap>(f, chain::run_map<U, A::kCap>(nt, D, tie, odd0, big));
+                if (nt && hi == L) last = ibase + j;
+            }
+            const Map x = wave_excl<A>(f);
+            if (lane == 63) {
+                const Map wt = chain::compose<U, A::kCap>(x, f);
+                sh.me[wave] = wt.e;
+                sh.mo[wave] = wt.o;
+            }
+            __syncthreads();
+            Map pw{0, 0}, tot{0, 0};
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const Map t{static_cast<U>(sh.me[w]), static_cast<U>(sh.mo[w])};
+                if (w < wave) pw = chain::compose<U, A::kCap>(pw, t);
+                tot = chain::compose<U, A::kCap>(tot, t);
+            }
+            const U r0 = chain::apply_from(chain::compose<U, A::kCap>(pw, x), b.m);
+            const U r_end = chain::sat_add_cap<U, A::kCap>(r0, chain::apply_from(f, static_cast<U>(b.m + r0)));
+            int ev = INT_MAX;
+            U r_ev = 0;
+            if (exceeds<kDesc>(b, r_end)) {  // the first exit may lie in this thread's items
+                U r = r0;
+#pragma unroll
+                for (int j = 0; j < kPer; ++j) {
+                    const uint32_t lo = max(pb[j], e0);
+                    const uint32_t hi = min(pb[j + 1], L);
+                    const uint32_t nt = hi > lo ? hi - lo : 0u;
+                    U D;
+                    bool tie, odd0, big;
+                    A::step(ab[j], b.uexp, D, tie, odd0, big);
+                    const Map mj = chain::run_map<U, A::kCap>(nt, D, tie, odd0, big);
+                    const U rn = chain::sat_add_cap<U, A::kCap>(r, chain::apply_from(mj, static_cast<U>(b.m + r)));
+                    if (ev == INT_MAX && nt && exceeds<kDesc>(b, rn)) {
+                        ev = ibase + j;
+                        r_ev = r;
+                    }
+                    r = rn;
+                }
+            }
+            const uint64_t em = __ballot(ev != INT_MAX);
+            if (lane == 0) sh.ev[wave] = em ? static_cast<int>(wave::readlane(static_cast<uint32_t>(ev), __builtin_ctzll(em))) : INT_MAX;
+            if (last >= 0) sh.last = last;
+            __syncthreads();
+            int fe = INT_MAX;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) fe = min(fe, sh.ev[w]);
+            if (fe == INT_MAX) {
+                const U rt = chain::apply_from(tot, b.m);
+                s = A::rebuild(s, b, kDesc ? b.m - rt : b.m + rt);
+                if (tile_end >= L) {
+                    cp.elem = L;
+                    cp.item = sh.last;
+                    return false;
+                }
+                cp.elem = tile_end;
+                cp.item = t0 + kTile;
+                break;
+            }
+            if (ev == fe) {  // this thread holds the event item: replay it
+                const int j = fe - ibase;
+                uint32_t lo = 0, hi = 0;
+                float a = 0.0f;
+#pragma unroll
+                for (int q = 0; q < kPer; ++q) {
+                    if (q == j) {
+                        lo = max(pb[q], e0);
+                        hi = min(pb[q + 1], L);
+                        a = u2f(ab[q]);
+                    }
+                }
+                const uint32_t nf = hi - lo;
+                double sv = A::rebuild(s, b, kDesc ? b.m - r_ev : b.m + r_ev);
+                bool hit = false;
+                const uint64_t used = kDesc ? A::desc(sv, static_cast<double>(a), nf, hit)
+                                            : A::asc(sv, static_cast<double>(a), nf, thr, hit);
+                sh.rs = sv;
+                sh.rhit = hit ? 1 : 0;
+                sh.relem = hit ? lo + static_cast<uint32_t>(kDesc ? used : used - 1) : hi;
+            }
+            __syncthreads();
+            s = sh.rs;
+            cp.elem = sh.relem;
+            const bool hit = sh.rhit != 0;
+            if (hit || cp.elem >= L) {
+                cp.item = fe;
+                return hit;
+            }
+            cp.item = fe + 1;
+        }
+        if (!more) return false;  // unreachable while L <= start(G)
+        t0 += kTile;
+#pragma unroll
+        for (int j = 0; j <= kPer; ++j) pb[j] = npb[j];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) ab[j] = nab[j];
+    }
+}
+
+}  // namespace bchain
+}  // namespace ge

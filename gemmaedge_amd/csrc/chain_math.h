@@ -296,7 +296,8 @@ GE_CHAIN_HD void float_fields(uint32_t bits, uint32_t& man, int& e) {
 //   sh >= 32     -> a / U < 2^-8: rounds to 0, no tie
 //   0 <= sh < 32 -> D = ma >> sh rounded to nearest by the sh dropped bits
 //                   (sh = 0 drops none: frac = half = 0, never a tie).
-GE_CHAIN_HD void step_bits(uint32_t ab, int uexp, uint32_t& D, bool& tie, bool& big) {
+// odd0 (ties only): floor(a / U) is odd, so D = floor + 1.
+GE_CHAIN_HD void step_bits_p(uint32_t ab, int uexp, uint32_t& D, bool& tie, bool& odd0, bool& big) {
     uint32_t ma;
     int ea;
     float_fields(ab, ma, ea);
@@ -309,8 +310,107 @@ GE_CHAIN_HD void step_bits(uint32_t ab, int uexp, uint32_t& D, bool& tie, bool& 
     const uint32_t half = (1u << shc) >> 1;
     big = nz && sh < 0;
     tie = in_range && shc != 0u && frac == half;
+    odd0 = tie && (d0 & 1u) != 0u;
     const uint32_t up = tie ? (d0 & 1u) : (frac > half ? 1u : 0u);
     D = in_range ? d0 + up : 0u;
+}
+GE_CHAIN_HD void step_bits(uint32_t ab, int uexp, uint32_t& D, bool& tie, bool& big) {
+    bool odd0;
+    step_bits_p(ab, uexp, D, tie, odd0, big);
+}
+
+// The same step for a double accumulator (U = 2^uexp, 53-bit significand)
+// and a float addend: D = round(a / U) as a 64-bit integer, big when
+// a / U >= 2^53. Addends at or above the ulp are whole multiples of it (no
+// rounding); below, as for the float accumulator.
+GE_CHAIN_HD void step_bits64(uint32_t ab, int uexp, uint64_t& D, bool& tie, bool& odd0, bool& big) {
+    uint32_t ma;
+    int ea;
+    float_fields(ab, ma, ea);
+    const int sh = uexp + 150 - ea;  // a / U = ma * 2^-sh
+    D = 0;
+    tie = false;
+    odd0 = false;
+    big = false;
+    if (ma == 0u) return;
+    if (sh <= 0) {
+        const int up = -sh;  // a / U = ma * 2^up, ma < 2^24
+        if (up >= 53 || (up >= 30 && ma >= (1u << (53 - up)))) {
+            big = true;
+            return;
+        }
+        D = static_cast<uint64_t>(ma) << up;  // < 2^53
+        return;
+    }
+    if (sh >= 32) return;  // a / U < 2^-8
+    const uint32_t d0 = ma >> sh;
+    const uint32_t frac = ma & ((1u << sh) - 1u);
+    const uint32_t half = 1u << (sh - 1);
+    tie = frac == half;
+    odd0 = tie && (d0 & 1u) != 0u;
+    D = d0 + (tie ? (d0 & 1u) : (frac > half ? 1u : 0u));
+}
+
+// ---- runs as functions of the accumulator's parity ---------------------------
+//
+// Inside one binade, a run of n elements of one addend moves m by a fixed
+// number of ulps, except that a tie's first element depends on the parity of
+// m (ties to even). A run, and any sequence of runs, is therefore the map
+// m -> m + e (m even) or m + o (m odd) for ascending sums, m - e / m - o for
+// descending ones: two magnitudes. The parity after the map is the start
+// parity plus that magnitude, so maps compose associatively and a block of
+// threads can scan them; the first element that would leave the binade (or
+// reach a threshold) is found from the scanned magnitudes, which only grow
+// along the sequence. Magnitudes saturate at kCap, beyond any binade's room.
+template <typename U>
+struct ParityMap {
+    U e;  // magnitude from an even m
+    U o;  // magnitude from an odd m
+};
+
+template <typename U, U kCap>
+GE_CHAIN_HD U sat_add_cap(U x, U y) {
+    const U s = x + y;  // x, y <= kCap <= half the range: no wrap
+    return s > kCap ? kCap : s;
+}
+
+// n elements of one addend with step D (tie / odd0 / big from step_bits*).
+// From an odd m a tie's first element moves by D + 1 when floor(a / U) is
+// even (D is that floor) and by D - 1 when it is odd (D is floor + 1); m is
+// even after it, and every later element moves by D.
+template <typename U, U kCap>
+GE_CHAIN_HD ParityMap<U> run_map(uint32_t n, U D, bool tie, bool odd0, bool big) {
+    ParityMap<U> r{0, 0};
+    if (n == 0) return r;
+    if (big) {
+        r.e = r.o = kCap;
+        return r;
+    }
+    U base;
+    if constexpr (sizeof(U) == 4) {  // D <= 2^24 + 1: the product fits 64 bits
+        const uint64_t p = static_cast<uint64_t>(n) * D;
+        base = p > kCap ? kCap : static_cast<U>(p);
+    } else {  // D < 2^53; a product near 2^61 is far beyond any binade's room
+        const bool over = static_cast<double>(n) * static_cast<double>(D) >= 2305843009213693952.0;  // 2^61
+        base = over ? kCap : static_cast<U>(static_cast<uint64_t>(n) * D);
+    }
+    r.e = base;
+    r.o = (tie && base != kCap) ? (odd0 ? base - 1 : base + 1) : base;
+    return r;
+}
+
+// f, then g.
+template <typename U, U kCap>
+GE_CHAIN_HD ParityMap<U> compose(ParityMap<U> f, ParityMap<U> g) {
+    ParityMap<U> h;
+    h.e = sat_add_cap<U, kCap>(f.e, (f.e & 1u) ? g.o : g.e);
+    h.o = sat_add_cap<U, kCap>(f.o, (f.o & 1u) ? g.e : g.o);
+    return h;
+}
+
+template <typename U>
+GE_CHAIN_HD U apply_from(ParityMap<U> f, U m) {
+    return (m & 1u) ? f.o : f.e;
 }
 
 // Smallest m with m * 2^uexp >= thr, for a float thr; kNoThreshold when thr is

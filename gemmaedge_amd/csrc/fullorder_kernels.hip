@@ -38,6 +38,7 @@
 #include <climits>
 #include <type_traits>
 
+#include "chain_block.h"
 #include "chain_math.h"
 #include "chain_wave.h"
 #include "ge_math.h"
@@ -633,7 +634,7 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
 // one scatters. Runs of equal keys then become the items (value, count).
 
 constexpr int kDigits = 256;
-constexpr int kSortUnroll = 4;  // 64-token steps in flight per wave
+constexpr int kSortUnroll = 8;  // 64-token steps in flight per wave
 
 struct SortShared {
     uint32_t cnt[2][kWaves][kDigits];  // per (portion, digit): counts, then cursors
@@ -808,13 +809,25 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
     //    go to the other buffer.
     const uint32_t* s = src;
     uint32_t* istart = dst;
+    // (kSortUnroll steps of loads in flight per wave)
+    auto load_pairs = [&](int base, uint32_t* cv, uint32_t* pv) {
+#pragma unroll
+        for (int u = 0; u < kSortUnroll; ++u) {
+            const int i = base + 64 * u + lane;
+            const bool act = i < whi;
+            cv[u] = act ? ld_l2(s + i) : 0u;
+            pv[u] = (act && i > 0) ? ld_l2(s + i - 1) : 0u;
+        }
+    };
     uint32_t nb = 0;
-    for (int base = wlo; base < whi; base += 64) {
-        const int i = base + lane;
-        const bool act = i < whi;
-        const uint32_t cv = act ? ld_l2(s + i) : 0u;
-        const uint32_t pv = (act && i > 0) ? ld_l2(s + i - 1) : ~cv;
-        nb += static_cast<uint32_t>(__popcll(__ballot(act && cv != pv)));
+    for (int base = wlo; base < whi; base += 64 * kSortUnroll) {
+        uint32_t cv[kSortUnroll], pv[kSortUnroll];
+        load_pairs(base, cv, pv);
+#pragma unroll
+        for (int u = 0; u < kSortUnroll; ++u) {
+            const int i = base + 64 * u + lane;
+            nb += static_cast<uint32_t>(__popcll(__ballot(i < whi && (i == 0 || cv[u] != pv[u]))));
+        }
     }
     if (lane == 0) sh.scan[wave] = nb;
     __syncthreads();
@@ -824,23 +837,41 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
         if (w < wave) j += x;
         G += x;
     }
-    for (int base = wlo; base < whi; base += 64) {
-        const int i = base + lane;
-        const bool act = i < whi;
-        const uint32_t cv = act ? ld_l2(s + i) : 0u;
-        const uint32_t pv = (act && i > 0) ? ld_l2(s + i - 1) : ~cv;
-        const bool bnd = act && cv != pv;
-        const uint64_t m = __ballot(bnd);
-        if (bnd) istart[j + static_cast<uint32_t>(__popcll(m & below))] = static_cast<uint32_t>(i);
-        j += static_cast<uint32_t>(__popcll(m));
+    for (int base = wlo; base < whi; base += 64 * kSortUnroll) {
+        uint32_t cv[kSortUnroll], pv[kSortUnroll];
+        load_pairs(base, cv, pv);
+#pragma unroll
+        for (int u = 0; u < kSortUnroll; ++u) {
+            const int i = base + 64 * u + lane;
+            const bool bnd = i < whi && (i == 0 || cv[u] != pv[u]);
+            const uint64_t m = __ballot(bnd);
+            if (bnd) istart[j + static_cast<uint32_t>(__popcll(m & below))] = static_cast<uint32_t>(i);
+            j += static_cast<uint32_t>(__popcll(m));
+        }
     }
     if (tid == 0) istart[G] = static_cast<uint32_t>(V);
     stores_done_barrier();
-    for (uint32_t q = tid; q < G; q += kThreads) {
-        const uint32_t st = ld_l2(istart + q);
-        const uint32_t key = ~ld_l2(s + st);
-        const uint32_t val = key == kKeyNaN ? 0x7fc00000u : f2u(key_value(key));
-        items[q] = (static_cast<uint64_t>(val) << 32) | (ld_l2(istart + q + 1) - st);
+    constexpr int kQ = 4;
+    for (uint32_t q0 = tid; q0 < G; q0 += kThreads * kQ) {
+        uint32_t st[kQ], en[kQ];
+#pragma unroll
+        for (int u = 0; u < kQ; ++u) {
+            const uint32_t q = q0 + u * kThreads;
+            st[u] = q < G ? ld_l2(istart + q) : 0u;
+            en[u] = q < G ? ld_l2(istart + q + 1) : 0u;
+        }
+        uint32_t kv[kQ];
+#pragma unroll
+        for (int u = 0; u < kQ; ++u) kv[u] = q0 + u * kThreads < G ? ld_l2(s + st[u]) : 0u;
+#pragma unroll
+        for (int u = 0; u < kQ; ++u) {
+            const uint32_t q = q0 + u * kThreads;
+            if (q < G) {
+                const uint32_t key = ~kv[u];
+                const uint32_t val = key == kKeyNaN ? 0x7fc00000u : f2u(key_value(key));
+                items[q] = (static_cast<uint64_t>(val) << 32) | (en[u] - st[u]);
+            }
+        }
     }
     if (tid == 0) {
         const bool last_nan = ~ld_l2(s + V - 1) == kKeyNaN;
@@ -1015,6 +1046,7 @@ struct DecideShared {
         } st;
         uint32_t gx_ids[kFoExtrasCap];  // penalised tokens of the selected value, ascending
     };
+    bchain::Shared<kDWaves> bc;  // block chains (sorted rows)
     double dred[kDWaves];
     int ired[kDWaves];
     uint32_t ured[kDWaves];
@@ -1135,8 +1167,40 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     int minlsb = INT_MAX;
     bool nan = false;
     uint32_t run_base = 0;
-    uint64_t it_next = tid < G ? items[tid] : 0ull;
-    for (int r0 = 0; r0 < G; r0 += kDThreads) {
+    if constexpr (kSorted) {
+        // The sort kernel left every item's first element in pre[] (and
+        // pre[G] = V), so the exps need no scan; 4 items per thread in flight.
+        constexpr int kU = 16;
+        for (int base = 0; base < G; base += kDThreads * kU) {
+            uint64_t itv[kU];
+            uint32_t piv[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int i = base + u * kDThreads + tid;
+                itv[u] = i < G ? items[i] : 0ull;
+                piv[u] = i < G ? pre[i] : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int i = base + u * kDThreads + tid;
+                if (i < G) {
+                    const uint32_t n = static_cast<uint32_t>(itv[u]);
+                    const uint32_t nk = piv[u] >= k ? 0u : min(n, k - piv[u]);
+                    const float pe = expf_glibc((u2f(static_cast<uint32_t>(itv[u] >> 32)) - vmax) * inv_temp);
+                    aux[i] = pe;
+                    if (nk) {
+                        if (pe != pe) nan = true;
+                        else if (pe > 0.0f) {
+                            minlsb = min(minlsb, lsb_exp(pe));
+                            S += static_cast<double>(nk) * static_cast<double>(pe);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    uint64_t it_next = (!kSorted && tid < G) ? items[tid] : 0ull;
+    for (int r0 = 0; r0 < (kSorted ? 0 : G); r0 += kDThreads) {
         const int i = r0 + tid;
         const uint64_t it = it_next;  // the next round's item loads while this one is scanned
         it_next = i + kDThreads < G ? items[i + kDThreads] : 0ull;
@@ -1160,7 +1224,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             }
         }
     }
-    if (tid == 0) {
+    if (!kSorted && tid == 0) {
         pre[G] = run_base;
         if (G <= kStage) sh.st.pre[G] = run_base;
     }
@@ -1186,7 +1250,19 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     // above that, every partial sum in every order is exact, so the parallel
     // sum equals the reference's sequential one (generation.cpp:97).
     const bool certified = !any_nan && (Sp == 0.0 || ml >= exp_of(Sp) - 51);
-    if (wave == 0) {
+    if constexpr (kSorted) {
+        // up to V single-token items: the whole block replays the sum
+        double den = Sp;
+        if (any_nan) {
+            den = __builtin_nan("");
+        } else if (!certified) {
+            ChainPos cp{0, 1};
+            double s2 = static_cast<double>(p0);
+            if (k > 1) bchain::block_chain<bchain::F64Acc, false, kDThreads>(pre, aux, G, cp, k, s2, __builtin_nan(""), sh.bc);
+            den = s2;
+        }
+        if (tid == 0) sh.den = den;
+    } else if (wave == 0) {
         double den = Sp;
         if (any_nan) {
             den = __builtin_nan("");
@@ -1209,19 +1285,49 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     const float q0 = p0 * inv;
     const float minimum = q0 * p.min_p;
     int first_low = INT_MAX;
-    for (int i = tid; i < G; i += kDThreads) {  // this thread staged item i in 4a
-        const float q = (i < kStage ? sh.st.add[i] : aux[i]) * inv;
-        aux[i] = q;
-        if (i < kStage) sh.st.add[i] = q;
-        if (i >= 1 && first_low == INT_MAX && q < minimum && (i <= kStage ? sh.st.pre[i] : pre[i]) < k) first_low = i;
+    if constexpr (kSorted) {
+        constexpr int kU = 16;
+        for (int base = 0; base < G; base += kDThreads * kU) {
+            float pv[kU];
+            uint32_t piv[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int i = base + u * kDThreads + tid;
+                pv[u] = i < G ? aux[i] : 0.0f;
+                piv[u] = i < G ? pre[i] : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int i = base + u * kDThreads + tid;
+                if (i < G) {
+                    const float q = pv[u] * inv;
+                    aux[i] = q;
+                    if (i >= 1 && first_low == INT_MAX && q < minimum && piv[u] < k) first_low = i;
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < G; i += kDThreads) {  // this thread staged item i in 4a
+            const float q = (i < kStage ? sh.st.add[i] : aux[i]) * inv;
+            aux[i] = q;
+            if (i < kStage) sh.st.add[i] = q;
+            if (i >= 1 && first_low == INT_MAX && q < minimum && (i <= kStage ? sh.st.pre[i] : pre[i]) < k) first_low = i;
+        }
     }
     first_low = wave_reduce(first_low, [](int x, int y) { return min(x, y); });
     __syncthreads();  // every reader of sh.ired above is done
     if (lane == 0) sh.ired[wave] = first_low;
     __syncthreads();
-    // Wave 0 decides: top-p cut, draw, near-boundary flag, selected value's
-    // group. The item view is LDS when the row's items fit, else global.
-    auto decide = [&](const auto& iv) {
+    // Top-p cut, draw and near-boundary flag, then the selected value's
+    // group. bf16 rows (a few thousand items at most): wave 0 alone, over LDS
+    // copies of the items when they fit, else the global arrays. Sorted rows
+    // (up to V items): the whole block replays the chains.
+    struct Drawn {
+        uint32_t pos;
+        int item;
+        bool near;
+    };
+    auto draw_wave = [&](const auto& iv) -> Drawn {
         int fl = lane < kDWaves ? sh.ired[lane] : INT_MAX;
         fl = wave_reduce(fl, [](int x, int y) { return min(x, y); });
         // generation.cpp:106-115: min-p stops before element e >= 1 with p_e < minimum.
@@ -1301,10 +1407,16 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             near = (pos > 0 && __builtin_fabs(ch - c_before) < 1e-6) ||
                    (pos + 1 < keep && __builtin_fabs(ch - c_at) < 1e-6);
         }
+        return Drawn{pos, item, near};
+    };
 
-        // 6. The selected value's group: items with the same order key are
-        //    adjacent; its tokens are the bins with that key (not penalised)
-        //    and the penalised tokens with that key.
+    // 6. The selected value's group: items with the same order key are
+    //    adjacent; its tokens are the bins with that key (not penalised)
+    //    and the penalised tokens with that key. Wave 0.
+    auto group = [&](const auto& iv, const Drawn& d) {
+        const uint32_t pos = d.pos;
+        const int item = d.item;
+        const bool near = d.near;
         const float cap = p.softcap;
         auto item_key = [&](int i) { return order_key(u2f(static_cast<uint32_t>(items[i] >> 32))); };
         const uint32_t key = item_key(item);
@@ -1364,9 +1476,113 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         for (uint32_t x = xs + static_cast<uint32_t>(lane); x < xe; x += 64)
             sh.gx_ids[x - xs] = composite_index(extras[x]);
     };
-    if (wave == 0) {
-        if (G <= kStage) decide(LdsView{sh.st.pre, sh.st.add});
-        else decide(GlobalView{pre, aux});
+    if constexpr (kSorted) {
+        // Every value below is uniform across the block (block_chain's
+        // results are), as block_chain requires of its arguments.
+        int fl = INT_MAX;
+        for (int w = 0; w < kDWaves; ++w) fl = min(fl, sh.ired[w]);
+        // generation.cpp:106-115: min-p stops before element e >= 1 with p_e < minimum.
+        uint32_t keff = k;
+        if (!any_nan) {
+            if (q0 < minimum) keff = 1;
+            else if (fl != INT_MAX) keff = min(keff, pre[fl]);
+        }
+        Drawn d{0, 0, false};
+        if (any_nan) {
+            // NaN probabilities: no cut fires and the walk never stops.
+            d.pos = k - 1;
+            d.item = wave_find_item(pre, G, d.pos);
+        } else {
+            // generation.cpp:105-113: fp32 cumulative, top-p stop needs keep > 0.
+            double s2 = static_cast<double>(q0);
+            ChainPos cp{0, 1};
+            uint32_t keep = keff;
+            if (keff > 1 && bchain::block_chain<bchain::F32Acc, false, kDThreads>(pre, aux, G, cp, keff, s2,
+                                                                                   static_cast<double>(p.top_p), sh.bc))
+                keep = cp.elem + 1;
+            const float mass = static_cast<float>(s2);
+            // random.h:1864-1871 and generation.cpp:118-124.
+            const float u = a.uniforms[row];
+            const float choice = u * (mass - 0.0f) + 0.0f;
+            if (choice > 0.0f && choice < __builtin_inff()) {
+                ChainPos w{0, 0};
+                double c = static_cast<double>(choice);
+                const bool stop = bchain::block_chain<bchain::F32Acc, true, kDThreads>(pre, aux, G, w, keep, c, 0.0, sh.bc);
+                d.pos = stop ? w.elem : keep - 1;
+                d.item = w.item;
+            } else if (choice <= 0.0f) {
+                d.pos = 0;
+                d.item = 0;
+            } else {  // NaN or +inf: the walk never stops
+                d.pos = keep - 1;
+                d.item = wave_find_item(pre, G, d.pos);
+            }
+            // Near-boundary flag: sequential double sums of the probabilities
+            // before and through the chosen position, as the oracle defines
+            // it: an exact parallel sum when certified, else the replay.
+            double c_before = 0.0;
+            if (d.pos > 0) {
+                double sum = 0.0;
+                int mlb = INT_MAX;
+                constexpr int kU = 8;
+                for (int base = 0; base <= d.item; base += kDThreads * kU) {
+                    uint32_t stv[kU], env[kU];
+                    float qv[kU];
+#pragma unroll
+                    for (int u2 = 0; u2 < kU; ++u2) {
+                        const int i = base + u2 * kDThreads + tid;
+                        const bool in = i <= d.item;
+                        stv[u2] = in ? pre[i] : 0u;
+                        env[u2] = in ? pre[i + 1] : 0u;
+                        qv[u2] = in ? aux[i] : 0.0f;
+                    }
+#pragma unroll
+                    for (int u2 = 0; u2 < kU; ++u2) {
+                        const uint32_t en = min(env[u2], d.pos);
+                        if (en > stv[u2] && qv[u2] > 0.0f) {
+                            sum += static_cast<double>(en - stv[u2]) * static_cast<double>(qv[u2]);
+                            mlb = min(mlb, lsb_exp(qv[u2]));
+                        }
+                    }
+                }
+                sum = wave_reduce(sum, [](double x, double y) { return x + y; });
+                mlb = wave_reduce(mlb, [](int x, int y) { return min(x, y); });
+                __syncthreads();  // every earlier reader of dred / ired is done
+                if (lane == 0) {
+                    sh.dred[wave] = sum;
+                    sh.ired[wave] = mlb;
+                }
+                __syncthreads();
+                sum = 0.0;
+                mlb = INT_MAX;
+                for (int w = 0; w < kDWaves; ++w) {
+                    sum += sh.dred[w];
+                    mlb = min(mlb, sh.ired[w]);
+                }
+                if (sum == 0.0 || mlb >= exp_of(sum) - 51) {
+                    c_before = sum;
+                } else {
+                    ChainPos cp2{0, 1};
+                    double sb = static_cast<double>(q0);
+                    if (d.pos > 1)
+                        bchain::block_chain<bchain::F64Acc, false, kDThreads>(pre, aux, G, cp2, d.pos, sb, __builtin_nan(""), sh.bc);
+                    c_before = sb;
+                }
+            }
+            const double c_at = c_before + static_cast<double>(aux[d.item]);
+            const double ch = static_cast<double>(choice);
+            d.near = (d.pos > 0 && __builtin_fabs(ch - c_before) < 1e-6) ||
+                     (d.pos + 1 < keep && __builtin_fabs(ch - c_at) < 1e-6);
+        }
+        if (wave == 0) group(GlobalView{pre, aux}, d);
+    } else if (wave == 0) {
+        if (G <= kStage) {
+            const LdsView v{sh.st.pre, sh.st.add};
+            group(v, draw_wave(v));
+        } else {
+            const GlobalView v{pre, aux};
+            group(v, draw_wave(v));
+        }
     }
     __syncthreads();
 

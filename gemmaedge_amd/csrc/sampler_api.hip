@@ -139,8 +139,11 @@ int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, 
         s->fo_items_stride = ge::fo_items_stride(max_history);
         s->fo_extras_cap = max_history < ge::kFoExtrasCap ? (max_history > 0 ? max_history : 1) : ge::kFoExtrasCap;
         s->fo_bitmap_words = (static_cast<int64_t>(max_vocab) + 31) / 32;
+        // f32 full-order rows take V items each (16 B per item over the three
+        // arrays): room for up to 256 of them per launch pair, one per CU.
+        const size_t f32_rows = std::min<size_t>(rows, 256);
         const size_t items = std::max(rows * static_cast<size_t>(s->fo_items_stride),
-                                      static_cast<size_t>(ge::fo_items_stride_f32(max_vocab)));
+                                      f32_rows * static_cast<size_t>(ge::fo_items_stride_f32(max_vocab)));
         s->fo_capacity = static_cast<int64_t>(items);
         const size_t words = rows * static_cast<size_t>(s->fo_bitmap_words);
         alloc(reinterpret_cast<void**>(&s->fo_items), items * sizeof(uint64_t));

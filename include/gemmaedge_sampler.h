@@ -141,7 +141,11 @@ int ge_sampler_available(void);
 
 /* Create a sampler on `device` for up to max_rows rows of up to max_vocab
  * entries. Allocates every workspace now; ge_sample never allocates.
- * max_history is the largest per-row history length that will be passed. */
+ * max_history is the largest per-row history length that will be passed.
+ * With max_vocab > 1024 the full-order workspace (top-k off or above 1024)
+ * takes 16 bytes per item for the larger of max_rows x (about 65,300 + min(
+ * max_history, 8192)) bf16 items and min(max_rows, 256) x max_vocab f32
+ * items: about 1 GiB at 256 or more rows of V = 262,144. */
 int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history,
                       ge_sampler** out);
 

@@ -38,6 +38,10 @@ def lib():
     (10, "float ascending chained runs, 32-bit version", 20000),
     (11, "float descending chained runs, 32-bit version", 20000),
     (12, "float step and threshold from bit fields", 1000000),
+    (13, "double step from bit fields (float addend)", 1000000),
+    (14, "block replay model, float ascending with threshold", 3000),
+    (15, "block replay model, float descending with stop", 3000),
+    (16, "block replay model, double ascending", 3000),
 ])
 def test_closed_form_matches_loop(lib, which, name, trials):
     for seed in (1, 2, 3):
