@@ -106,34 +106,6 @@ struct Shared {
     int rhit;             // whether the threshold / stop fired
 };
 
-template <int kCtrl, int kRowMask, typename U>
-__device__ __forceinline__ U dpp_any(U x) {
-    if constexpr (sizeof(U) == 4) return wave::dpp<kCtrl, kRowMask>(x, 0u);
-    else return wave::dpp64<kCtrl, kRowMask>(x, 0ull);
-}
-
-template <typename A, int kCtrl, int kRowMask>
-__device__ __forceinline__ chain::ParityMap<typename A::U> scan_step(chain::ParityMap<typename A::U> v) {
-    using U = typename A::U;
-    // lanes without a source read the identity map (0, 0)
-    const chain::ParityMap<U> t{dpp_any<kCtrl, kRowMask>(v.e), dpp_any<kCtrl, kRowMask>(v.o)};
-    return chain::compose<U, A::kCap>(t, v);
-}
-
-// Exclusive scan of the lanes' maps in lane order (lane 0: the identity).
-template <typename A>
-__device__ __forceinline__ chain::ParityMap<typename A::U> wave_excl(chain::ParityMap<typename A::U> f) {
-    constexpr int kWaveShr1 = 0x138;
-    chain::ParityMap<typename A::U> v{dpp_any<kWaveShr1, 0xf>(f.e), dpp_any<kWaveShr1, 0xf>(f.o)};
-    v = scan_step<A, wave::kRowShr1, 0xf>(v);
-    v = scan_step<A, wave::kRowShr2, 0xf>(v);
-    v = scan_step<A, wave::kRowShr4, 0xf>(v);
-    v = scan_step<A, wave::kRowShr8, 0xf>(v);
-    v = scan_step<A, wave::kRowBcast15, 0xa>(v);
-    v = scan_step<A, wave::kRowBcast31, 0xc>(v);
-    return v;
-}
-
 // Items i .. i + kPer - 1: boundaries pb[0..kPer] (clamped to start(G), so
 // items past G hold no element) and addend bits ab.
 __device__ __forceinline__ void load_tile(const uint32_t* pre, const float* add, int G, int i, uint32_t* pb,
@@ -206,7 +178,7 @@ __device__ bool block_chain(const uint32_t* pre, const float* add, int G, ChainP
                 f = chain::compose<U, A::kCap>(f, chain::run_map<U, A::kCap>(nt, D, tie, odd0, big));
                 if (nt && hi == L) last = ibase + j;
             }
-            const Map x = wave_excl<A>(f);
+            const Map x = map_wave_excl<U, A::kCap>(f);
             if (lane == 63) {
                 const Map wt = chain::compose<U, A::kCap>(x, f);
                 sh.me[wave] = wt.e;

@@ -23,6 +23,34 @@ struct ChainPos {
     uint32_t elem;  // global element index (next to consume, or the event element)
 };
 
+template <int kCtrl, int kRowMask, typename U>
+__device__ __forceinline__ U dpp_move(U x) {  // lanes without a source read 0
+    if constexpr (sizeof(U) == 4) return wave::dpp<kCtrl, kRowMask>(x, 0u);
+    else return wave::dpp64<kCtrl, kRowMask>(x, 0ull);
+}
+template <int kCtrl, int kRowMask, typename U, U kCap>
+__device__ __forceinline__ chain::ParityMap<U> map_scan_step(chain::ParityMap<U> v) {
+    const chain::ParityMap<U> t{dpp_move<kCtrl, kRowMask>(v.e), dpp_move<kCtrl, kRowMask>(v.o)};
+    return chain::compose<U, kCap>(t, v);
+}
+
+// Exclusive scan of the lanes' parity maps (chain_math.h ParityMap) in lane
+// order, lane 0 getting the identity (0, 0): a wave shift by one lane
+// (wave_shr:1), then the row shifts and row broadcasts of wave::incl_u32,
+// each composing the map shifted in from lower lanes before the lane's own.
+template <typename U, U kCap>
+__device__ __forceinline__ chain::ParityMap<U> map_wave_excl(chain::ParityMap<U> f) {
+    constexpr int kWaveShr1 = 0x138;
+    chain::ParityMap<U> v{dpp_move<kWaveShr1, 0xf>(f.e), dpp_move<kWaveShr1, 0xf>(f.o)};
+    v = map_scan_step<wave::kRowShr1, 0xf, U, kCap>(v);
+    v = map_scan_step<wave::kRowShr2, 0xf, U, kCap>(v);
+    v = map_scan_step<wave::kRowShr4, 0xf, U, kCap>(v);
+    v = map_scan_step<wave::kRowShr8, 0xf, U, kCap>(v);
+    v = map_scan_step<wave::kRowBcast15, 0xa, U, kCap>(v);
+    v = map_scan_step<wave::kRowBcast31, 0xc, U, kCap>(v);
+    return v;
+}
+
 // The same walk for a float accumulator, in 32-bit integer arithmetic: the
 // accumulator is carried as its float bits, each item's increment comes from
 // the bit fields of its addend (chain_math.h step_bits), increments are capped

@@ -19,6 +19,10 @@
 // goes to its word of the row's slot area; the last chunk of the row (ticket)
 // takes the largest word. Cross-workgroup data is written with agent-scope
 // relaxed atomic stores and waited for before the ticket (no L2 writeback).
+// On small grids (every workgroup of the launch resident at once, as for one
+// row) the chunks instead store words tagged with the row's call epoch and
+// leave, and the row's last chunk polls them: one store and one load on the
+// last chunk's path instead of a store wait, a ticket and a load.
 //
 // No MFMA and no LDS staging of logits: a single HBM pass, bound by HBM
 // bandwidth for large batches and by the round trips for a single row.
@@ -66,6 +70,21 @@ __device__ __forceinline__ uint32_t pick_word(const uint32_t (&d)[N], uint32_t i
     return t[0];
 }
 
+// Polled chunk words: the composite key's value key, the index in 24 bits
+// (vocabularies below 2^24; the largest word is still the best key) and a
+// tag: 0x80 | the call epoch's low 7 bits (zero-filled words carry none). A
+// chunk with no candidate (key 0) publishes the tag alone.
+constexpr uint32_t kPollSpins = 1u << 22;  // about 4 s of polling: never reached with every chunk resident
+__device__ __forceinline__ uint64_t poll_word(uint64_t b, uint32_t tag) {
+    if (b == 0ull) return tag;
+    const uint32_t idx = composite_index(b);
+    return (static_cast<uint64_t>(composite_key(b)) << 32) | (static_cast<uint64_t>(0xffffffu - idx) << 8) | tag;
+}
+__device__ __forceinline__ uint64_t poll_composite(uint64_t w) {
+    if ((w >> 8) == 0ull) return 0ull;
+    return composite(static_cast<uint32_t>(w >> 32), 0xffffffu - static_cast<uint32_t>((w >> 8) & 0xffffffu));
+}
+
 __device__ __forceinline__ float load_one(const float* rowp, int i) { return rowp[i]; }
 __device__ __forceinline__ float load_one(const uint16_t* rowp, int i) { return bf16_to_f32(rowp[i]); }
 
@@ -100,25 +119,15 @@ __global__ __launch_bounds__(kBlock) void greedy_kernel(DevArgs a) {
     const int V = a.vocab;
     const int c0 = chunk * CHUNK;
     const int cend = min(c0 + CHUNK, V);
-    const int32_t* hist;
-    int H;
-    row_history(a, row, hist, H);
-    const bool pen = H > 0 && !(r == 1.0f);
-
-    // Logit 0 for the NaN rule of the last step (one cached load per chunk,
-    // issued now so that the last chunk does not wait for it).
-    const float x0 = load_one(rowp, 0);
 
     // Slot s of this thread is element c0 + ((s / W) * kBlock + tid) * W + s % W.
     auto elem = [&](int s) { return c0 + ((s / W) * kBlock + tid) * W + (s % W); };
 
-    // 1. The first history ids, then the chunk's loads (loads return in issue
-    //    order, so the bitmap below waits only for the ids).
-    int hid[kHistBatch];
-    if (pen) {
-#pragma unroll
-        for (int u = 0; u < kHistBatch; ++u) hid[u] = hist[min(u * kBlock + tid, H - 1)];
-    }
+    // 1. The chunk's loads first: they depend on nothing in memory. The
+    //    history's length, its first ids, logit 0 (the NaN rule of the last
+    //    step) and the row's call epoch (polled words) follow; loads return
+    //    in issue order, so the history bitmap below waits for the chunk's
+    //    data as well, but no load waits behind another's round trip.
     uint32_t d[NW];
     uint64_t vmask = ~0ull;  // in-range slots
     if (a.vec_ok && c0 + CHUNK <= V) {
@@ -148,6 +157,21 @@ __global__ __launch_bounds__(kBlock) void greedy_kernel(DevArgs a) {
             }
         }
     }
+    const int32_t* hist;
+    int H;
+    row_history(a, row, hist, H);
+    const bool pen = H > 0 && !(r == 1.0f);
+    int hid[kHistBatch];
+    if (pen) {
+#pragma unroll
+        for (int u = 0; u < kHistBatch; ++u) hid[u] = hist[min(u * kBlock + tid, H - 1)];
+    }
+    const float x0 = load_one(rowp, 0);
+    uint64_t* pw = a.poll ? a.poll + static_cast<int64_t>(row) * kPollStride : nullptr;
+    const uint32_t epoch =
+        pw ? __hip_atomic_load(reinterpret_cast<const uint32_t*>(&pw[kPollWords]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT)
+           : 0u;
     auto value = [&](int s) -> float {
         if constexpr (W == 4) return u2f(d[s]);
         else return u2f((s % 2 == 0) ? (d[s / 2] << 16) : (d[s / 2] & 0xffff0000u));
@@ -233,6 +257,55 @@ __global__ __launch_bounds__(kBlock) void greedy_kernel(DevArgs a) {
     if (lane == 0) s_best[wave] = best;
     __syncthreads();
 
+    // The NaN rule and the outputs (one lane of the row's last chunk):
+    // std::max_element (generation.cpp:66-70) keeps index 0 when its final
+    // value is NaN (NaN < x is false): token 0's final value is NaN iff its
+    // raw value is, unless the penalty is NaN and 0 is penalised. softcap(x)
+    // is NaN iff x is, except c * tanhf(inf / c) with c = inf.
+    auto finish = [&](uint64_t b) {
+        int32_t token = static_cast<int32_t>(composite_index(b));
+        bool nan0 = __builtin_isnan(x0) || (__builtin_isinf(x0) && __builtin_isnan(softcap(x0, cap)));
+        if (!nan0 && pen && __builtin_isnan(r))
+            for (int j = 0; j < H && !nan0; ++j) nan0 = hist[j] == 0;
+        if (nan0) token = 0;
+        emit_row(a, row, token, 1.0f, 0);
+    };
+
+    if (pw) {
+        // Store the tagged word and leave; the row's last chunk polls every
+        // word of the row until all carry this call's tag (each chunk stores
+        // exactly one, so the wait ends once all have run), clears them and
+        // advances the epoch for the next call (the tag guards against a word
+        // stored late, after a wait that ran out).
+        const uint32_t tag = 0x80u | (epoch & 0x7fu);
+        if (tid == 0) {
+            uint64_t b = s_best[0];
+#pragma unroll
+            for (int w = 1; w < kBlock / 64; ++w) b = max64(b, s_best[w]);
+            __hip_atomic_store(&pw[chunk], poll_word(b, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (chunk != a.cpr - 1 || wave != 0) return;
+        uint64_t w = 0ull;
+        bool all = false;
+        for (uint32_t it = 0; it < kPollSpins && !all; ++it) {
+            w = lane < a.cpr ? __hip_atomic_load(&pw[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : static_cast<uint64_t>(tag);
+            all = __ballot((static_cast<uint32_t>(w) & 0xffu) != tag) == 0ull;
+            if (!all) __builtin_amdgcn_s_sleep(1);
+        }
+        // Clear the words (zero carries no tag): a later call whose chunks
+        // outnumber this one's never reads a word left from an older call.
+        if (lane < a.cpr) __hip_atomic_store(&pw[lane], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t best = wave_max_u64(w);
+        if (lane == 0) {
+            __hip_atomic_store(&pw[kPollWords], static_cast<uint64_t>(epoch + 1u), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            if (all) finish(poll_composite(best));
+            else emit_row(a, row, -1, 0.0f, GE_FLAG_UNSUPPORTED);  // a chunk never ran: no token
+        }
+        return;
+    }
+
     // Publish the chunk's best, wait for the store, take a ticket; the last
     // chunk of the row reduces the row's words.
     uint64_t* slot = a.slots + static_cast<int64_t>(row) * kSlotWords;
@@ -254,16 +327,7 @@ __global__ __launch_bounds__(kBlock) void greedy_kernel(DevArgs a) {
         b = max64(b, __hip_atomic_load(&slot[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     b = wave_max_u64(b);
     if (lane == 0) {
-        int32_t token = static_cast<int32_t>(composite_index(b));
-        // std::max_element (generation.cpp:66-70) keeps index 0 when its
-        // final value is NaN (NaN < x is false): token 0's final value is NaN
-        // iff its raw value is, unless the penalty is NaN and 0 is penalised.
-        // softcap(x) is NaN iff x is, except c * tanhf(inf / c) with c = inf.
-        bool nan0 = __builtin_isnan(x0) || (__builtin_isinf(x0) && __builtin_isnan(softcap(x0, cap)));
-        if (!nan0 && pen && __builtin_isnan(r))
-            for (int j = 0; j < H && !nan0; ++j) nan0 = hist[j] == 0;
-        if (nan0) token = 0;
-        emit_row(a, row, token, 1.0f, 0);
+        finish(b);
         a.tickets[row] = 0u;  // ready for the next launch
     }
 }

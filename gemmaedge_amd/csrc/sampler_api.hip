@@ -31,6 +31,7 @@ struct ge_sampler {
     int max_history;
     uint32_t* tickets;
     uint64_t* slots;
+    uint64_t* poll;  // greedy calls on small grids, zero at creation
     // Full-order path (bf16 rows with k > kMaxTopK); allocated when max_vocab > kMaxTopK.
     uint64_t* fo_items;
     float* fo_aux;
@@ -134,7 +135,9 @@ int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, 
     };
     alloc(reinterpret_cast<void**>(&s->tickets), rows * sizeof(uint32_t));
     alloc(reinterpret_cast<void**>(&s->slots), rows * ge::kSlotWords * sizeof(uint64_t));
+    alloc(reinterpret_cast<void**>(&s->poll), rows * ge::kPollStride * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMemset(s->tickets, 0, rows * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(s->poll, 0, rows * ge::kPollStride * sizeof(uint64_t));
     if (max_vocab > ge::kMaxTopK) {
         s->fo_items_stride = ge::fo_items_stride(max_history);
         s->fo_extras_cap = max_history < ge::kFoExtrasCap ? (max_history > 0 ? max_history : 1) : ge::kFoExtrasCap;
@@ -168,6 +171,7 @@ void ge_sampler_destroy(ge_sampler* s) {
     DeviceGuard guard(s->device);
     (void)hipFree(s->tickets);
     (void)hipFree(s->slots);
+    (void)hipFree(s->poll);
     (void)hipFree(s->fo_items);
     (void)hipFree(s->fo_aux);
     (void)hipFree(s->fo_pre);
@@ -190,6 +194,7 @@ struct Workspace {
     int max_history;
     uint32_t* tickets;
     uint64_t* slots;
+    uint64_t* poll;  // NULL: greedy rows take tickets
     uint64_t* fo_items;
     float* fo_aux;
     uint32_t* fo_pre;
@@ -240,6 +245,11 @@ int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
     a.done = x.done;
     a.tickets = ws.tickets;
     a.slots = ws.slots;
+    // Greedy chunks publish polled words when every workgroup of the launch
+    // can be resident at once and indices fit the word's 24-bit field.
+    const bool poll = plan.run_greedy && ws.poll && cpr <= ge::kPollWords &&
+                      static_cast<int64_t>(x.rows) * cpr <= ge::kPollMaxBlocks && x.vocab < (1 << 24);
+    a.poll = poll ? ws.poll : nullptr;
     a.cpr = cpr;
     a.chunk_len = chunk_len;
     a.vec_ok = vec_ok ? 1 : 0;
@@ -334,6 +344,7 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     ws.max_history = s->max_history;
     ws.tickets = s->tickets;
     ws.slots = s->slots;
+    ws.poll = s->poll;
     ws.fo_items = s->fo_items;
     ws.fo_aux = s->fo_aux;
     ws.fo_pre = s->fo_pre;

@@ -14,6 +14,11 @@ constexpr int kMaxTopK = 1024;     // largest k of the selection path
 constexpr int kMaxChunks = 256;    // chunks (workgroups) per row
 constexpr int kMaxEpt = 64;        // elements per thread in the streaming pass
 constexpr int kSlotWords = 2048;   // per-row words of the chunk lists (all chunks together)
+// Greedy calls on small grids (every workgroup resident at once): per row,
+// kPollWords tagged chunk words and the row's call epoch, kPollStride words.
+constexpr int kPollWords = 64;
+constexpr int kPollStride = 72;
+constexpr int kPollMaxBlocks = 256;
 
 // Device-side view of one ge_sample call plus the handle's workspace.
 struct DevArgs {
@@ -41,6 +46,7 @@ struct DevArgs {
     // Workspace (allocated by ge_sampler_create, sized for max_rows x max_vocab).
     uint32_t* tickets;            // [max_rows]          zero between calls
     uint64_t* slots;              // [max_rows * kSlotWords]  per chunk: guarantee + sorted top-m list
+    uint64_t* poll;               // [max_rows * kPollStride] or NULL: greedy chunks publish polled words
 
     // Launch geometry of the streaming pass.
     int32_t cpr;                  // chunks per row
@@ -87,16 +93,28 @@ __device__ __forceinline__ ge_sample_params row_params(const DevArgs& a, int row
     return a.row_params ? a.row_params[row] : a.params;
 }
 
+// A load of a word at a wave-uniform address through the scalar unit (the
+// constant address space): it waits on the scalar counter, never behind the
+// vector loads a kernel has already issued. Only for words no thread of the
+// kernel writes before reading them.
+template <typename T>
+__device__ __forceinline__ T scalar_load(const T* p) {
+    return *(const __attribute__((address_space(4))) T*)p;
+}
+
+// The row's history. Its length is read with scalar loads (the ring length is
+// written only by the row's last workgroup, after every workgroup has read
+// it), so kernels may issue their logit loads first.
 __device__ __forceinline__ void row_history(const DevArgs& a, int row, const int32_t*& h, int& n) {
     h = nullptr;
     n = 0;
     if (a.ring) {
         h = a.ring + static_cast<int64_t>(row) * a.ring_capacity;
-        n = min(max(a.ring_len[row], 0), a.ring_capacity);
+        n = min(max(scalar_load(a.ring_len + row), 0), a.ring_capacity);
     } else if (a.history && a.history_offsets) {
-        const int s = a.history_offsets[row];
+        const int s = scalar_load(a.history_offsets + row);
         h = a.history + s;
-        n = max(a.history_offsets[row + 1] - s, 0);
+        n = max(scalar_load(a.history_offsets + row + 1) - s, 0);
     }
 }
 

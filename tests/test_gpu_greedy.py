@@ -111,3 +111,17 @@ def test_small_and_ragged_vocab(sampler, vocab):
                        history=rng.integers(0, vocab, 9).astype(np.int32),
                        offsets=np.array([0, 3, 6, 9], np.int32))
     _check(sampler, w, f"vocab {vocab}")
+
+
+def test_polled_words_across_calls(sampler):
+    """Launches small enough for every workgroup to be resident at once (one
+    row here) publish tagged chunk words that the row's last chunk polls.
+    Calls alternating between many and few chunks per row, with the winner
+    in a different chunk each time, check that no word of an earlier call is
+    taken for a later one's."""
+    rng = _rng(77)
+    for i, vocab in enumerate([V, 4096, V, 70000, V, 1000, V, V]):
+        x = (rng.standard_normal(vocab, dtype=np.float32) * np.float32(3.0)).astype(np.float32)
+        x[int(rng.integers(0, vocab))] += np.float32(40.0 - i)
+        w = small_workload(f"poll{i}", x, dict(temperature=0.0, softcap=30.0))
+        _check(sampler, w, f"polled words, call {i}, V={vocab}")
