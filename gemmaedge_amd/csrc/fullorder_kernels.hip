@@ -626,19 +626,26 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
 // complemented so that ascending order is the reference's descending one.
 // One 1024-thread workgroup per row runs a stable LSD radix sort, 8 bits per
 // pass, ping-ponging between two per-row buffers in global memory (the decide
-// kernel's aux and pre arrays, unused until then). Each wave owns a fixed
-// portion of the positions and scatters it in order through per-(portion,
-// digit) cursors, so equal digits keep their order without synchronisation
-// inside a pass; the ranks among the 64 lanes of one step come from ballots
-// over the digit's bits. The counts of the next pass are taken while this
-// one scatters. Runs of equal keys then become the items (value, count).
+// kernel's aux and pre arrays, unused until then). The four digit histograms
+// are counted once, while the keys are made. Each pass takes the row in tiles
+// of 16384 keys in order: every wave ranks its 512 consecutive keys per digit
+// (ballots over the digit's bits give the ranks among the 64 lanes of a step;
+// per-wave LDS counters carry them across steps), the tile's keys are then
+// placed in LDS grouped by digit, and the block writes each digit's group to
+// its place in the output, so consecutive threads store consecutive
+// addresses. Runs of equal keys then become the items (value, count).
 
 constexpr int kDigits = 256;
 constexpr int kSortUnroll = 8;  // 64-token steps in flight per wave
+constexpr int kTileSteps = 16;  // 64-key steps per wave per tile
+constexpr int kTileKeys = kThreads * kTileSteps;
 
 struct SortShared {
-    uint32_t cnt[2][kWaves][kDigits];  // per (portion, digit): counts, then cursors
-    uint32_t excl[kDigits];
+    uint32_t staged[kTileKeys];       // the tile's keys grouped by digit
+    uint32_t wc[kWaves][kDigits];     // per wave: keys of each digit so far in the tile, then its offset
+    uint32_t hist[4][kDigits];        // the row's four digit histograms
+    uint32_t gbase[kDigits];          // next output position of each digit
+    uint32_t toff[kDigits];           // first staged position of each digit in the tile
     uint32_t scan[kWaves];
 };
 
@@ -664,6 +671,18 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t act) {
         m &= bit ? bb : ~bb;
     }
     return m;
+}
+
+// Exclusive prefix over the 256 digits of v (one value per thread tid < 256;
+// the 4 waves holding them combine through scan[]), with the total.
+__device__ __forceinline__ uint32_t digit_excl_scan(uint32_t v, uint32_t* scan, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    const uint32_t incl = wave_incl_u32(v);
+    if (tid < kDigits && lane == 63) scan[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0;
+    for (int w = 0; w < wave && w < kDigits / 64; ++w) before += scan[w];
+    return before + incl - v;
 }
 
 template <typename T>
@@ -708,39 +727,32 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
             if (id >= 0 && id < V) atomicOr(&bitmap[id >> 5], 1u << (id & 31));
         }
     }
-    for (int i = tid; i < 2 * kWaves * kDigits; i += kThreads) (&sh.cnt[0][0][0])[i] = 0u;
+    for (int i = tid; i < 4 * kDigits; i += kThreads) (&sh.hist[0][0])[i] = 0u;
     stores_done_barrier();
 
-    // Wave w owns positions [w P, (w + 1) P), P a power of two.
-    int lgP = 6;
-    while ((static_cast<int64_t>(kWaves) << lgP) < V) ++lgP;
-    const int wlo = min(wave << lgP, V);
-    const int whi = min(wlo + (1 << lgP), V);
     const uint64_t below = (1ull << lane) - 1ull;
 
-    // 2. Final keys (generation.cpp:431-437 softcap, then the penalty) and
-    //    the counts of the first digit.
-    {
-        uint32_t* c0 = sh.cnt[0][wave];
-        for (int base = wlo; base < whi; base += 64 * kSortUnroll) {
-            float x[kSortUnroll];
-            uint32_t bw[kSortUnroll];
+    // 2. Final keys (generation.cpp:431-437 softcap, then the penalty) and the
+    //    four digit histograms.
+    for (int base = 0; base < V; base += kThreads * kSortUnroll) {
+        float x[kSortUnroll];
+        uint32_t bw[kSortUnroll];
 #pragma unroll
-            for (int u = 0; u < kSortUnroll; ++u) {
-                const int i = base + 64 * u + lane;
-                x[u] = i < whi ? load_value(rowp, i) : 0.0f;
-                bw[u] = (pen && i < whi) ? ld_l2(bitmap + (i >> 5)) : 0u;
-            }
+        for (int u = 0; u < kSortUnroll; ++u) {
+            const int i = base + u * kThreads + tid;
+            x[u] = i < V ? load_value(rowp, i) : 0.0f;
+            bw[u] = (pen && i < V) ? ld_l2(bitmap + (i >> 5)) : 0u;
+        }
 #pragma unroll
-            for (int u = 0; u < kSortUnroll; ++u) {
-                const int i = base + 64 * u + lane;
-                if (i < whi) {
-                    float f = softcap(x[u], cap);
-                    if ((bw[u] >> (i & 31)) & 1u) f = penalize(f, r);
-                    const uint32_t s = ~order_key(f);
-                    buf0[i] = s;
-                    atomicAdd(&c0[s & 255u], 1u);
-                }
+        for (int u = 0; u < kSortUnroll; ++u) {
+            const int i = base + u * kThreads + tid;
+            if (i < V) {
+                float f = softcap(x[u], cap);
+                if ((bw[u] >> (i & 31)) & 1u) f = penalize(f, r);
+                const uint32_t s = ~order_key(f);
+                buf0[i] = s;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) atomicAdd(&sh.hist[b][(s >> (8 * b)) & 255u], 1u);
             }
         }
     }
@@ -748,62 +760,99 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
     // 3. Four stable passes, least significant digit first.
     uint32_t* src = buf0;
     uint32_t* dst = buf1;
+    const int ntiles = (V + kTileKeys - 1) / kTileKeys;
     for (int pass = 0; pass < 4; ++pass) {
         const int shift = 8 * pass;
-        uint32_t (*C)[kDigits] = sh.cnt[pass & 1];
-        uint32_t (*N)[kDigits] = sh.cnt[(pass + 1) & 1];
-        stores_done_barrier();  // counts complete, the previous pass's stores done
-        if (tid < kDigits) {
-            uint32_t t = 0;
-            for (int w = 0; w < kWaves; ++w) t += C[w][tid];
-            const uint32_t incl = wave_incl_u32(t);
-            if (lane == 63) sh.scan[wave] = incl;
-            sh.excl[tid] = incl - t;
-        }
-        __syncthreads();
-        if (tid < kDigits) {
-            uint32_t run = sh.excl[tid];
-            for (int w = 0; w < wave; ++w) run += sh.scan[w];
-            for (int w = 0; w < kWaves; ++w) {
-                const uint32_t c = C[w][tid];
-                C[w][tid] = run;
-                run += c;
-            }
-        }
-        for (int i = tid; i < kWaves * kDigits; i += kThreads) (&N[0][0])[i] = 0u;
-        __syncthreads();
-        uint32_t* cur = C[wave];
-        for (int base = wlo; base < whi; base += 64 * kSortUnroll) {
-            uint32_t key[kSortUnroll];
+        stores_done_barrier();  // histograms complete, the previous pass's stores done
+        // (every thread takes part in the scan's barrier; gbase is first read
+        // in step d, after three more)
+        const uint32_t g0 = digit_excl_scan(tid < kDigits ? sh.hist[pass][tid] : 0u, sh.scan, tid);
+        if (tid < kDigits) sh.gbase[tid] = g0;
+        uint32_t key[kTileSteps], nkey[kTileSteps];
+        auto load_tile = [&](int t, uint32_t* kv) {
 #pragma unroll
-            for (int u = 0; u < kSortUnroll; ++u) {
-                const int i = base + 64 * u + lane;
-                key[u] = i < whi ? ld_l2(src + i) : 0u;
+            for (int u = 0; u < kTileSteps; ++u) {
+                const int i = t * kTileKeys + wave * (64 * kTileSteps) + u * 64 + lane;
+                kv[u] = i < V ? ld_l2(src + i) : 0u;
             }
+        };
+        load_tile(0, key);
+        uint32_t tot_prev = 0;  // (thread d < 256) keys of digit d in the previous tile
+        for (int t = 0; t < ntiles; ++t) {
+            if (t + 1 < ntiles) load_tile(t + 1, nkey);
+            // a. Ranks among this wave's keys of the same digit, in position order.
+            //    (The previous tile's step d read staged, gbase and toff before
+            //    the barrier below; its readers of wc finished before step d.)
+            for (int d = lane; d < kDigits; d += 64) sh.wc[wave][d] = 0u;  // only this wave uses its row
+            uint32_t lr[kTileSteps];
 #pragma unroll
-            for (int u = 0; u < kSortUnroll; ++u) {
-                const bool act = base + 64 * u + lane < whi;
+            for (int u = 0; u < kTileSteps; ++u) {
+                const int i = t * kTileKeys + wave * (64 * kTileSteps) + u * 64 + lane;
+                const bool act = i < V;
                 const uint64_t am = __ballot(act);
-                if (am == 0ull) break;
                 const uint32_t d = (key[u] >> shift) & 255u;
                 const uint64_t mm = match_digit(d, am);
+                lr[u] = 0u;
                 if (act) {
-                    // Lanes of one digit read the same cursor, then all
-                    // write the same advanced value (in program order, so
-                    // the next step reads it).
-                    const uint32_t c = cur[d];
-                    const uint32_t dest = c + static_cast<uint32_t>(__popcll(mm & below));
-                    dst[dest] = key[u];
-                    cur[d] = c + static_cast<uint32_t>(__popcll(mm));
-                    if (pass < 3) atomicAdd(&N[dest >> lgP][(key[u] >> (shift + 8)) & 255u], 1u);
+                    // Lanes of one digit read the same counter, then all write
+                    // the same advanced value (in program order, so the next
+                    // step reads it).
+                    const uint32_t c = sh.wc[wave][d];
+                    lr[u] = c + static_cast<uint32_t>(__popcll(mm & below));
+                    sh.wc[wave][d] = c + static_cast<uint32_t>(__popcll(mm));
                 }
             }
+            __syncthreads();
+            // b. Per digit: each wave's offset among the tile's keys of that
+            //    digit, and the digit's first position in the staged tile.
+            uint32_t tot = 0;
+            if (tid < kDigits) {
+                sh.gbase[tid] += tot_prev;  // the previous tile's keys of this digit are placed
+                for (int w = 0; w < kWaves; ++w) {
+                    const uint32_t c = sh.wc[w][tid];
+                    sh.wc[w][tid] = tot;
+                    tot += c;
+                }
+            }
+            const uint32_t to = digit_excl_scan(tid < kDigits ? tot : 0u, sh.scan, tid);
+            if (tid < kDigits) sh.toff[tid] = to;
+            __syncthreads();
+            // c. The tile's keys grouped by digit, in position order inside a group.
+#pragma unroll
+            for (int u = 0; u < kTileSteps; ++u) {
+                const int i = t * kTileKeys + wave * (64 * kTileSteps) + u * 64 + lane;
+                if (i < V) {
+                    const uint32_t d = (key[u] >> shift) & 255u;
+                    sh.staged[sh.toff[d] + sh.wc[wave][d] + lr[u]] = key[u];
+                }
+            }
+            __syncthreads();
+            // d. Each digit's group to its place in the output.
+            const int nt = min(kTileKeys, V - t * kTileKeys);
+#pragma unroll
+            for (int u = 0; u < kTileSteps; ++u) {
+                const int q = u * kThreads + tid;
+                if (q < nt) {
+                    const uint32_t kv = sh.staged[q];
+                    const uint32_t d = (kv >> shift) & 255u;
+                    dst[sh.gbase[d] + static_cast<uint32_t>(q) - sh.toff[d]] = kv;
+                }
+            }
+            tot_prev = tot;
+#pragma unroll
+            for (int u = 0; u < kTileSteps; ++u) key[u] = nkey[u];
         }
-        uint32_t* t = src;
+        uint32_t* tmp = src;
         src = dst;
-        dst = t;
+        dst = tmp;
     }
     stores_done_barrier();
+
+    // Wave w owns positions [w P, (w + 1) P), P a power of two, in the items.
+    int lgP = 6;
+    while ((static_cast<int64_t>(kWaves) << lgP) < V) ++lgP;
+    const int wlo = min(wave << lgP, V);
+    const int whi = min(wlo + (1 << lgP), V);
 
     // 4. Items: runs of equal keys in the sorted order (src); their starts
     //    go to the other buffer.
