@@ -107,24 +107,26 @@ struct Shared {
 };
 
 // Items i .. i + kPer - 1: boundaries pb[0..kPer] (clamped to start(G), so
-// items past G hold no element) and addend bits ab.
-__device__ __forceinline__ void load_tile(const uint32_t* pre, const float* add, int G, int i, uint32_t* pb,
-                                          uint32_t* ab) {
+// items past G hold no element) and the bits of their addends, add[i] *
+// scale (one float multiplication, so the addend is exactly the float a
+// separate scaling pass would have stored; scale 1 leaves it unchanged).
+__device__ __forceinline__ void load_tile(const uint32_t* pre, const float* add, float scale, int G, int i,
+                                          uint32_t* pb, uint32_t* ab) {
     if (i + kPer <= G) {  // pre has G + 1 entries; i is a multiple of kPer
         const uint4 p0 = *reinterpret_cast<const uint4*>(pre + i);
         const uint4 p1 = *reinterpret_cast<const uint4*>(pre + i + 4);
         pb[0] = p0.x; pb[1] = p0.y; pb[2] = p0.z; pb[3] = p0.w;
         pb[4] = p1.x; pb[5] = p1.y; pb[6] = p1.z; pb[7] = p1.w;
         pb[8] = pre[i + 8];
-        const uint4 a0 = *reinterpret_cast<const uint4*>(add + i);
-        const uint4 a1 = *reinterpret_cast<const uint4*>(add + i + 4);
-        ab[0] = a0.x; ab[1] = a0.y; ab[2] = a0.z; ab[3] = a0.w;
-        ab[4] = a1.x; ab[5] = a1.y; ab[6] = a1.z; ab[7] = a1.w;
+        const float4 a0 = *reinterpret_cast<const float4*>(add + i);
+        const float4 a1 = *reinterpret_cast<const float4*>(add + i + 4);
+        ab[0] = f2u(a0.x * scale); ab[1] = f2u(a0.y * scale); ab[2] = f2u(a0.z * scale); ab[3] = f2u(a0.w * scale);
+        ab[4] = f2u(a1.x * scale); ab[5] = f2u(a1.y * scale); ab[6] = f2u(a1.z * scale); ab[7] = f2u(a1.w * scale);
     } else {
 #pragma unroll
         for (int j = 0; j <= kPer; ++j) pb[j] = pre[min(i + j, G)];
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) ab[j] = i + j < G ? f2u(add[i + j]) : 0u;
+        for (int j = 0; j < kPer; ++j) ab[j] = i + j < G ? f2u(add[i + j] * scale) : 0u;
     }
 }
 
@@ -140,10 +142,10 @@ __device__ __forceinline__ bool exceeds(const Bin& b, U r) {
 // thr (NaN: never), descending ones before the first element with c <= a.
 // Returns true on a stop with cp at the stop element; otherwise false with
 // cp.elem == L and cp.item holding element L - 1. Requires L <= start(G);
-// pre and add 16-byte aligned.
+// pre and add 16-byte aligned. Item i's addend is add[i] * scale.
 template <typename A, bool kDesc, int kThreads>
-__device__ bool block_chain(const uint32_t* pre, const float* add, int G, ChainPos& cp, uint32_t L, double& s,
-                            double thr, Shared<kThreads / 64>& sh) {
+__device__ bool block_chain(const uint32_t* pre, const float* add, float scale, int G, ChainPos& cp, uint32_t L,
+                            double& s, double thr, Shared<kThreads / 64>& sh) {
     using U = typename A::U;
     using Map = chain::ParityMap<U>;
     constexpr int kWaves = kThreads / 64;
@@ -154,12 +156,12 @@ __device__ bool block_chain(const uint32_t* pre, const float* add, int G, ChainP
     if (!(cp.elem < L && cp.item < G)) return false;
     int t0 = cp.item / kTile * kTile;
     uint32_t pb[kPer + 1], ab[kPer];
-    load_tile(pre, add, G, t0 + tid * kPer, pb, ab);
+    load_tile(pre, add, scale, G, t0 + tid * kPer, pb, ab);
     for (;;) {
         // the next tile's loads are in flight while this one is scanned
         uint32_t npb[kPer + 1], nab[kPer];
         const bool more = t0 + kTile < G;
-        if (more) load_tile(pre, add, G, t0 + kTile + tid * kPer, npb, nab);
+        if (more) load_tile(pre, add, scale, G, t0 + kTile + tid * kPer, npb, nab);
         const uint32_t tile_end = pre[min(t0 + kTile, G)];
         const int ibase = t0 + tid * kPer;
         for (;;) {  // one pass per binade the tile's remaining items start in

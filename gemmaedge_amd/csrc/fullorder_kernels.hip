@@ -1307,7 +1307,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         } else if (!certified) {
             ChainPos cp{0, 1};
             double s2 = static_cast<double>(p0);
-            if (k > 1) bchain::block_chain<bchain::F64Acc, false, kDThreads>(pre, aux, G, cp, k, s2, __builtin_nan(""), sh.bc);
+            if (k > 1) bchain::block_chain<bchain::F64Acc, false, kDThreads>(pre, aux, 1.0f, G, cp, k, s2, __builtin_nan(""), sh.bc);
             den = s2;
         }
         if (tid == 0) sh.den = den;
@@ -1335,25 +1335,15 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     const float minimum = q0 * p.min_p;
     int first_low = INT_MAX;
     if constexpr (kSorted) {
-        constexpr int kU = 16;
-        for (int base = 0; base < G; base += kDThreads * kU) {
-            float pv[kU];
-            uint32_t piv[kU];
-#pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                const int i = base + u * kDThreads + tid;
-                pv[u] = i < G ? aux[i] : 0.0f;
-                piv[u] = i < G ? pre[i] : 0u;
-            }
-#pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                const int i = base + u * kDThreads + tid;
-                if (i < G) {
-                    const float q = pv[u] * inv;
-                    aux[i] = q;
-                    if (i >= 1 && first_low == INT_MAX && q < minimum && piv[u] < k) first_low = i;
-                }
-            }
+        // The probabilities stay unscaled in aux: every reader takes
+        // aux[i] * inv, the float operation a scaling pass would store. With
+        // no NaN they are non-increasing (sorted values, monotone expf), so
+        // the min-p cut (generation.cpp:106-108: the first element e >= 1
+        // with p_e < minimum, within the top k) is a search, not a pass.
+        if (!any_nan && minimum > 0.0f && G > 1) {
+            const uint32_t pp = wave_partition_point(1u, static_cast<uint32_t>(G),
+                                                     [&](uint32_t i) { return !(aux[i] * inv < minimum); });
+            if (pp < static_cast<uint32_t>(G) && pre[pp] < k) first_low = static_cast<int>(pp);
         }
     } else {
         for (int i = tid; i < G; i += kDThreads) {  // this thread staged item i in 4a
@@ -1546,7 +1536,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             double s2 = static_cast<double>(q0);
             ChainPos cp{0, 1};
             uint32_t keep = keff;
-            if (keff > 1 && bchain::block_chain<bchain::F32Acc, false, kDThreads>(pre, aux, G, cp, keff, s2,
+            if (keff > 1 && bchain::block_chain<bchain::F32Acc, false, kDThreads>(pre, aux, inv, G, cp, keff, s2,
                                                                                    static_cast<double>(p.top_p), sh.bc))
                 keep = cp.elem + 1;
             const float mass = static_cast<float>(s2);
@@ -1556,7 +1546,8 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             if (choice > 0.0f && choice < __builtin_inff()) {
                 ChainPos w{0, 0};
                 double c = static_cast<double>(choice);
-                const bool stop = bchain::block_chain<bchain::F32Acc, true, kDThreads>(pre, aux, G, w, keep, c, 0.0, sh.bc);
+                const bool stop =
+                    bchain::block_chain<bchain::F32Acc, true, kDThreads>(pre, aux, inv, G, w, keep, c, 0.0, sh.bc);
                 d.pos = stop ? w.elem : keep - 1;
                 d.item = w.item;
             } else if (choice <= 0.0f) {
@@ -1583,7 +1574,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                         const bool in = i <= d.item;
                         stv[u2] = in ? pre[i] : 0u;
                         env[u2] = in ? pre[i + 1] : 0u;
-                        qv[u2] = in ? aux[i] : 0.0f;
+                        qv[u2] = in ? aux[i] * inv : 0.0f;
                     }
 #pragma unroll
                     for (int u2 = 0; u2 < kU; ++u2) {
@@ -1614,11 +1605,12 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                     ChainPos cp2{0, 1};
                     double sb = static_cast<double>(q0);
                     if (d.pos > 1)
-                        bchain::block_chain<bchain::F64Acc, false, kDThreads>(pre, aux, G, cp2, d.pos, sb, __builtin_nan(""), sh.bc);
+                        bchain::block_chain<bchain::F64Acc, false, kDThreads>(pre, aux, inv, G, cp2, d.pos, sb,
+                                                                              __builtin_nan(""), sh.bc);
                     c_before = sb;
                 }
             }
-            const double c_at = c_before + static_cast<double>(aux[d.item]);
+            const double c_at = c_before + static_cast<double>(aux[d.item] * inv);
             const double ch = static_cast<double>(choice);
             d.near = (d.pos > 0 && __builtin_fabs(ch - c_before) < 1e-6) ||
                      (d.pos + 1 < keep && __builtin_fabs(ch - c_at) < 1e-6);
@@ -1768,7 +1760,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         }
     }
     __syncthreads();
-    finish(sh.token, aux[sh.item], sh.near ? GE_FLAG_NEAR_BOUNDARY : 0);
+    finish(sh.token, kSorted ? aux[sh.item] * inv : aux[sh.item], sh.near ? GE_FLAG_NEAR_BOUNDARY : 0);
 }
 
 // The per-row pointers of rows [r0, r0 + n) of a call, as a call of its own
