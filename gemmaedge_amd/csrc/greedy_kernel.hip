@@ -219,43 +219,47 @@ __global__ __launch_bounds__(kBlock) void greedy_kernel(DevArgs a) {
         const uint32_t w = pick_word(d, static_cast<uint32_t>(W == 4 ? sp : sp / 2));
         xp = W == 4 ? u2f(w) : u2f((sp % 2 == 0) ? (w << 16) : (w & 0xffff0000u));
     }
-    // One softcap pass, two independent chains per lane: lanes 0 and 1 cap
-    // M and the key below it (equal values mean a tie class wider than one
-    // key); every lane caps its penalised value.
-    const float s01 = softcap(key_value(M - static_cast<uint32_t>(lane & 1)), cap);
-    const float fp = pen ? softcap(xp, cap) : 0.0f;
-    uint64_t best = 0ull;
+    // One softcap evaluation per lane: lanes 0 and 1 cap M and the key below
+    // it (equal values mean a tie class wider than one key), the others
+    // their first penalised value; lanes 0 and 1 cap theirs in a second
+    // round, only when one of them has one.
+    const bool pair = lane < 2;
+    const float sc = softcap(pair ? key_value(M - static_cast<uint32_t>(lane)) : xp, cap);
+    float fp = pair ? 0.0f : sc;
+    if (pen && __any(pair && sp >= 0)) {
+        const float f2 = softcap(xp, cap);
+        if (pair) fp = f2;
+    }
+    uint64_t cand = 0ull;  // this lane's best composite key
     if (M != 0u) {
-        const float target = u2f(wave::readlane(f2u(s01), 0));
-        const float below = u2f(wave::readlane(f2u(s01), 1));
+        const float target = u2f(wave::readlane(f2u(sc), 0));
+        const float below = u2f(wave::readlane(f2u(sc), 1));
         const uint32_t L = (cap > 0.0f) ? tie_floor_given(M, cap, target, below) : M;
-        // 3. The lowest index among unpenalised tokens in the class [L, M].
+        // 3. The lowest index among unpenalised tokens in the class [L, M]
+        //    (the wave's maximum below picks the lowest).
         uint32_t imin = 0xffffffffu;
 #pragma unroll
         for (int s = 0; s < EPT; ++s) {
             const uint32_t k = key_of(s);
             if (k >= L && k != 0u) imin = min(imin, static_cast<uint32_t>(elem(s)));
         }
-        imin = wave::min_u32(imin);
-        best = composite(order_key(cap > 0.0f ? target : key_value(M)), imin);
+        if (imin != 0xffffffffu) cand = composite(order_key(cap > 0.0f ? target : key_value(M)), imin);
     }
     // 4. Penalised tokens with their exact final values (softcap, then the
     //    penalty); a lane's further penalised slots, rare, one at a time.
     if (pen && __any(sp >= 0)) {
-        uint64_t pb = sp >= 0 ? composite(order_key(penalize(fp, r)), static_cast<uint32_t>(elem(sp))) : 0ull;
+        if (sp >= 0) cand = max64(cand, composite(order_key(penalize(fp, r)), static_cast<uint32_t>(elem(sp))));
         while (__any(pmv != 0ull)) {
             if (pmv != 0ull) {
                 const int s = __builtin_ctzll(pmv);
                 pmv &= pmv - 1ull;
                 const uint32_t w = pick_word(d, static_cast<uint32_t>(W == 4 ? s : s / 2));
                 const float x = W == 4 ? u2f(w) : u2f((s % 2 == 0) ? (w << 16) : (w & 0xffff0000u));
-                pb = max64(pb, composite(order_key(penalize(softcap(x, cap), r)), static_cast<uint32_t>(elem(s))));
+                cand = max64(cand, composite(order_key(penalize(softcap(x, cap), r)), static_cast<uint32_t>(elem(s))));
             }
         }
-        best = max64(best, wave_max_u64(pb));
     }
-    if (lane == 0) s_best[wave] = best;
-    __syncthreads();
+    const uint64_t best = wave_max_u64(cand);
 
     // The NaN rule and the outputs (one lane of the row's last chunk):
     // std::max_element (generation.cpp:66-70) keeps index 0 when its final
@@ -272,39 +276,53 @@ __global__ __launch_bounds__(kBlock) void greedy_kernel(DevArgs a) {
     };
 
     if (pw) {
-        // Store the tagged word and leave; the row's last chunk polls every
-        // word of the row until all carry this call's tag (each chunk stores
-        // exactly one, so the wait ends once all have run), clears them and
-        // advances the epoch for the next call (the tag guards against a word
-        // stored late, after a wait that ran out).
+        // Each wave stores its tagged word and leaves (no barrier in the
+        // chunk; words [4 c, 4 c + 4) belong to chunk c). The row's last
+        // chunk polls every word of the row until all carry this call's tag
+        // (each wave stores exactly one, so the wait ends once all have run),
+        // clears them and advances the epoch for the next call (the tag guards
+        // against a word stored late, after a wait that ran out).
+        constexpr int kWpc = kBlock / 64;
         const uint32_t tag = 0x80u | (epoch & 0x7fu);
-        if (tid == 0) {
-            uint64_t b = s_best[0];
-#pragma unroll
-            for (int w = 1; w < kBlock / 64; ++w) b = max64(b, s_best[w]);
-            __hip_atomic_store(&pw[chunk], poll_word(b, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if (lane == 0)
+            __hip_atomic_store(&pw[chunk * kWpc + wave], poll_word(best, tag), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         if (chunk != a.cpr - 1 || wave != 0) return;
-        uint64_t w = 0ull;
+        const int nw = a.cpr * kWpc;  // <= kPollWords
+        uint64_t w[kWpc];
         bool all = false;
         for (uint32_t it = 0; it < kPollSpins && !all; ++it) {
-            w = lane < a.cpr ? __hip_atomic_load(&pw[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                             : static_cast<uint64_t>(tag);
-            all = __ballot((static_cast<uint32_t>(w) & 0xffu) != tag) == 0ull;
+            bool mine = true;
+#pragma unroll
+            for (int j = 0; j < kWpc; ++j) {
+                const int q = j * 64 + lane;
+                w[j] = q < nw ? __hip_atomic_load(&pw[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : static_cast<uint64_t>(tag);
+                mine = mine && (static_cast<uint32_t>(w[j]) & 0xffu) == tag;
+            }
+            all = __ballot(!mine) == 0ull;
             if (!all) __builtin_amdgcn_s_sleep(1);
         }
         // Clear the words (zero carries no tag): a later call whose chunks
         // outnumber this one's never reads a word left from an older call.
-        if (lane < a.cpr) __hip_atomic_store(&pw[lane], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint64_t best = wave_max_u64(w);
+        uint64_t wb = 0ull;
+#pragma unroll
+        for (int j = 0; j < kWpc; ++j) {
+            const int q = j * 64 + lane;
+            if (q < nw) __hip_atomic_store(&pw[q], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wb = max64(wb, w[j]);
+        }
+        const uint64_t rbest = wave_max_u64(wb);
         if (lane == 0) {
             __hip_atomic_store(&pw[kPollWords], static_cast<uint64_t>(epoch + 1u), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-            if (all) finish(poll_composite(best));
+            if (all) finish(poll_composite(rbest));
             else emit_row(a, row, -1, 0.0f, GE_FLAG_UNSUPPORTED);  // a chunk never ran: no token
         }
         return;
     }
+    if (lane == 0) s_best[wave] = best;
+    __syncthreads();
 
     // Publish the chunk's best, wait for the store, take a ticket; the last
     // chunk of the row reduces the row's words.

@@ -247,7 +247,7 @@ int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
     a.slots = ws.slots;
     // Greedy chunks publish polled words when every workgroup of the launch
     // can be resident at once and indices fit the word's 24-bit field.
-    const bool poll = plan.run_greedy && ws.poll && cpr <= ge::kPollWords &&
+    const bool poll = plan.run_greedy && ws.poll && cpr <= ge::kPollChunks &&
                       static_cast<int64_t>(x.rows) * cpr <= ge::kPollMaxBlocks && x.vocab < (1 << 24);
     a.poll = poll ? ws.poll : nullptr;
     a.cpr = cpr;

@@ -15,9 +15,11 @@ constexpr int kMaxChunks = 256;    // chunks (workgroups) per row
 constexpr int kMaxEpt = 64;        // elements per thread in the streaming pass
 constexpr int kSlotWords = 2048;   // per-row words of the chunk lists (all chunks together)
 // Greedy calls on small grids (every workgroup resident at once): per row,
-// kPollWords tagged chunk words and the row's call epoch, kPollStride words.
-constexpr int kPollWords = 64;
-constexpr int kPollStride = 72;
+// one tagged word per wave of up to kPollChunks chunks, then the row's call
+// epoch; kPollStride words.
+constexpr int kPollChunks = 64;
+constexpr int kPollWords = kPollChunks * (kBlock / 64);
+constexpr int kPollStride = kPollWords + 8;
 constexpr int kPollMaxBlocks = 256;
 
 // Device-side view of one ge_sample call plus the handle's workspace.
