@@ -60,7 +60,12 @@ constexpr uint32_t kHighBin = 0xFF80u;    // +inf
 constexpr int kSpillCap = 512;
 constexpr uint64_t kSat = static_cast<uint64_t>(1) << 62;
 
-enum : uint32_t { kMetaItems = 0, kMetaExtras = 1, kMetaNan = 2, kMetaStatus = 3 };
+enum : uint32_t {
+    kMetaItems = 0, kMetaExtras = 1, kMetaNan = 2, kMetaStatus = 3,
+    // sorted rows only: the top k's exps, from the sort kernel (their sum
+    // as two words of a double, the lowest set bit, any NaN)
+    kMetaSumLo = 4, kMetaSumHi = 5, kMetaMinLsb = 6, kMetaAnyNan = 7
+};
 // kStatusFallback: items of a flagged bf16 row, made by the fallback sort;
 // kStatusSkip: a row the fallback pass leaves as the first pass wrote it.
 enum : uint32_t { kStatusOk = 0, kStatusTooManyPenalised = 1, kStatusFallback = 2, kStatusSkip = 3 };
@@ -200,6 +205,14 @@ __device__ __forceinline__ uint64_t wave_incl_u64_sat(uint64_t v) {
 __device__ __forceinline__ uint64_t sat_mul(uint64_t n, uint64_t d) {
     const uint64_t lo = n * d;
     return (__umul64hi(n, d) != 0 || lo > kSat) ? kSat : lo;
+}
+
+// Elements of an item (first element `first`, `n` elements) inside the top k.
+// The saturating subtract is spelled as the builtin: clang has folded the
+// form `first >= k ? 0 : min(n, k - first)` into an unguarded `k - first`
+// marked no-wrap, so items past k were counted.
+__device__ __forceinline__ uint32_t top_k_count(uint32_t first, uint32_t n, uint32_t k) {
+    return min(n, __builtin_elementwise_sub_sat(k, first));
 }
 
 __device__ __forceinline__ int lsb_exp(float x) {  // exponent of the lowest set bit, x > 0 finite
@@ -378,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void fo_hist_kernel(DevArgs a) {
     uint32_t* bitmap = a.fo_bitmap + static_cast<int64_t>(row) * a.fo_bitmap_words;
     uint64_t* extras = a.fo_extras + static_cast<int64_t>(row) * a.fo_extras_cap;
     uint64_t* items = a.fo_items + static_cast<int64_t>(row) * a.fo_items_stride;
-    uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * 4;
+    uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * kMetaWords;
     const uint32_t ecap = static_cast<uint32_t>(a.fo_extras_cap);
 
     if (tid < 4) sh.counters[tid] = 0;
@@ -647,6 +660,9 @@ struct SortShared {
     uint32_t gbase[kDigits];          // next output position of each digit
     uint32_t toff[kDigits];           // first staged position of each digit in the tile
     uint32_t scan[kWaves];
+    double dred[kWaves];              // per-wave sums, lowest set bits, NaN flags of the exps
+    int ired[kWaves];
+    uint32_t ured[kWaves];
 };
 
 // Buffer reads of the sort read from L2 (agent-scope loads skip the CU's L1),
@@ -699,10 +715,10 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
     if (a.fo_fallback) {
         // Only rows the first pass flagged (its status word, at the call
         // row); the decide kernel of this pass skips the others.
-        const uint32_t st = a.fo_meta[static_cast<int64_t>(a.fo_row0 + row) * 4 + kMetaStatus];
+        const uint32_t st = a.fo_meta[static_cast<int64_t>(a.fo_row0 + row) * kMetaWords + kMetaStatus];
         __syncthreads();  // every thread has read it before thread 0 may rewrite it below
         if (st != kStatusTooManyPenalised) {
-            if (tid == 0) a.fo_meta[static_cast<int64_t>(row) * 4 + kMetaStatus] = kStatusSkip;
+            if (tid == 0) a.fo_meta[static_cast<int64_t>(row) * kMetaWords + kMetaStatus] = kStatusSkip;
             return;
         }
     }
@@ -716,7 +732,7 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
     const bool pen = H > 0 && !(r == 1.0f);
     uint32_t* bitmap = a.fo_bitmap + static_cast<int64_t>(row) * a.fo_bitmap_words;
     uint64_t* items = a.fo_items + static_cast<int64_t>(row) * a.fo_items_stride;
-    uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * 4;
+    uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * kMetaWords;
     uint32_t* buf0 = reinterpret_cast<uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
     uint32_t* buf1 = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
 
@@ -900,8 +916,23 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
     }
     if (tid == 0) istart[G] = static_cast<uint32_t>(V);
     stores_done_barrier();
+    // 5. The items (value, count), and each item's exp in aux for the decide
+    //    kernel (generation.cpp:94-97: p = exp((l - max) * (1/T)), max the
+    //    first item's value) with the certificate of their double sum over the
+    //    top k (the sum, the lowest set bit, any NaN). aux holds the sorted
+    //    keys being read: rounds of 4096 items read their keys, wait at a
+    //    barrier, then write; later rounds read only keys at or after their
+    //    own items' positions, past every position written before.
+    const uint32_t key0 = ~ld_l2(s);
+    const float vmax = key0 == kKeyNaN ? u2f(0x7fc00000u) : key_value(key0);
+    const bool last_nan = ~ld_l2(s + V - 1) == kKeyNaN;  // (read before aux is rewritten)
+    const float inv_temp = 1.0f / p.temperature;
+    float* aux = a.fo_aux + static_cast<int64_t>(row) * a.fo_items_stride;
+    double S = 0.0;
+    int minlsb = INT_MAX;
+    bool nan = false;
     constexpr int kQ = 4;
-    for (uint32_t q0 = tid; q0 < G; q0 += kThreads * kQ) {
+    for (uint32_t q0 = tid; q0 - tid < G; q0 += kThreads * kQ) {  // uniform trip count
         uint32_t st[kQ], en[kQ];
 #pragma unroll
         for (int u = 0; u < kQ; ++u) {
@@ -912,18 +943,55 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
         uint32_t kv[kQ];
 #pragma unroll
         for (int u = 0; u < kQ; ++u) kv[u] = q0 + u * kThreads < G ? ld_l2(s + st[u]) : 0u;
+        // Every thread's key loads of this round have returned before any
+        // thread writes aux: an item's first key can sit at the position of
+        // a later item of the same round (a barrier alone does not wait for
+        // loads in flight).
+        stores_done_barrier();
 #pragma unroll
         for (int u = 0; u < kQ; ++u) {
             const uint32_t q = q0 + u * kThreads;
             if (q < G) {
                 const uint32_t key = ~kv[u];
                 const uint32_t val = key == kKeyNaN ? 0x7fc00000u : f2u(key_value(key));
-                items[q] = (static_cast<uint64_t>(val) << 32) | (en[u] - st[u]);
+                const uint32_t n = en[u] - st[u];
+                items[q] = (static_cast<uint64_t>(val) << 32) | n;
+                const float pe = expf_glibc((u2f(val) - vmax) * inv_temp);
+                aux[q] = pe;
+                const uint32_t nk = top_k_count(st[u], n, k);
+                if (nk) {
+                    if (pe != pe) nan = true;
+                    else if (pe > 0.0f) {
+                        minlsb = min(minlsb, lsb_exp(pe));
+                        S += static_cast<double>(nk) * static_cast<double>(pe);
+                    }
+                }
             }
         }
     }
+    S = wave::sum_f64(S);  // a certificate: exact whenever it certifies
+    minlsb = wave::min_i32(minlsb);
+    const uint32_t nanw = __ballot(nan) != 0ull ? 1u : 0u;
+    if (lane == 0) {
+        sh.dred[wave] = S;
+        sh.ired[wave] = minlsb;
+        sh.ured[wave] = nanw;
+    }
+    __syncthreads();
     if (tid == 0) {
-        const bool last_nan = ~ld_l2(s + V - 1) == kKeyNaN;
+        double Sp = 0.0;
+        int ml = INT_MAX;
+        uint32_t nn = 0;
+        for (int w = 0; w < kWaves; ++w) {
+            Sp += sh.dred[w];
+            ml = min(ml, sh.ired[w]);
+            nn |= sh.ured[w];
+        }
+        const uint64_t sb = __builtin_bit_cast(uint64_t, Sp);
+        meta[kMetaSumLo] = static_cast<uint32_t>(sb);
+        meta[kMetaSumHi] = static_cast<uint32_t>(sb >> 32);
+        meta[kMetaMinLsb] = static_cast<uint32_t>(ml);
+        meta[kMetaAnyNan] = nn;
         meta[kMetaItems] = G;
         meta[kMetaExtras] = 0;
         meta[kMetaNan] = last_nan ? static_cast<uint32_t>(V) - ld_l2(istart + G - 1) : 0u;
@@ -1170,14 +1238,14 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         if (tid == 0 && !a.fo_fallback) skipped_row(a, row);
         return;
     }
-    if (a.fo_fallback && a.fo_meta[static_cast<int64_t>(row) * 4 + kMetaStatus] != kStatusFallback) return;
+    if (a.fo_fallback && a.fo_meta[static_cast<int64_t>(row) * kMetaWords + kMetaStatus] != kStatusFallback) return;
 
     const int32_t* hist;
     int H;
     history_of(a, row, hist, H);
     const bool pen = H > 0 && !(p.repetition_penalty == 1.0f);
     uint32_t* bitmap = a.fo_bitmap + static_cast<int64_t>(row) * a.fo_bitmap_words;
-    const uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * 4;
+    const uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * kMetaWords;
     // The bitmap is all zero again after every call. It is cleared from the
     // history before the token is appended: with a device ring the history
     // IS the ring, and once it is full the new token overwrites the oldest
@@ -1217,35 +1285,13 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     bool nan = false;
     uint32_t run_base = 0;
     if constexpr (kSorted) {
-        // The sort kernel left every item's first element in pre[] (and
-        // pre[G] = V), so the exps need no scan; 4 items per thread in flight.
-        constexpr int kU = 16;
-        for (int base = 0; base < G; base += kDThreads * kU) {
-            uint64_t itv[kU];
-            uint32_t piv[kU];
-#pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                const int i = base + u * kDThreads + tid;
-                itv[u] = i < G ? items[i] : 0ull;
-                piv[u] = i < G ? pre[i] : 0u;
-            }
-#pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                const int i = base + u * kDThreads + tid;
-                if (i < G) {
-                    const uint32_t n = static_cast<uint32_t>(itv[u]);
-                    const uint32_t nk = piv[u] >= k ? 0u : min(n, k - piv[u]);
-                    const float pe = expf_glibc((u2f(static_cast<uint32_t>(itv[u] >> 32)) - vmax) * inv_temp);
-                    aux[i] = pe;
-                    if (nk) {
-                        if (pe != pe) nan = true;
-                        else if (pe > 0.0f) {
-                            minlsb = min(minlsb, lsb_exp(pe));
-                            S += static_cast<double>(nk) * static_cast<double>(pe);
-                        }
-                    }
-                }
-            }
+        // The sort kernel wrote each item's exp to aux (and every item's first
+        // element to pre, pre[G] = V) and the certificate of their double sum
+        // over the top k to the row's meta words.
+        if (tid == 0) {
+            S = __builtin_bit_cast(double, (static_cast<uint64_t>(meta[kMetaSumHi]) << 32) | meta[kMetaSumLo]);
+            minlsb = static_cast<int>(meta[kMetaMinLsb]);
+            nan = meta[kMetaAnyNan] != 0u;
         }
     }
     uint64_t it_next = (!kSorted && tid < G) ? items[tid] : 0ull;
@@ -1260,7 +1306,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         if (i < G) {
             pre[i] = pi;
             if (i <= kStage) sh.st.pre[i] = pi;
-            const uint32_t nk = pi >= k ? 0u : min(n, k - pi);
+            const uint32_t nk = top_k_count(pi, n, k);
             const float pe = expf_glibc((u2f(static_cast<uint32_t>(it >> 32)) - vmax) * inv_temp);
             aux[i] = pe;
             if (i < kStage) sh.st.add[i] = pe;

@@ -154,7 +154,7 @@ int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, 
         alloc(reinterpret_cast<void**>(&s->fo_pre), items * sizeof(uint32_t));
         alloc(reinterpret_cast<void**>(&s->fo_extras), rows * static_cast<size_t>(s->fo_extras_cap) * sizeof(uint64_t));
         alloc(reinterpret_cast<void**>(&s->fo_bitmap), words * sizeof(uint32_t));
-        alloc(reinterpret_cast<void**>(&s->fo_meta), rows * 4 * sizeof(uint32_t));
+        alloc(reinterpret_cast<void**>(&s->fo_meta), rows * ge::kMetaWords * sizeof(uint32_t));
         if (e == hipSuccess) e = hipMemset(s->fo_bitmap, 0, words * sizeof(uint32_t));
     }
     if (e == hipSuccess) e = hipDeviceSynchronize();

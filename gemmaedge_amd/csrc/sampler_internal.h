@@ -64,7 +64,7 @@ struct DevArgs {
     uint32_t* fo_pre;             // [max_rows * fo_items_stride]  elements before the item
     uint64_t* fo_extras;          // [max_rows * fo_extras_cap]    penalised tokens, composite keys
     uint32_t* fo_bitmap;          // [max_rows * fo_bitmap_words]  history bitmap, zero between calls
-    uint32_t* fo_meta;            // [max_rows * 4]                items, extras, NaN count, status
+    uint32_t* fo_meta;            // [max_rows * kMetaWords]       items, extras, NaN count, status, exps' certificate
     int64_t fo_items_stride;
     int32_t fo_extras_cap;        // <= kFoExtrasCap
     int64_t fo_bitmap_words;
@@ -80,6 +80,7 @@ struct DevArgs {
 constexpr int kFoBins = 65536;                 // bf16 order keys
 constexpr int kFoNonNanBins = 65536 - 254;     // bf16 patterns that are not NaN
 constexpr int kFoExtrasCap = 8192;             // penalised tokens per row it handles
+constexpr int kMetaWords = 8;                  // per-row words of fo_meta
 
 inline int64_t fo_items_stride(int max_history) {
     const int64_t extras = max_history < kFoExtrasCap ? (max_history > 0 ? max_history : 0) : kFoExtrasCap;
