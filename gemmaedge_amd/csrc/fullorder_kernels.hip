@@ -999,6 +999,444 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
     }
 }
 
+// ---- f32 rows over many workgroups: the same items, tile by tile -----------
+//
+// The sort above gives each row one workgroup; with few rows most of the GPU
+// idles while its passes run. Here a row's keys are cut into tiles of
+// kSTile keys, one 256-thread workgroup per (tile, row), and each step of the
+// sort is a kernel of its own: the kernel boundaries order every exchange
+// between workgroups, so no workgroup waits for another. The results are
+// those of fo_sort_kernel<float>: the sorted keys' items (value, count) in
+// fo_items, their first elements in fo_pre (and pre[G] = V), their exps in
+// fo_aux and the row's meta words; fo_decide_kernel<float, true> follows.
+// Per row the tile area (fo_tiles) holds the (digit, tile) counts, then their
+// output positions, the tiles' item counts and their certificate partials.
+
+constexpr int kSThreads = 256;
+constexpr int kSWaves = kSThreads / 64;
+constexpr int kSSteps = 16;                     // 64-key steps per wave per tile
+constexpr int kSTile = kSThreads * kSSteps;     // 4096 keys
+constexpr int64_t kSplitMaxRows = 160;          // larger f32 slices: fo_sort_kernel
+
+static_assert(kSTile == 4096, "fo_split_tiles() and fo_tile_words() assume 4096-key tiles");
+
+// The row's tile area: counts [kDigits][T], item counts [T], partials [T][4].
+struct SplitRow {
+    uint32_t* cnt;
+    uint32_t* bc;
+    uint32_t* part;
+};
+__device__ __forceinline__ SplitRow split_row(const DevArgs& a, int row, int T) {
+    uint32_t* w = a.fo_tiles + static_cast<int64_t>(row) * fo_tile_words(T);
+    return SplitRow{w, w + kDigits * T, w + (kDigits + 1) * T};
+}
+
+// Rows this path serves (the sort kernel's condition).
+__device__ __forceinline__ bool split_row_active(const DevArgs& a, int row, uint32_t& k, ge_sample_params& p) {
+    p = params_of(a, row);
+    return full_order_row(p, a.vocab, k) && !row_done(a, row);
+}
+
+// Items before tile t: the sum of the tiles' item counts (one wave).
+__device__ __forceinline__ uint32_t items_before(const uint32_t* bc, int t) {
+    uint32_t s = 0;
+    for (int i = __lane_id(); i < t; i += 64) s += bc[i];
+    return wave::readlane(wave::incl_add(s), 63);
+}
+
+// 1. The penalty bitmap of the row's unique in-range history ids (cleared by
+//    the decide kernel).
+__global__ __launch_bounds__(kSThreads) void fs_bitmap_kernel(DevArgs a) {
+    const int row = blockIdx.x;
+    uint32_t k;
+    ge_sample_params p;
+    if (!split_row_active(a, row, k, p)) return;
+    const int32_t* hist;
+    int H;
+    history_of(a, row, hist, H);
+    if (!(H > 0 && !(p.repetition_penalty == 1.0f))) return;
+    uint32_t* bitmap = a.fo_bitmap + static_cast<int64_t>(row) * a.fo_bitmap_words;
+    for (int i = threadIdx.x; i < H; i += kSThreads) {
+        const int32_t id = hist[i];
+        if (id >= 0 && id < a.vocab) atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+    }
+}
+
+// 2. Final keys (generation.cpp:431-437 softcap, then the penalty) of tile t
+//    into buf0, and the tile's count of each lowest digit.
+__global__ __launch_bounds__(kSThreads) void fs_keys_kernel(DevArgs a) {
+    __shared__ uint32_t h[kDigits];
+    const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    uint32_t k;
+    ge_sample_params p;
+    if (!split_row_active(a, row, k, p)) return;
+    const int V = a.vocab, T = gridDim.x;
+    const int32_t* hist;
+    int H;
+    history_of(a, row, hist, H);
+    const bool pen = H > 0 && !(p.repetition_penalty == 1.0f);
+    const float* rowp = static_cast<const float*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
+    const uint32_t* bitmap = a.fo_bitmap + static_cast<int64_t>(row) * a.fo_bitmap_words;
+    uint32_t* buf0 = reinterpret_cast<uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
+    h[tid] = 0u;
+    __syncthreads();
+    float x[kSSteps];
+    uint32_t bw[kSSteps];
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + u * kSThreads + tid;
+        x[u] = i < V ? rowp[i] : 0.0f;
+        bw[u] = (pen && i < V) ? bitmap[i >> 5] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + u * kSThreads + tid;
+        if (i < V) {
+            float f = softcap(x[u], p.softcap);
+            if ((bw[u] >> (i & 31)) & 1u) f = penalize(f, p.repetition_penalty);
+            const uint32_t s = ~order_key(f);
+            buf0[i] = s;
+            atomicAdd(&h[s & 255u], 1u);
+        }
+    }
+    __syncthreads();
+    split_row(a, row, T).cnt[tid * T + t] = h[tid];
+}
+
+// 3a. The tile's count of each digit of pass `shift` (passes after the first).
+__global__ __launch_bounds__(kSThreads) void fs_count_kernel(DevArgs a, int shift, int src_is_buf1) {
+    __shared__ uint32_t h[kDigits];
+    const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    uint32_t k;
+    ge_sample_params p;
+    if (!split_row_active(a, row, k, p)) return;
+    const int V = a.vocab, T = gridDim.x;
+    const uint32_t* src = src_is_buf1 ? a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride
+                                      : reinterpret_cast<const uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
+    h[tid] = 0u;
+    __syncthreads();
+    uint32_t kv[kSSteps];
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + u * kSThreads + tid;
+        kv[u] = i < V ? src[i] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + u * kSThreads + tid;
+        if (i < V) atomicAdd(&h[(kv[u] >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    split_row(a, row, T).cnt[tid * T + t] = h[tid];
+}
+
+// 3b. Output position of each (digit, tile) group: digits in order, tiles in
+//     order inside a digit (a stable pass). In place over the counts.
+__global__ __launch_bounds__(kSThreads) void fs_scan_kernel(DevArgs a, int T) {
+    __shared__ uint32_t scan[kSWaves];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    uint32_t k;
+    ge_sample_params p;
+    if (!split_row_active(a, row, k, p)) return;
+    uint32_t* c = split_row(a, row, T).cnt + tid * T;
+    uint32_t run = 0;
+    for (int t = 0; t < T; ++t) {
+        const uint32_t x = c[t];
+        c[t] = run;
+        run += x;
+    }
+    const uint32_t base = digit_excl_scan(run, scan, tid);
+    for (int t = 0; t < T; ++t) c[t] += base;
+}
+
+// 3c. The stable scatter of tile t by the digit at `shift`: ranks among the
+//     tile's keys of the same digit in position order (ballots per 64-key
+//     step, per-wave LDS counters across steps), the keys grouped by digit in
+//     LDS, each group stored at its output position (consecutive addresses).
+__global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int shift, int src_is_buf1) {
+    __shared__ uint32_t staged[kSTile];
+    __shared__ uint32_t wc[kSWaves][kDigits];
+    __shared__ uint32_t toff[kDigits];
+    __shared__ uint32_t gb[kDigits];
+    __shared__ uint32_t scan[kSWaves];
+    const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int lane = __lane_id(), wave = tid >> 6;
+    uint32_t k;
+    ge_sample_params p;
+    if (!split_row_active(a, row, k, p)) return;
+    const int V = a.vocab, T = gridDim.x;
+    uint32_t* b0 = reinterpret_cast<uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
+    uint32_t* b1 = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
+    const uint32_t* src = src_is_buf1 ? b1 : b0;
+    uint32_t* dst = src_is_buf1 ? b0 : b1;
+    uint32_t key[kSSteps];
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+        key[u] = i < V ? src[i] : 0u;
+    }
+    for (int d = lane; d < kDigits; d += 64) wc[wave][d] = 0u;  // only this wave uses its row
+    gb[tid] = split_row(a, row, T).cnt[tid * T + t];
+    const uint64_t below = (1ull << lane) - 1ull;
+    uint32_t lr[kSSteps];
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+        const bool act = i < V;
+        const uint64_t am = __ballot(act);
+        const uint32_t d = (key[u] >> shift) & 255u;
+        const uint64_t mm = match_digit(d, am);
+        lr[u] = 0u;
+        if (act) {
+            // lanes of one digit read the same counter, then all write the
+            // same advanced value (in program order, so the next step reads it)
+            const uint32_t c = wc[wave][d];
+            lr[u] = c + static_cast<uint32_t>(__popcll(mm & below));
+            wc[wave][d] = c + static_cast<uint32_t>(__popcll(mm));
+        }
+    }
+    __syncthreads();
+    uint32_t tot = 0;
+    for (int w = 0; w < kSWaves; ++w) {  // thread d: each wave's offset among the tile's keys of digit d
+        const uint32_t c = wc[w][tid];
+        wc[w][tid] = tot;
+        tot += c;
+    }
+    toff[tid] = digit_excl_scan(tot, scan, tid);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+        if (i < V) {
+            const uint32_t d = (key[u] >> shift) & 255u;
+            staged[toff[d] + wc[wave][d] + lr[u]] = key[u];
+        }
+    }
+    __syncthreads();
+    const int nt = min(kSTile, V - t * kSTile);
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int q = u * kSThreads + tid;
+        if (q < nt) {
+            const uint32_t kv = staged[q];
+            const uint32_t d = (kv >> shift) & 255u;
+            dst[gb[d] + static_cast<uint32_t>(q) - toff[d]] = kv;
+        }
+    }
+}
+
+// Item boundaries of the sorted keys: position i starts an item when i == 0
+// or its key differs from position i - 1's.
+__device__ __forceinline__ bool is_boundary(const uint32_t* s, int i, int V, uint32_t kv) {
+    return i < V && (i == 0 || kv != s[i - 1]);
+}
+
+// 4a. Items starting in tile t.
+__global__ __launch_bounds__(kSThreads) void fs_bounds_kernel(DevArgs a) {
+    __shared__ uint32_t red[kSWaves];
+    const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    uint32_t k;
+    ge_sample_params p;
+    if (!split_row_active(a, row, k, p)) return;
+    const int V = a.vocab, T = gridDim.x;
+    const uint32_t* s = reinterpret_cast<const uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
+    uint32_t n = 0;
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + u * kSThreads + tid;
+        const uint32_t kv = i < V ? s[i] : 0u;
+        n += is_boundary(s, i, V, kv) ? 1u : 0u;
+    }
+    n = wave::readlane(wave::incl_add(n), 63);
+    if (__lane_id() == 0) red[tid >> 6] = n;
+    __syncthreads();
+    if (tid == 0) split_row(a, row, T).bc[t] = red[0] + red[1] + red[2] + red[3];
+}
+
+// 4b. Each item's first element into pre (buf1), in position order; the last
+//     tile also writes pre[G] = V.
+__global__ __launch_bounds__(kSThreads) void fs_istart_kernel(DevArgs a) {
+    __shared__ uint32_t scan[kSWaves];
+    __shared__ uint32_t base_s;
+    const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int lane = __lane_id(), wave = tid >> 6;
+    uint32_t k;
+    ge_sample_params p;
+    if (!split_row_active(a, row, k, p)) return;
+    const int V = a.vocab, T = gridDim.x;
+    const SplitRow sr = split_row(a, row, T);
+    const uint32_t* s = reinterpret_cast<const uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
+    uint32_t* istart = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
+    if (wave == 0) {
+        const uint32_t b = items_before(sr.bc, t);
+        if (lane == 0) base_s = b;
+    }
+    // wave w owns positions [w * 1024, (w + 1) * 1024) of the tile
+    uint32_t kv[kSSteps];
+    bool bnd[kSSteps];
+    uint32_t nb = 0;
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+        kv[u] = i < V ? s[i] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+        bnd[u] = is_boundary(s, i, V, kv[u]);
+        nb += static_cast<uint32_t>(__popcll(__ballot(bnd[u])));
+    }
+    if (lane == 0) scan[wave] = nb;
+    __syncthreads();
+    uint32_t j = base_s;
+    for (int w = 0; w < wave; ++w) j += scan[w];
+    const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+        const uint64_t m = __ballot(bnd[u]);
+        if (bnd[u]) istart[j + static_cast<uint32_t>(__popcll(m & below))] = static_cast<uint32_t>(i);
+        j += static_cast<uint32_t>(__popcll(m));
+    }
+    if (t == T - 1 && tid == 0) istart[base_s + scan[0] + scan[1] + scan[2] + scan[3]] = static_cast<uint32_t>(V);
+}
+
+// 4c. The items (value, count) that start in tile t.
+__global__ __launch_bounds__(kSThreads) void fs_items_kernel(DevArgs a) {
+    __shared__ uint32_t base_s;
+    const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    uint32_t k;
+    ge_sample_params p;
+    if (!split_row_active(a, row, k, p)) return;
+    const int T = gridDim.x;
+    const SplitRow sr = split_row(a, row, T);
+    const uint32_t* s = reinterpret_cast<const uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
+    const uint32_t* istart = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
+    uint64_t* items = a.fo_items + static_cast<int64_t>(row) * a.fo_items_stride;
+    if ((tid >> 6) == 0) {
+        const uint32_t b = items_before(sr.bc, t);
+        if (__lane_id() == 0) base_s = b;
+    }
+    __syncthreads();
+    const uint32_t j0 = base_s, nj = sr.bc[t];
+    for (uint32_t q = tid; q < nj; q += kSThreads) {
+        const uint32_t j = j0 + q;
+        const uint32_t st = istart[j], en = istart[j + 1];
+        const uint32_t key = ~s[st];
+        const uint32_t val = key == kKeyNaN ? 0x7fc00000u : f2u(key_value(key));
+        items[j] = (static_cast<uint64_t>(val) << 32) | (en - st);
+    }
+}
+
+// 4d. Each item's exp into aux (generation.cpp:94-97: p = exp((l - max) *
+//     (1/T)), max the first item's value), and the tile's part of the
+//     certificate of the top k's double sum: the sum, the lowest set bit,
+//     any NaN. aux held the sorted keys, which 4c was the last to read.
+__global__ __launch_bounds__(kSThreads) void fs_exps_kernel(DevArgs a) {
+    __shared__ uint32_t base_s;
+    __shared__ double dred[kSWaves];
+    __shared__ int ired[kSWaves];
+    __shared__ uint32_t ured[kSWaves];
+    const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int lane = __lane_id(), wave = tid >> 6;
+    uint32_t k;
+    ge_sample_params p;
+    if (!split_row_active(a, row, k, p)) return;
+    const int T = gridDim.x;
+    const SplitRow sr = split_row(a, row, T);
+    const uint32_t* istart = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
+    const uint64_t* items = a.fo_items + static_cast<int64_t>(row) * a.fo_items_stride;
+    float* aux = a.fo_aux + static_cast<int64_t>(row) * a.fo_items_stride;
+    if (wave == 0) {
+        const uint32_t b = items_before(sr.bc, t);
+        if (lane == 0) base_s = b;
+    }
+    __syncthreads();
+    const float vmax = u2f(static_cast<uint32_t>(items[0] >> 32));
+    const float inv_temp = 1.0f / p.temperature;
+    const uint32_t j0 = base_s, nj = sr.bc[t];
+    double S = 0.0;
+    int minlsb = INT_MAX;
+    bool nan = false;
+    for (uint32_t q = tid; q < nj; q += kSThreads) {
+        const uint32_t j = j0 + q;
+        const uint64_t it = items[j];
+        const float pe = expf_glibc((u2f(static_cast<uint32_t>(it >> 32)) - vmax) * inv_temp);
+        aux[j] = pe;
+        const uint32_t nk = top_k_count(istart[j], static_cast<uint32_t>(it), k);
+        if (nk) {
+            if (pe != pe) nan = true;
+            else if (pe > 0.0f) {
+                minlsb = min(minlsb, lsb_exp(pe));
+                S += static_cast<double>(nk) * static_cast<double>(pe);
+            }
+        }
+    }
+    S = wave::sum_f64(S);  // a certificate: exact whenever it certifies
+    minlsb = wave::min_i32(minlsb);
+    const uint32_t nanw = __ballot(nan) != 0ull ? 1u : 0u;
+    if (lane == 0) {
+        dred[wave] = S;
+        ired[wave] = minlsb;
+        ured[wave] = nanw;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double Sp = 0.0;
+        int ml = INT_MAX;
+        uint32_t nn = 0;
+        for (int w = 0; w < kSWaves; ++w) {
+            Sp += dred[w];
+            ml = min(ml, ired[w]);
+            nn |= ured[w];
+        }
+        const uint64_t sb = __builtin_bit_cast(uint64_t, Sp);
+        uint32_t* pt = sr.part + 4 * t;
+        pt[0] = static_cast<uint32_t>(sb);
+        pt[1] = static_cast<uint32_t>(sb >> 32);
+        pt[2] = static_cast<uint32_t>(ml);
+        pt[3] = nn;
+    }
+}
+
+// 4e. The row's meta words, as fo_sort_kernel writes them.
+__global__ __launch_bounds__(64) void fs_meta_kernel(DevArgs a, int T) {
+    const int row = blockIdx.x, lane = __lane_id();
+    uint32_t k;
+    ge_sample_params p;
+    if (!split_row_active(a, row, k, p)) return;
+    const SplitRow sr = split_row(a, row, T);
+    double S = 0.0;
+    int ml = INT_MAX;
+    uint32_t nn = 0, G = 0;
+    for (int t = lane; t < T; t += 64) {
+        const uint32_t* pt = sr.part + 4 * t;
+        S += __builtin_bit_cast(double, (static_cast<uint64_t>(pt[1]) << 32) | pt[0]);
+        ml = min(ml, static_cast<int>(pt[2]));
+        nn |= pt[3];
+        G += sr.bc[t];
+    }
+    S = wave::sum_f64(S);
+    ml = wave::min_i32(ml);
+    nn = __ballot(nn != 0u) != 0ull ? 1u : 0u;
+    G = wave::readlane(wave::incl_add(G), 63);
+    if (lane == 0) {
+        const uint64_t* items = a.fo_items + static_cast<int64_t>(row) * a.fo_items_stride;
+        const uint32_t* istart = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
+        const bool last_nan = static_cast<uint32_t>(items[G - 1] >> 32) == 0x7fc00000u;
+        uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * kMetaWords;
+        const uint64_t sb = __builtin_bit_cast(uint64_t, S);
+        meta[kMetaSumLo] = static_cast<uint32_t>(sb);
+        meta[kMetaSumHi] = static_cast<uint32_t>(sb >> 32);
+        meta[kMetaMinLsb] = static_cast<uint32_t>(ml);
+        meta[kMetaAnyNan] = nn;
+        meta[kMetaItems] = G;
+        meta[kMetaExtras] = 0;
+        meta[kMetaNan] = last_nan ? static_cast<uint32_t>(a.vocab) - istart[G - 1] : 0u;
+        meta[kMetaStatus] = kStatusOk;
+    }
+}
+
 // ---- kernel 2: probabilities, exact chains, token ----------------------------
 
 
@@ -1835,15 +2273,49 @@ namespace {
 
 // Rows [0, a.rows) through the sort-based kernels, as many per launch pair as
 // the workspace holds at the f32 stride (at least one, by construction).
+// The items of f32 rows [0, s.rows) through the many-workgroup sort: tiles
+// of 4096 keys, one workgroup each, one kernel per step.
+hipError_t split_sort_f32(const DevArgs& s, hipStream_t stream) {
+    const int T = fo_split_tiles(s.vocab);
+    const dim3 tiles(static_cast<unsigned>(T), static_cast<unsigned>(s.rows));
+    const dim3 rows(static_cast<unsigned>(s.rows));
+    hipLaunchKernelGGL(fs_bitmap_kernel, rows, dim3(kSThreads), 0, stream, s);
+    hipLaunchKernelGGL(fs_keys_kernel, tiles, dim3(kSThreads), 0, stream, s);
+    for (int pass = 0; pass < 4; ++pass) {
+        const int src_is_buf1 = pass & 1;  // buf0 -> buf1 -> buf0 -> buf1 -> buf0
+        if (pass > 0) hipLaunchKernelGGL(fs_count_kernel, tiles, dim3(kSThreads), 0, stream, s, 8 * pass, src_is_buf1);
+        hipLaunchKernelGGL(fs_scan_kernel, rows, dim3(kSThreads), 0, stream, s, T);
+        hipLaunchKernelGGL(fs_scatter_kernel, tiles, dim3(kSThreads), 0, stream, s, 8 * pass, src_is_buf1);
+    }
+    hipLaunchKernelGGL(fs_bounds_kernel, tiles, dim3(kSThreads), 0, stream, s);
+    hipLaunchKernelGGL(fs_istart_kernel, tiles, dim3(kSThreads), 0, stream, s);
+    hipLaunchKernelGGL(fs_items_kernel, tiles, dim3(kSThreads), 0, stream, s);
+    hipLaunchKernelGGL(fs_exps_kernel, tiles, dim3(kSThreads), 0, stream, s);
+    hipLaunchKernelGGL(fs_meta_kernel, rows, dim3(64), 0, stream, s, T);
+    return hipGetLastError();
+}
+
 template <typename T>
 hipError_t sorted_pass(const DevArgs& a, hipStream_t stream) {
     const int64_t stride = fo_items_stride_f32(a.vocab);
     if (a.fo_capacity < stride) return hipErrorInvalidValue;
-    const int per = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.fo_capacity / stride, a.rows)));
+    const int64_t per64 = std::min<int64_t>(a.fo_capacity / stride, a.rows);
+    // f32 slices of up to kSplitMaxRows rows take the many-workgroup sort
+    // (when the handle's tile area holds them): its time grows with the rows,
+    // while fo_sort_kernel runs up to 256 rows side by side in about the time
+    // of one (about equal near 200 rows of V = 262,144).
+    const bool split = std::is_same<T, float>::value && !a.fo_fallback && a.fo_tiles != nullptr &&
+                       per64 <= kSplitMaxRows && per64 * fo_tile_words(fo_split_tiles(a.vocab)) <= a.fo_tiles_words;
+    const int per = static_cast<int>(std::max<int64_t>(1, per64));
     for (int r0 = 0; r0 < a.rows; r0 += per) {
         DevArgs s = slice_rows(a, r0, std::min(per, a.rows - r0));
         s.fo_items_stride = stride;
-        hipLaunchKernelGGL(fo_sort_kernel<T>, dim3(s.rows), dim3(kThreads), 0, stream, s);
+        if (split) {
+            const hipError_t es = split_sort_f32(s, stream);
+            if (es != hipSuccess) return es;
+        } else {
+            hipLaunchKernelGGL(fo_sort_kernel<T>, dim3(s.rows), dim3(kThreads), 0, stream, s);
+        }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL((fo_decide_kernel<T, true>), dim3(s.rows), dim3(kDThreads), 0, stream, s);

@@ -39,6 +39,8 @@ struct ge_sampler {
     uint64_t* fo_extras;
     uint32_t* fo_bitmap;
     uint32_t* fo_meta;
+    uint32_t* fo_tiles;
+    int64_t fo_tiles_words;
     int64_t fo_items_stride;
     int64_t fo_capacity;
     int32_t fo_extras_cap;
@@ -155,6 +157,9 @@ int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, 
         alloc(reinterpret_cast<void**>(&s->fo_extras), rows * static_cast<size_t>(s->fo_extras_cap) * sizeof(uint64_t));
         alloc(reinterpret_cast<void**>(&s->fo_bitmap), words * sizeof(uint32_t));
         alloc(reinterpret_cast<void**>(&s->fo_meta), rows * ge::kMetaWords * sizeof(uint32_t));
+        // the many-workgroup f32 sort: per-tile counts for the same 256 rows
+        s->fo_tiles_words = static_cast<int64_t>(f32_rows) * ge::fo_tile_words(ge::fo_split_tiles(max_vocab));
+        alloc(reinterpret_cast<void**>(&s->fo_tiles), static_cast<size_t>(s->fo_tiles_words) * sizeof(uint32_t));
         if (e == hipSuccess) e = hipMemset(s->fo_bitmap, 0, words * sizeof(uint32_t));
     }
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -178,6 +183,7 @@ void ge_sampler_destroy(ge_sampler* s) {
     (void)hipFree(s->fo_extras);
     (void)hipFree(s->fo_bitmap);
     (void)hipFree(s->fo_meta);
+    (void)hipFree(s->fo_tiles);
     delete s;
 }
 
@@ -201,6 +207,8 @@ struct Workspace {
     uint64_t* fo_extras;
     uint32_t* fo_bitmap;
     uint32_t* fo_meta;
+    uint32_t* fo_tiles;
+    int64_t fo_tiles_words;
     int64_t fo_items_stride;
     int64_t fo_capacity;
     int32_t fo_extras_cap;
@@ -259,6 +267,8 @@ int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
     a.fo_extras = ws.fo_extras;
     a.fo_bitmap = ws.fo_bitmap;
     a.fo_meta = ws.fo_meta;
+    a.fo_tiles = ws.fo_tiles;
+    a.fo_tiles_words = ws.fo_tiles_words;
     a.fo_items_stride = ws.fo_items_stride;
     a.fo_extras_cap = ws.fo_extras_cap;
     a.fo_bitmap_words = ws.fo_bitmap_words;
@@ -351,6 +361,8 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     ws.fo_extras = s->fo_extras;
     ws.fo_bitmap = s->fo_bitmap;
     ws.fo_meta = s->fo_meta;
+    ws.fo_tiles = s->fo_tiles;
+    ws.fo_tiles_words = s->fo_tiles_words;
     ws.fo_items_stride = s->fo_items_stride;
     ws.fo_capacity = s->fo_capacity;
     ws.fo_extras_cap = s->fo_extras_cap;

@@ -69,6 +69,8 @@ struct DevArgs {
     int32_t fo_extras_cap;        // <= kFoExtrasCap
     int64_t fo_bitmap_words;
     int64_t fo_capacity;          // items (and aux, pre entries) in the workspace
+    uint32_t* fo_tiles;           // [fo_tiles_words] f32 rows' per-tile counts and partials (many-workgroup sort)
+    int64_t fo_tiles_words;
     // Full-order fallback pass (bf16 rows with more unique penalised ids than
     // fo_extras_cap): the sort-based kernels serve only the rows the first
     // pass flagged. fo_row0: the first call row of a slice of rows.
@@ -90,6 +92,10 @@ inline int64_t fo_items_stride(int max_history) {
 // f32 rows: one item per distinct final value (up to V) and the end
 // boundary; the sort also uses the aux and pre arrays as two V-entry buffers.
 inline int64_t fo_items_stride_f32(int vocab) { return (static_cast<int64_t>(vocab) + 2 + 63) / 64 * 64; }
+// The many-workgroup f32 sort: tiles of 4096 keys per row; per row and tile
+// 256 digit counts, an item count and four partial words.
+constexpr int fo_split_tiles(int vocab) { return (vocab + 4095) / 4096; }
+constexpr int64_t fo_tile_words(int tiles) { return static_cast<int64_t>(tiles) * (256 + 1 + 4); }
 
 // The row's parameters: the shared ones, or its entry of row_params.
 __device__ __forceinline__ ge_sample_params row_params(const DevArgs& a, int row) {

@@ -238,3 +238,26 @@ def test_rows_in_several_launches():
             _check(s, w)
         finally:
             s.close()
+
+
+def test_large_batches_keep_the_per_row_sort():
+    # Slices of more than 160 f32 rows take the one-workgroup-per-row sort;
+    # smaller ones (every other test here) the sort over 4096-key tiles.
+    from gemmaedge_amd import Sampler
+
+    rng = np.random.default_rng(53)
+    rows, V = 200, 6007
+    s = Sampler(max_rows=rows, max_vocab=V, max_history=64)
+    try:
+        x = (rng.standard_normal((rows, V)) * 2).astype(np.float32)
+        x[::7, ::13] = 0.0  # ties
+        x[3, 5] = np.nan
+        hist = rng.integers(0, V, size=rows * 64).astype(np.int32)
+        offs = (np.arange(rows + 1) * 64).astype(np.int32)
+        for k in (0, 3000):
+            w = small_workload(f"per-row-sort-k{k}", x,
+                               dict(temperature=0.8, top_k=k, top_p=0.9, softcap=30.0, repetition_penalty=1.2),
+                               history=hist, offsets=offs, uniforms=W.mt_uniforms(V + k, rows))
+            _check(s, w)
+    finally:
+        s.close()
