@@ -145,7 +145,9 @@ int ge_sampler_available(void);
  * With max_vocab > 1024 the full-order workspace (top-k off or above 1024)
  * takes 16 bytes per item for the larger of max_rows x (about 65,300 + min(
  * max_history, 8192)) bf16 items and min(max_rows, 256) x max_vocab f32
- * items: about 1 GiB at 256 or more rows of V = 262,144. */
+ * items, plus 1,044 bytes per 4096 vocab entries for each of min(max_rows,
+ * 256) rows (the f32 sort's tile counts): about 1 GiB at 256 or more rows of
+ * V = 262,144. */
 int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history,
                       ge_sampler** out);
 
