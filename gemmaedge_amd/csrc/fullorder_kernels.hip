@@ -1020,7 +1020,7 @@ constexpr int64_t kSplitMaxRows = 160;          // larger f32 slices: fo_sort_ke
 
 static_assert(kSTile == 4096, "fo_split_tiles() and fo_tile_words() assume 4096-key tiles");
 
-// The row's tile area: counts [kDigits][T], item counts [T], partials [T][4].
+// The row's tile area: counts [T][kDigits], item counts [T], partials [T][4].
 struct SplitRow {
     uint32_t* cnt;
     uint32_t* bc;
@@ -1100,7 +1100,7 @@ __global__ __launch_bounds__(kSThreads) void fs_keys_kernel(DevArgs a) {
         }
     }
     __syncthreads();
-    split_row(a, row, T).cnt[tid * T + t] = h[tid];
+    split_row(a, row, T).cnt[t * kDigits + tid] = h[tid];
 }
 
 // 3a. The tile's count of each digit of pass `shift` (passes after the first).
@@ -1127,26 +1127,40 @@ __global__ __launch_bounds__(kSThreads) void fs_count_kernel(DevArgs a, int shif
         if (i < V) atomicAdd(&h[(kv[u] >> shift) & 255u], 1u);
     }
     __syncthreads();
-    split_row(a, row, T).cnt[tid * T + t] = h[tid];
+    split_row(a, row, T).cnt[t * kDigits + tid] = h[tid];
 }
 
 // 3b. Output position of each (digit, tile) group: digits in order, tiles in
-//     order inside a digit (a stable pass). In place over the counts.
+//     order inside a digit (a stable pass). In place over the counts; thread
+//     d walks its digit's counts down the tiles, 64 loads in flight, a wave's
+//     loads of one tile on consecutive words.
 __global__ __launch_bounds__(kSThreads) void fs_scan_kernel(DevArgs a, int T) {
     __shared__ uint32_t scan[kSWaves];
+    constexpr int kB = 64;
     const int row = blockIdx.x, tid = threadIdx.x;
     uint32_t k;
     ge_sample_params p;
     if (!split_row_active(a, row, k, p)) return;
-    uint32_t* c = split_row(a, row, T).cnt + tid * T;
-    uint32_t run = 0;
-    for (int t = 0; t < T; ++t) {
-        const uint32_t x = c[t];
-        c[t] = run;
-        run += x;
+    uint32_t* c = split_row(a, row, T).cnt + tid;
+    uint32_t total = 0;
+    for (int t0 = 0; t0 < T; t0 += kB) {
+        uint32_t v[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) v[u] = c[min(t0 + u, T - 1) * kDigits];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) total += t0 + u < T ? v[u] : 0u;
     }
-    const uint32_t base = digit_excl_scan(run, scan, tid);
-    for (int t = 0; t < T; ++t) c[t] += base;
+    uint32_t run = digit_excl_scan(total, scan, tid);
+    for (int t0 = 0; t0 < T; t0 += kB) {
+        uint32_t v[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) v[u] = c[min(t0 + u, T - 1) * kDigits];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+            if (t0 + u < T) c[(t0 + u) * kDigits] = run;
+            run += t0 + u < T ? v[u] : 0u;
+        }
+    }
 }
 
 // 3c. The stable scatter of tile t by the digit at `shift`: ranks among the
@@ -1176,7 +1190,7 @@ __global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int sh
         key[u] = i < V ? src[i] : 0u;
     }
     for (int d = lane; d < kDigits; d += 64) wc[wave][d] = 0u;  // only this wave uses its row
-    gb[tid] = split_row(a, row, T).cnt[tid * T + t];
+    gb[tid] = split_row(a, row, T).cnt[t * kDigits + tid];
     const uint64_t below = (1ull << lane) - 1ull;
     uint32_t lr[kSSteps];
 #pragma unroll
@@ -1253,8 +1267,9 @@ __global__ __launch_bounds__(kSThreads) void fs_bounds_kernel(DevArgs a) {
     if (tid == 0) split_row(a, row, T).bc[t] = red[0] + red[1] + red[2] + red[3];
 }
 
-// 4b. Each item's first element into pre (buf1), in position order; the last
-//     tile also writes pre[G] = V.
+// 4b. Each item's first element into pre (buf1), in position order, and its
+//     value into the high word of its items entry (4c adds the count); the
+//     last tile also writes pre[G] = V.
 __global__ __launch_bounds__(kSThreads) void fs_istart_kernel(DevArgs a) {
     __shared__ uint32_t scan[kSWaves];
     __shared__ uint32_t base_s;
@@ -1267,6 +1282,7 @@ __global__ __launch_bounds__(kSThreads) void fs_istart_kernel(DevArgs a) {
     const SplitRow sr = split_row(a, row, T);
     const uint32_t* s = reinterpret_cast<const uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
     uint32_t* istart = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
+    uint64_t* items = a.fo_items + static_cast<int64_t>(row) * a.fo_items_stride;
     if (wave == 0) {
         const uint32_t b = items_before(sr.bc, t);
         if (lane == 0) base_s = b;
@@ -1295,43 +1311,23 @@ __global__ __launch_bounds__(kSThreads) void fs_istart_kernel(DevArgs a) {
     for (int u = 0; u < kSSteps; ++u) {
         const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
         const uint64_t m = __ballot(bnd[u]);
-        if (bnd[u]) istart[j + static_cast<uint32_t>(__popcll(m & below))] = static_cast<uint32_t>(i);
+        if (bnd[u]) {
+            const uint32_t jj = j + static_cast<uint32_t>(__popcll(m & below));
+            const uint32_t key = ~kv[u];
+            istart[jj] = static_cast<uint32_t>(i);
+            items[jj] = static_cast<uint64_t>(key == kKeyNaN ? 0x7fc00000u : f2u(key_value(key))) << 32;
+        }
         j += static_cast<uint32_t>(__popcll(m));
     }
     if (t == T - 1 && tid == 0) istart[base_s + scan[0] + scan[1] + scan[2] + scan[3]] = static_cast<uint32_t>(V);
 }
 
-// 4c. The items (value, count) that start in tile t.
-__global__ __launch_bounds__(kSThreads) void fs_items_kernel(DevArgs a) {
-    __shared__ uint32_t base_s;
-    const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
-    uint32_t k;
-    ge_sample_params p;
-    if (!split_row_active(a, row, k, p)) return;
-    const int T = gridDim.x;
-    const SplitRow sr = split_row(a, row, T);
-    const uint32_t* s = reinterpret_cast<const uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
-    const uint32_t* istart = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
-    uint64_t* items = a.fo_items + static_cast<int64_t>(row) * a.fo_items_stride;
-    if ((tid >> 6) == 0) {
-        const uint32_t b = items_before(sr.bc, t);
-        if (__lane_id() == 0) base_s = b;
-    }
-    __syncthreads();
-    const uint32_t j0 = base_s, nj = sr.bc[t];
-    for (uint32_t q = tid; q < nj; q += kSThreads) {
-        const uint32_t j = j0 + q;
-        const uint32_t st = istart[j], en = istart[j + 1];
-        const uint32_t key = ~s[st];
-        const uint32_t val = key == kKeyNaN ? 0x7fc00000u : f2u(key_value(key));
-        items[j] = (static_cast<uint64_t>(val) << 32) | (en - st);
-    }
-}
-
-// 4d. Each item's exp into aux (generation.cpp:94-97: p = exp((l - max) *
-//     (1/T)), max the first item's value), and the tile's part of the
-//     certificate of the top k's double sum: the sum, the lowest set bit,
-//     any NaN. aux held the sorted keys, which 4c was the last to read.
+// 4c. The items that start in tile t: each one's count (from the next
+//     item's first element) beside its value, its exp into aux
+//     (generation.cpp:94-97: p = exp((l - max) * (1/T)), max the first
+//     item's value), and the tile's part of the certificate of the top k's
+//     double sum: the sum, the lowest set bit, any NaN. aux held the sorted
+//     keys, which 4b was the last to read.
 __global__ __launch_bounds__(kSThreads) void fs_exps_kernel(DevArgs a) {
     __shared__ uint32_t base_s;
     __shared__ double dred[kSWaves];
@@ -1345,7 +1341,7 @@ __global__ __launch_bounds__(kSThreads) void fs_exps_kernel(DevArgs a) {
     const int T = gridDim.x;
     const SplitRow sr = split_row(a, row, T);
     const uint32_t* istart = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
-    const uint64_t* items = a.fo_items + static_cast<int64_t>(row) * a.fo_items_stride;
+    uint64_t* items = a.fo_items + static_cast<int64_t>(row) * a.fo_items_stride;
     float* aux = a.fo_aux + static_cast<int64_t>(row) * a.fo_items_stride;
     if (wave == 0) {
         const uint32_t b = items_before(sr.bc, t);
@@ -1358,17 +1354,33 @@ __global__ __launch_bounds__(kSThreads) void fs_exps_kernel(DevArgs a) {
     double S = 0.0;
     int minlsb = INT_MAX;
     bool nan = false;
-    for (uint32_t q = tid; q < nj; q += kSThreads) {
-        const uint32_t j = j0 + q;
-        const uint64_t it = items[j];
-        const float pe = expf_glibc((u2f(static_cast<uint32_t>(it >> 32)) - vmax) * inv_temp);
-        aux[j] = pe;
-        const uint32_t nk = top_k_count(istart[j], static_cast<uint32_t>(it), k);
-        if (nk) {
-            if (pe != pe) nan = true;
-            else if (pe > 0.0f) {
-                minlsb = min(minlsb, lsb_exp(pe));
-                S += static_cast<double>(nk) * static_cast<double>(pe);
+    uint64_t itv[kSSteps];
+    uint32_t stv[kSSteps], env[kSSteps];
+    if (nj > 0u) {
+#pragma unroll
+        for (int u = 0; u < kSSteps; ++u) {  // nj <= kSTile; clamped indices, no conditional load
+            const uint32_t q = min(static_cast<uint32_t>(u * kSThreads + tid), nj - 1u);
+            itv[u] = items[j0 + q];
+            stv[u] = istart[j0 + q];
+            env[u] = istart[j0 + q + 1];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kSSteps; ++u) {
+        const uint32_t q = static_cast<uint32_t>(u * kSThreads + tid);
+        if (q < nj) {
+            const uint32_t n = env[u] - stv[u];
+            const uint32_t vb = static_cast<uint32_t>(itv[u] >> 32);
+            items[j0 + q] = (static_cast<uint64_t>(vb) << 32) | n;
+            const float pe = expf_glibc((u2f(vb) - vmax) * inv_temp);
+            aux[j0 + q] = pe;
+            const uint32_t nk = top_k_count(stv[u], n, k);
+            if (nk) {
+                if (pe != pe) nan = true;
+                else if (pe > 0.0f) {
+                    minlsb = min(minlsb, lsb_exp(pe));
+                    S += static_cast<double>(nk) * static_cast<double>(pe);
+                }
             }
         }
     }
@@ -1399,7 +1411,7 @@ __global__ __launch_bounds__(kSThreads) void fs_exps_kernel(DevArgs a) {
     }
 }
 
-// 4e. The row's meta words, as fo_sort_kernel writes them.
+// 4d. The row's meta words, as fo_sort_kernel writes them.
 __global__ __launch_bounds__(64) void fs_meta_kernel(DevArgs a, int T) {
     const int row = blockIdx.x, lane = __lane_id();
     uint32_t k;
@@ -2289,7 +2301,6 @@ hipError_t split_sort_f32(const DevArgs& s, hipStream_t stream) {
     }
     hipLaunchKernelGGL(fs_bounds_kernel, tiles, dim3(kSThreads), 0, stream, s);
     hipLaunchKernelGGL(fs_istart_kernel, tiles, dim3(kSThreads), 0, stream, s);
-    hipLaunchKernelGGL(fs_items_kernel, tiles, dim3(kSThreads), 0, stream, s);
     hipLaunchKernelGGL(fs_exps_kernel, tiles, dim3(kSThreads), 0, stream, s);
     hipLaunchKernelGGL(fs_meta_kernel, rows, dim3(64), 0, stream, s, T);
     return hipGetLastError();
