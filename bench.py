@@ -59,7 +59,7 @@ def parse_args():
                     help="target wall time of the oracle baseline sample")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for rocprofv3: --steps launches of one config plus a copy-kernel calibration")
-    ap.add_argument("--profile-config", default="C2", choices=["C1", "C1g", "C2", "C3", "C4", "C4f32", "C5"],
+    ap.add_argument("--profile-config", default="C2", choices=["C1", "C1g", "C1f", "C2", "C3", "C4", "C4f32", "C5"],
                     help="config of the profile pass (C5: --steps consecutive decode steps on the device ring)")
     return ap.parse_args()
 
@@ -442,8 +442,10 @@ def main():
         if pc == "C5":
             c5_sweep(torch, sampler, W, args.steps)
         else:
-            pw = {"C1": lambda: W.c1(), "C1g": lambda: W.c1(greedy=True), "C2": lambda: w, "C3": W.c3,
-                  "C4": W.c4, "C4f32": lambda: W.c4(f32=True)}[pc]()
+            pw = {"C1": lambda: W.c1(), "C1g": lambda: W.c1(greedy=True),
+                  "C1f": lambda: dataclasses.replace(W.c1(), name="C1-f32-full-order",
+                                                     params=dict(W.c1().params, top_k=0)),
+                  "C2": lambda: w, "C3": W.c3, "C4": W.c4, "C4f32": lambda: W.c4(f32=True)}[pc]()
             pb = b if pc == "C2" else Bound(sampler, pw, torch)
             for _ in range(args.steps):
                 pb.launch(stream.cuda_stream)
