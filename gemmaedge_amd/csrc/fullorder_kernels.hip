@@ -920,7 +920,7 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
     //    kernel (generation.cpp:94-97: p = exp((l - max) * (1/T)), max the
     //    first item's value) with the certificate of their double sum over the
     //    top k (the sum, the lowest set bit, any NaN). aux holds the sorted
-    //    keys being read: rounds of 4096 items read their keys, wait at a
+    //    keys being read: rounds of 16384 items read their keys, wait at a
     //    barrier, then write; later rounds read only keys at or after their
     //    own items' positions, past every position written before.
     const uint32_t key0 = ~ld_l2(s);
@@ -931,18 +931,18 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
     double S = 0.0;
     int minlsb = INT_MAX;
     bool nan = false;
-    constexpr int kQ = 4;
+    constexpr int kQ = 16;
     for (uint32_t q0 = tid; q0 - tid < G; q0 += kThreads * kQ) {  // uniform trip count
         uint32_t st[kQ], en[kQ];
 #pragma unroll
-        for (int u = 0; u < kQ; ++u) {
-            const uint32_t q = q0 + u * kThreads;
-            st[u] = q < G ? ld_l2(istart + q) : 0u;
-            en[u] = q < G ? ld_l2(istart + q + 1) : 0u;
+        for (int u = 0; u < kQ; ++u) {  // indices clamped to the last item: no conditional load
+            const uint32_t q = min(q0 + u * kThreads, G - 1u);
+            st[u] = ld_l2(istart + q);
+            en[u] = ld_l2(istart + q + 1);
         }
         uint32_t kv[kQ];
 #pragma unroll
-        for (int u = 0; u < kQ; ++u) kv[u] = q0 + u * kThreads < G ? ld_l2(s + st[u]) : 0u;
+        for (int u = 0; u < kQ; ++u) kv[u] = ld_l2(s + st[u]);
         // Every thread's key loads of this round have returned before any
         // thread writes aux: an item's first key can sit at the position of
         // a later item of the same round (a barrier alone does not wait for
