@@ -2060,22 +2060,22 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             if (d.pos > 0) {
                 double sum = 0.0;
                 int mlb = INT_MAX;
-                constexpr int kU = 8;
+                constexpr int kU = 16;
                 for (int base = 0; base <= d.item; base += kDThreads * kU) {
                     uint32_t stv[kU], env[kU];
                     float qv[kU];
 #pragma unroll
-                    for (int u2 = 0; u2 < kU; ++u2) {
-                        const int i = base + u2 * kDThreads + tid;
-                        const bool in = i <= d.item;
-                        stv[u2] = in ? pre[i] : 0u;
-                        env[u2] = in ? pre[i + 1] : 0u;
-                        qv[u2] = in ? aux[i] * inv : 0.0f;
+                    for (int u2 = 0; u2 < kU; ++u2) {  // clamped to d.item: no conditional load
+                        const int i = min(base + u2 * kDThreads + tid, d.item);
+                        stv[u2] = pre[i];
+                        env[u2] = pre[i + 1];
+                        qv[u2] = aux[i] * inv;
                     }
 #pragma unroll
                     for (int u2 = 0; u2 < kU; ++u2) {
+                        const bool in = base + u2 * kDThreads + tid <= d.item;
                         const uint32_t en = min(env[u2], d.pos);
-                        if (en > stv[u2] && qv[u2] > 0.0f) {
+                        if (in && en > stv[u2] && qv[u2] > 0.0f) {
                             sum += static_cast<double>(en - stv[u2]) * static_cast<double>(qv[u2]);
                             mlb = min(mlb, lsb_exp(qv[u2]));
                         }
