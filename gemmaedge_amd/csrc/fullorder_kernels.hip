@@ -756,8 +756,9 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
 #pragma unroll
         for (int u = 0; u < kSortUnroll; ++u) {
             const int i = base + u * kThreads + tid;
-            x[u] = i < V ? load_value(rowp, i) : 0.0f;
-            bw[u] = (pen && i < V) ? ld_l2(bitmap + (i >> 5)) : 0u;
+            const int ic = min(i, V - 1);  // clamped: no conditional load (values past V unused)
+            x[u] = load_value(rowp, ic);
+            bw[u] = pen ? ld_l2(bitmap + (ic >> 5)) : 0u;
         }
 #pragma unroll
         for (int u = 0; u < kSortUnroll; ++u) {
@@ -789,7 +790,7 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
 #pragma unroll
             for (int u = 0; u < kTileSteps; ++u) {
                 const int i = t * kTileKeys + wave * (64 * kTileSteps) + u * 64 + lane;
-                kv[u] = i < V ? ld_l2(src + i) : 0u;
+                kv[u] = ld_l2(src + min(i, V - 1));  // clamped: keys past V unused
             }
         };
         load_tile(0, key);
@@ -880,8 +881,9 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
         for (int u = 0; u < kSortUnroll; ++u) {
             const int i = base + 64 * u + lane;
             const bool act = i < whi;
-            cv[u] = act ? ld_l2(s + i) : 0u;
-            pv[u] = (act && i > 0) ? ld_l2(s + i - 1) : 0u;
+            const int ic = min(i, whi - 1);  // clamped: no conditional load (unused when !act)
+            cv[u] = ld_l2(s + ic);
+            pv[u] = ld_l2(s + max(ic - 1, 0));
         }
     };
     uint32_t nb = 0;
@@ -1085,8 +1087,9 @@ __global__ __launch_bounds__(kSThreads) void fs_keys_kernel(DevArgs a) {
 #pragma unroll
     for (int u = 0; u < kSSteps; ++u) {
         const int i = t * kSTile + u * kSThreads + tid;
-        x[u] = i < V ? rowp[i] : 0.0f;
-        bw[u] = (pen && i < V) ? bitmap[i >> 5] : 0u;
+        const int ic = min(i, V - 1);  // clamped: no conditional load (values past V unused)
+        x[u] = rowp[ic];
+        bw[u] = pen ? bitmap[ic >> 5] : 0u;
     }
 #pragma unroll
     for (int u = 0; u < kSSteps; ++u) {
