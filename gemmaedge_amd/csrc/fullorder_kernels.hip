@@ -1122,7 +1122,7 @@ __global__ __launch_bounds__(kSThreads) void fs_count_kernel(DevArgs a, int shif
 #pragma unroll
     for (int u = 0; u < kSSteps; ++u) {
         const int i = t * kSTile + u * kSThreads + tid;
-        kv[u] = i < V ? src[i] : 0u;
+        kv[u] = src[min(i, V - 1)];  // clamped: keys past V unused
     }
 #pragma unroll
     for (int u = 0; u < kSSteps; ++u) {
@@ -1190,7 +1190,7 @@ __global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int sh
 #pragma unroll
     for (int u = 0; u < kSSteps; ++u) {
         const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
-        key[u] = i < V ? src[i] : 0u;
+        key[u] = src[min(i, V - 1)];  // clamped: keys past V unused
     }
     for (int d = lane; d < kDigits; d += 64) wc[wave][d] = 0u;  // only this wave uses its row
     gb[tid] = split_row(a, row, T).cnt[t * kDigits + tid];
@@ -1261,7 +1261,7 @@ __global__ __launch_bounds__(kSThreads) void fs_bounds_kernel(DevArgs a) {
 #pragma unroll
     for (int u = 0; u < kSSteps; ++u) {
         const int i = t * kSTile + u * kSThreads + tid;
-        const uint32_t kv = i < V ? s[i] : 0u;
+        const uint32_t kv = s[min(i, V - 1)];  // clamped: is_boundary checks i < V
         n += is_boundary(s, i, V, kv) ? 1u : 0u;
     }
     n = wave::readlane(wave::incl_add(n), 63);
@@ -1297,7 +1297,7 @@ __global__ __launch_bounds__(kSThreads) void fs_istart_kernel(DevArgs a) {
 #pragma unroll
     for (int u = 0; u < kSSteps; ++u) {
         const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
-        kv[u] = i < V ? s[i] : 0u;
+        kv[u] = s[min(i, V - 1)];  // clamped: is_boundary checks i < V
     }
 #pragma unroll
     for (int u = 0; u < kSSteps; ++u) {
