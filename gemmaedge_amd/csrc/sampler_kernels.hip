@@ -2197,18 +2197,34 @@ __device__ __forceinline__ bool merge_lean(const DevArgs& a, SelShared& sh, cons
     // 1. One round trip: per wave the chunks' headers (lane c: chunk c), per
     //    thread one entry slot (chunk t % cpr, position t / cpr < j1) with its
     //    chunk's count and its final key, and the expf table.
+    //    The loads are unconditional (lanes and positions past the lists read
+    //    the last chunk's header or entry, and their words are then dropped):
+    //    a load under a lane mask is followed by a wait for every load in
+    //    flight, which would make this three round trips.
     const bool hl = static_cast<uint32_t>(lane) < cpr;
-    const uint32_t hbase = static_cast<uint32_t>(lane) * stride;
-    const uint64_t hg = hl ? load_shared(&slot_row[hbase]) : 0ull;
-    const uint64_t hc = hl ? load_shared(&slot_row[hbase + 1u]) : 0ull;
-    const uint64_t hj = hl ? load_shared(&slot_row[hbase + 1u + j1]) : 0ull;
-    const uint64_t hb = hl ? load_shared(&slot_row[hbase + ll.bound]) : 0ull;
+    const uint32_t hbase = min(static_cast<uint32_t>(lane), cpr - 1u) * stride;
+    //    Words whose high half is not used are loaded as their low 32 bits
+    //    (little-endian): a 64-bit load with a dead half lets the compiler
+    //    reuse that register, which needs a wait for the load first.
+    auto lo32 = [&](uint32_t w) { return load_shared(reinterpret_cast<const uint32_t*>(&slot_row[w])); };
+    const uint64_t hg0 = load_shared(&slot_row[hbase]);
+    const uint32_t hc0 = lo32(hbase + 1u);
+    const uint64_t hj0 = load_shared(&slot_row[hbase + 1u + j1]);
+    const uint32_t hb0 = lo32(hbase + ll.bound);
     const bool es = ej < j1;
     const uint32_t ebase = ec * stride;
-    const uint64_t er = es ? load_shared(&slot_row[ebase + 2u + ej]) : 0ull;
-    const uint64_t ef = es ? load_shared(&slot_row[ebase + ll.fin + ej]) : 0ull;
-    const uint64_t en = es ? load_shared(&slot_row[ebase + 1u]) : 0ull;
-    const uint64_t et = tid < 32 ? exp2_table(static_cast<uint32_t>(tid)) : 0ull;
+    const uint32_t ejc = min(ej, j1 - 1u);
+    const uint64_t er0 = load_shared(&slot_row[ebase + 2u + ejc]);
+    const uint32_t ef0 = lo32(ebase + ll.fin + ejc);
+    const uint32_t en0 = lo32(ebase + 1u);
+    const uint64_t et = exp2_table(static_cast<uint32_t>(tid) & 31u);
+    const uint64_t hg = hl ? hg0 : 0ull;
+    const uint32_t hc = hl ? hc0 : 0u;
+    const uint64_t hj = hl ? hj0 : 0ull;
+    const uint32_t hb = hl ? hb0 : 0u;
+    const uint64_t er = es ? er0 : 0ull;
+    const uint32_t ef = es ? ef0 : 0u;
+    const uint32_t en = es ? en0 : 0u;
     const float inv_temp = 1.0f / p.temperature;
     if (tid < 32) sh.exp_tab[tid] = et;
     // 2. G1 and B: over the chunks that listed j1 or more (a chunk that
