@@ -1710,15 +1710,20 @@ __device__ __forceinline__ void load_slots(const DevArgs& a, SelShared& sh, int 
     const uint32_t words = static_cast<uint32_t>(a.cpr) * stride;  // <= kSlotWords
     const uint64_t* slot_row = a.slots + static_cast<int64_t>(row) * kSlotWords;
     // All loads first (independent round trips in flight together), then the
-    // LDS writes that need their results.
+    // LDS writes that need their results. The loads are unconditional (words
+    // past the slots read the last word and are then dropped): a load under
+    // a lane mask is followed by a wait for every load in flight.
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         const uint32_t g = static_cast<uint32_t>(i * kBlock + tid);
-        w[i] = g < words ? load_shared(&slot_row[g]) : 0ull;
+        w[i] = load_shared(&slot_row[min(g, words - 1u)]);
     }
     // The expf table (2^(i/32)) from constant memory, in flight with the
     // lists (a wait for it alone would delay their issue by a round trip).
-    const uint64_t et = tid < 32 ? exp2_table(static_cast<uint32_t>(tid)) : 0ull;
+    const uint64_t et = exp2_table(static_cast<uint32_t>(tid) & 31u);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (static_cast<uint32_t>(i * kBlock + tid) >= words) w[i] = 0ull;
     uint32_t c = static_cast<uint32_t>(tid) / stride, q = static_cast<uint32_t>(tid) % stride;
     const uint32_t dc = kBlock / stride, dq = kBlock % stride;
 #pragma unroll
