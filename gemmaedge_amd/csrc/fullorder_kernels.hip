@@ -1747,11 +1747,14 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             nan = meta[kMetaAnyNan] != 0u;
         }
     }
-    uint64_t it_next = (!kSorted && tid < G) ? items[tid] : 0ull;
+    // (clamped prefetch: a masked load would wait for every load in flight)
+    uint64_t it_next = !kSorted ? items[min(tid, G - 1)] : 0ull;
     for (int r0 = 0; r0 < (kSorted ? 0 : G); r0 += kDThreads) {
         const int i = r0 + tid;
-        const uint64_t it = it_next;  // the next round's item loads while this one is scanned
-        it_next = i + kDThreads < G ? items[i + kDThreads] : 0ull;
+        // the next round's item loads while this one is scanned; lanes past
+        // G take 0 (an empty item) whatever the clamped load returned
+        const uint64_t it = i < G ? it_next : 0ull;
+        it_next = items[min(i + kDThreads, G - 1)];
         const uint32_t n = static_cast<uint32_t>(it);
         uint32_t tot;
         const uint32_t pi = run_base + dblock_excl_scan(n, sh.scan, tot);
