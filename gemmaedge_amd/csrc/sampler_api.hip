@@ -23,6 +23,7 @@
 static_assert(ge::kPlanBlock == ge::kBlock && ge::kPlanMaxTopK == ge::kMaxTopK &&
                   ge::kPlanMaxChunks == ge::kMaxChunks && ge::kPlanMaxChunkLen == ge::kBlock * ge::kMaxEpt,
               "plan and kernel geometry");
+static_assert(ge::kPlanStreamMaxChunks == ge::kStreamMaxChunks && ge::kStreamMaxChunks * 4 <= 64, "single-pass geometry");
 
 struct ge_sampler {
     int device;
@@ -32,6 +33,7 @@ struct ge_sampler {
     uint32_t* tickets;
     uint64_t* slots;
     uint64_t* poll;  // greedy calls on small grids, zero at creation
+    uint64_t* plists;  // single-pass kernel's candidate lists and call counts, zero at creation
     // Full-order path (bf16 rows with k > kMaxTopK); allocated when max_vocab > kMaxTopK.
     uint64_t* fo_items;
     float* fo_aux;
@@ -138,8 +140,10 @@ int ge_sampler_create(int device, int max_rows, int max_vocab, int max_history, 
     alloc(reinterpret_cast<void**>(&s->tickets), rows * sizeof(uint32_t));
     alloc(reinterpret_cast<void**>(&s->slots), rows * ge::kSlotWords * sizeof(uint64_t));
     alloc(reinterpret_cast<void**>(&s->poll), rows * ge::kPollStride * sizeof(uint64_t));
+    alloc(reinterpret_cast<void**>(&s->plists), rows * ge::kPollRowWords * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMemset(s->tickets, 0, rows * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(s->poll, 0, rows * ge::kPollStride * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMemset(s->plists, 0, rows * ge::kPollRowWords * sizeof(uint64_t));
     if (max_vocab > ge::kMaxTopK) {
         s->fo_items_stride = ge::fo_items_stride(max_history);
         s->fo_extras_cap = max_history < ge::kFoExtrasCap ? (max_history > 0 ? max_history : 1) : ge::kFoExtrasCap;
@@ -177,6 +181,7 @@ void ge_sampler_destroy(ge_sampler* s) {
     (void)hipFree(s->tickets);
     (void)hipFree(s->slots);
     (void)hipFree(s->poll);
+    (void)hipFree(s->plists);
     (void)hipFree(s->fo_items);
     (void)hipFree(s->fo_aux);
     (void)hipFree(s->fo_pre);
@@ -201,6 +206,7 @@ struct Workspace {
     uint32_t* tickets;
     uint64_t* slots;
     uint64_t* poll;  // NULL: greedy rows take tickets
+    uint64_t* plists;  // NULL: no single-pass kernel
     uint64_t* fo_items;
     float* fo_aux;
     uint32_t* fo_pre;
@@ -220,8 +226,9 @@ struct Workspace {
 int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
     ge::CallPlan plan{};
     char msg[256];
-    const int rc = ge::plan_call(x, ge::CallCapacity{ws.max_rows, ws.max_vocab, ws.fo_items != nullptr}, plan, msg,
-                                 sizeof(msg));
+    const int rc = ge::plan_call(
+        x, ge::CallCapacity{ws.max_rows, ws.max_vocab, ws.fo_items != nullptr, ws.plists != nullptr}, plan, msg,
+        sizeof(msg));
     if (rc != GE_OK) return fail(rc, "%s", msg);
     const bool run_select = plan.run_select;
     const bool run_full = plan.run_full;
@@ -258,6 +265,7 @@ int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
     const bool poll = plan.run_greedy && ws.poll && cpr <= ge::kPollChunks &&
                       static_cast<int64_t>(x.rows) * cpr <= ge::kPollMaxBlocks && x.vocab < (1 << 24);
     a.poll = poll ? ws.poll : nullptr;
+    a.plists = plan.run_stream ? ws.plists : nullptr;
     a.cpr = cpr;
     a.chunk_len = chunk_len;
     a.vec_ok = vec_ok ? 1 : 0;
@@ -279,7 +287,10 @@ int sample_on(const Workspace& ws, void* stream, const ge_sample_args& x) {
         const hipError_t e = ge::launch_greedy(a, st, ept);
         if (e != hipSuccess) return hip_fail(e, "launch (greedy)");
     }
-    if (run_select) {
+    if (plan.run_stream) {
+        const hipError_t e = ge::launch_stream(a, st);
+        if (e != hipSuccess) return hip_fail(e, "launch (single pass)");
+    } else if (run_select) {
         const hipError_t e = ge::launch_select(a, st, ept);
         if (e != hipSuccess) return hip_fail(e, "launch");
     }
@@ -355,6 +366,7 @@ int ge_sample(ge_sampler* s, void* stream, const ge_sample_args* args) {
     ws.tickets = s->tickets;
     ws.slots = s->slots;
     ws.poll = s->poll;
+    ws.plists = s->plists;
     ws.fo_items = s->fo_items;
     ws.fo_aux = s->fo_aux;
     ws.fo_pre = s->fo_pre;

@@ -21,6 +21,15 @@ constexpr int kPollChunks = 64;
 constexpr int kPollWords = kPollChunks * (kBlock / 64);
 constexpr int kPollStride = kPollWords + 8;
 constexpr int kPollMaxBlocks = 256;
+// Single-pass selection (stream_kernel): per row two areas of kPollListWords
+// for the polled candidate lists of up to 64 waves (16 chunks), used by
+// alternate calls (the parity of the row's call count, kept in the word at
+// kPollEpochWord), and kPollRowWords in all. The area a call uses is zero
+// when it starts: the previous call's other chunks cleared it.
+constexpr int kPollListWords = 1536;
+constexpr int kPollEpochWord = 2 * kPollListWords;
+constexpr int kPollRowWords = 2 * kPollListWords + 64;
+constexpr int kStreamMaxChunks = 16;
 
 // Device-side view of one ge_sample call plus the handle's workspace.
 struct DevArgs {
@@ -49,6 +58,7 @@ struct DevArgs {
     uint32_t* tickets;            // [max_rows]          zero between calls
     uint64_t* slots;              // [max_rows * kSlotWords]  per chunk: guarantee + sorted top-m list
     uint64_t* poll;               // [max_rows * kPollStride] or NULL: greedy chunks publish polled words
+    uint64_t* plists;             // [max_rows * kPollRowWords] or NULL: stream_kernel's candidate lists
 
     // Launch geometry of the streaming pass.
     int32_t cpr;                  // chunks per row
@@ -164,6 +174,11 @@ __device__ __forceinline__ void emit_row(const DevArgs& a, int row, int32_t toke
 // Launches the fused select/sample kernel for rows whose k <= kMaxTopK.
 // ept in {16, 64}. Returns a hipError_t.
 hipError_t launch_select(const DevArgs& a, hipStream_t stream, int ept);
+
+// Launches the single-pass selection kernel (CallPlan::run_stream: shared
+// parameters, 1 <= k <= 64, temperature > 0, no penalty below 1, 64 logits
+// per thread, at most kStreamMaxChunks chunks per row). Returns a hipError_t.
+hipError_t launch_stream(const DevArgs& a, hipStream_t stream);
 
 // Launches the greedy kernel (every row greedy, shared parameters): one pass,
 // ept in {16, 64}. Returns a hipError_t.

@@ -2729,12 +2729,517 @@ hipError_t launch_t(const DevArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---- Single-pass selection with polled candidate lists (stream_kernel) -----
+//
+// For calls with shared parameters, 1 <= k <= 64, temperature > 0 and no
+// penalty below 1 (CallPlan::run_stream), at 64 logits per thread and at most
+// 16 chunks per row. The chunks publish unsorted candidate lists and leave; no
+// chunk ranks anything, waits for its stores or takes a ticket at its end.
+//
+// Per chunk (workgroup), once its logits are in registers:
+//   1. each wave takes the q_hi-th and q_lo-th largest of its 64 lane maxima;
+//      the chunk's bounds tau_hi >= tau_lo are the smallest over its waves, so
+//      at least 4 q elements of the chunk lie at or above each;
+//   2. every wave lists the elements of its slots at or above tau_lo (a wave
+//      with fewer than q_lo lane maxima lists all its non-NaN elements) as
+//      final composite keys (softcap, then the penalty for history ids), and
+//      publishes the capped values of tau_hi and tau_lo as its header.
+// Every element a chunk leaves out has a raw value below tau_lo, so its final
+// value is at most softcap(tau_lo) (softcap is monotone and a penalty >= 1
+// never raises a value); with B the largest capped bound of the row at a
+// level, every element whose final value exceeds B is listed. So when at
+// least k listed entries exceed B, their top k (final value descending, index
+// ascending) is the row's top k: everything outside ends at or below B.
+//
+// The merging workgroup of a row is its last chunk, the row's highest block
+// index in dispatch order (also under the XCD-aware mapping): workgroups are
+// dispatched in index order, so every other workgroup of the row has been
+// dispatched before it, and they finish without waiting for anything; the
+// merge's wait ends, resident grid or not. (A start ticket would pin this
+// without the dispatch order, but its atomic's return, queued behind the
+// streaming loads, held back every workgroup's loads: C2 30 us.) The wait is
+// bounded all the same (kPlSpins: GE_FLAG_TIMEOUT). It polls the row's list
+// words, which are zero between calls: a list is complete when its header and
+// all its entry words are non-zero (each wave writes every word of its list,
+// unused positions as kPlFiller). Then it clears them for the next call,
+// takes the row's bound at level hi (or lo when hi leaves fewer than k
+// entries), ranks the entries above it and runs the reference's softmax,
+// min-p / top-p and draw (src/generation.cpp:89-126). A row with fewer than k
+// entries above either bound, an overflowing list or a wait that runs out
+// falls back to exact rescans of every chunk.
+//
+// Cross-workgroup words are agent-scope relaxed atomic stores and loads (the
+// sc1 bit: coherent across the XCDs' L2s); each word is written once per call
+// and read only after it is seen non-zero, and 64-bit aligned stores are
+// single-copy atomic, so no fence or ordering between words is needed.
+
+constexpr uint32_t kPlPer = 6;          // entry words per merging thread per list
+constexpr uint32_t kPlMaxEntries = 62;  // entry positions of one list at most
+constexpr uint64_t kPlFiller = 1;    // an unused entry position (value key 0: never a candidate)
+constexpr uint64_t kPlOverflow = ~uint64_t{0}; // header of a list that could not hold its candidates
+constexpr uint32_t kPlCand = 4;         // candidates a lane stages (more: the list overflows)
+constexpr uint32_t kPlSpins = 1u << 22; // about 4 s of polling; every awaited workgroup has started
+
+// Entry positions per list for a row of nl = 4 * cpr lists (nl <= 64). An
+// area holds the nl headers, then each list's entries in turn: nl * (1 + ne)
+// <= kPollListWords = kPlPer * kBlock words, so the merge reads the entries
+// as kPlPer contiguous words per thread.
+__device__ __forceinline__ uint32_t pl_entries(uint32_t nl) {
+    return min(static_cast<uint32_t>(kPollListWords) / nl - 1u, kPlMaxEntries);
+}
+
+// Lane-maximum ranks of the two levels for a row with effective top-k k over
+// cpr chunks: with mu = k / cpr, about (mu + sd + 2) / 4 and (mu + 2 sd + 4) / 4
+// per wave (sd = sqrt(mu)). Any values are correct (they only set how many
+// entries are listed); these keep the lists short while level lo leaves at
+// least k entries above its bound in nearly every row (simulated on the
+// benchmark distributions). Deterministic, so every workgroup of a row agrees.
+__device__ __forceinline__ void pl_levels(uint32_t k, int cpr, uint32_t entries, uint32_t& qhi, uint32_t& qlo) {
+    const float mu = spec_mu(k, cpr);
+    const float sd = __builtin_amdgcn_sqrtf(mu);
+    qlo = static_cast<uint32_t>(ceilf((mu + 2.0f * sd + 4.0f) * 0.25f));
+    qhi = static_cast<uint32_t>(ceilf((mu + sd + 2.0f) * 0.25f));
+    qlo = min(max(qlo, 1u), max(min(16u, entries / 2u), 1u));
+    qhi = min(max(qhi, 1u), qlo);
+}
+
+template <typename T, int EPT>
+__global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
+    constexpr int W = sizeof(T) == 4 ? 4 : 8;  // elements per 16-byte load
+    constexpr int NV = EPT / W;                 // 16-byte loads per thread
+    constexpr int NW = EPT * sizeof(T) / 4;     // 32-bit words per thread
+    constexpr int CHUNK = kBlock * EPT;
+    constexpr int NG = EPT / 4;                 // groups of 4 slots per thread
+    static_assert(EPT % W == 0 && EPT <= 64 && EPT % 4 == 0, "bad tiling");
+    __shared__ uint32_t s_pbits[CHUNK / 32];
+    __shared__ SelShared sh;
+
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const int wave = tid >> 6;
+    // XCD-aware mapping as in select_kernel: each XCD streams whole rows.
+    int bid = static_cast<int>(blockIdx.x);
+    if ((a.rows & 7) == 0) bid = (bid & 7) * static_cast<int>(gridDim.x >> 3) + (bid >> 3);
+    const int row = bid / a.cpr;
+    const int chunk = bid - row * a.cpr;
+    const int V = a.vocab;
+    const ge_sample_params p = a.params;  // launched only with shared parameters
+    const uint32_t k = p.top_k ? min(p.top_k, static_cast<uint32_t>(V)) : static_cast<uint32_t>(V);  // generation.cpp:80
+    if (row_done(a, row)) {
+        // Finished by an earlier call: nothing is read, no ticket is taken.
+        if (chunk == 0 && tid == 0) skipped_row(a, row);
+        return;
+    }
+    RowCtx rc;
+    rc.rowp = static_cast<const T*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
+    row_history(a, row, rc.hist, rc.H);
+    rc.row = row;
+    rc.V = V;
+    rc.vec_ok = a.vec_ok;
+    rc.r = p.repetition_penalty;
+    rc.pen = rc.H > 0 && !(rc.r == 1.0f);
+    rc.cap = p.softcap;
+    const T* rowp = static_cast<const T*>(rc.rowp);
+    const int c0 = chunk * CHUNK;
+    const int cend = min(c0 + CHUNK, V);
+    const uint32_t nl = 4u * static_cast<uint32_t>(a.cpr);
+    const uint32_t ne = pl_entries(nl);  // entry positions per list
+    // The row's call count: its parity picks this call's list area.
+    uint64_t* const prow_base = a.plists + static_cast<int64_t>(row) * kPollRowWords;
+    const uint64_t epoch = scalar_load(prow_base + kPollEpochWord);
+    uint64_t* const prow = prow_base + (epoch & 1ull) * kPollListWords;
+    uint64_t* const pnext = prow_base + ((epoch + 1ull) & 1ull) * kPollListWords;
+
+    // 1. The first kBlock * kLoadBatch history ids, then the chunk's 16-byte
+    //    nontemporal loads; the chunk's penalty bitmap is built from the ids
+    //    while the logits are in flight (as in chunk_topm).
+    int hid[kLoadBatch];
+    if (rc.pen) {
+#pragma unroll
+        for (int u = 0; u < kLoadBatch; ++u) hid[u] = rc.hist[min(u * kBlock + tid, rc.H - 1)];
+    }
+    auto mark_history = [&]() {
+        if (!rc.pen) return;
+        for (int w = tid; w < CHUNK / 32; w += kBlock) s_pbits[w] = 0u;
+        __syncthreads();
+        for (int base = 0; base < rc.H; base += kBlock * kLoadBatch) {
+            if (base > 0) {
+#pragma unroll
+                for (int u = 0; u < kLoadBatch; ++u) hid[u] = rc.hist[min(base + u * kBlock + tid, rc.H - 1)];
+            }
+#pragma unroll
+            for (int u = 0; u < kLoadBatch; ++u)
+                if (base + u * kBlock + tid < rc.H && hid[u] >= c0 && hid[u] < cend)
+                    atomicOr(&s_pbits[(hid[u] - c0) >> 5], 1u << ((hid[u] - c0) & 31));
+        }
+    };
+    uint32_t d[NW];
+    auto value = [&](int s) -> float {
+        if constexpr (W == 4) return u2f(d[s]);
+        else return u2f((s % 2 == 0) ? (d[s / 2] << 16) : (d[s / 2] & 0xffff0000u));
+    };
+    constexpr uint32_t kHole = 0x7fc00000u;  // NaN in out-of-range slots
+    if (rc.vec_ok && c0 + CHUNK <= V) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + c0 + (v * kBlock + tid) * W));
+            d[4 * v + 0] = q.x;
+            d[4 * v + 1] = q.y;
+            d[4 * v + 2] = q.z;
+            d[4 * v + 3] = q.w;
+        }
+        mark_history();
+    } else {
+        mark_history();
+#pragma unroll
+        for (int s = 0; s < EPT; ++s) {
+            const int e = c0 + ((s / W) * kBlock + tid) * W + (s % W);
+            const uint32_t bits = e < cend ? f2u(load_one(rowp, e)) : kHole;
+            if constexpr (W == 4) {
+                d[s] = bits;
+            } else if (s % 2 == 0) {
+                d[s / 2] = bits >> 16;
+            } else {
+                d[s / 2] |= bits & 0xffff0000u;
+            }
+        }
+    }
+    const float u = a.uniforms[row];
+    if (tid < 32) sh.exp_tab[tid] = exp2_table(static_cast<uint32_t>(tid));
+
+    // 2. Maxima of groups of 4 slots and of the lane (fmaxf skips NaN).
+    float gm[NG];
+    float lmf = NAN;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        float x = value(g * 4);
+#pragma unroll
+        for (int j = 1; j < 4; ++j) x = fmaxf(x, value(g * 4 + j));
+        gm[g] = x;
+        lmf = fmaxf(lmf, x);
+    }
+    // bf16: the packed words made opaque, so that the unpacked floats are
+    // recomputed in the staging loop instead of held in registers.
+    if constexpr (W == 8) {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) asm volatile("" : "+v"(d[i]));
+    }
+    // 3. The wave's q_hi-th and q_lo-th largest lane maxima (lanes without a
+    //    number count as 0); 0 means fewer such lanes: no bound from this wave.
+    uint32_t qhi, qlo;
+    pl_levels(k, a.cpr, ne, qhi, qlo);
+    uint32_t key = order_key(lmf);
+    key = key > kKeyNaN ? key : 0u;
+    uint32_t thi = 0u, tlo = 0u;
+    for (uint32_t i = 0; i < qlo; ++i) {
+        const uint32_t mx = wave::max_u32(key);
+        const uint64_t eq = __ballot(key == mx);
+        if (lane == __ffsll(static_cast<unsigned long long>(eq)) - 1) key = 0u;
+        if (i + 1u == qhi) thi = mx;
+        tlo = mx;
+    }
+    if (lane == 0) {
+        sh.u32[8 + wave] = thi ? thi : 0xffffffffu;
+        sh.u32[12 + wave] = tlo ? tlo : 0xffffffffu;
+    }
+    __syncthreads();  // (also orders the bitmap's marks before the reads below)
+    const uint32_t tau_hi = min(min(sh.u32[8], sh.u32[9]), min(sh.u32[10], sh.u32[11]));
+    const uint32_t tau_lo = min(min(sh.u32[12], sh.u32[13]), min(sh.u32[14], sh.u32[15]));
+    const bool merger = chunk == a.cpr - 1;
+
+    // 4. Stage this wave's candidates: lane l keeps its c-th at seg[64 c + l]
+    //    (c < kPlCand), then they move to cmp[0, n_w) in (c, lane) order.
+    const float floor_v = tlo ? key_value(tau_lo) : -INFINITY;
+    uint64_t* seg = sh.stage + wave * kSeg;
+    uint64_t* cmp = seg + kPlCand * 64;
+    const uint32_t ebase = static_cast<uint32_t>(c0 + tid * W);
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        if (__ballot(gm[g] >= floor_v) == 0ull) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int s = 4 * g + j;
+            const float x = value(s);
+            if (x >= floor_v) {
+                const uint32_t e = ebase + static_cast<uint32_t>((s / W) * kBlock * W + s % W);
+                if (cnt < kPlCand) seg[64u * cnt + static_cast<uint32_t>(lane)] = (static_cast<uint64_t>(f2u(x)) << 32) | e;
+                ++cnt;
+            }
+        }
+    }
+    const uint64_t m0 = __ballot(cnt > 0u), m1 = __ballot(cnt > 1u), m2 = __ballot(cnt > 2u), m3 = __ballot(cnt > 3u);
+    const uint32_t p0 = static_cast<uint32_t>(__popcll(m0)), p1 = static_cast<uint32_t>(__popcll(m1));
+    const uint32_t p2 = static_cast<uint32_t>(__popcll(m2)), p3 = static_cast<uint32_t>(__popcll(m3));
+    const uint32_t n_w = p0 + p1 + p2 + p3;
+    const bool overflow = __ballot(cnt > kPlCand) != 0ull || n_w > ne;
+    {
+        uint64_t y0 = 0, y1 = 0, y2 = 0, y3 = 0;
+        if (cnt > 0u) y0 = seg[lane];
+        if (cnt > 1u) y1 = seg[64 + lane];
+        if (cnt > 2u) y2 = seg[128 + lane];
+        if (cnt > 3u) y3 = seg[192 + lane];
+        if (cnt > 0u) cmp[lanes_below(m0)] = y0;
+        if (cnt > 1u) cmp[p0 + lanes_below(m1)] = y1;
+        if (cnt > 2u) cmp[p0 + p1 + lanes_below(m2)] = y2;
+        if (cnt > 3u) cmp[p0 + p1 + p2 + lanes_below(m3)] = y3;
+    }
+    wave_lds_sync();
+    // 5. Final keys (one softcap round for the wave: lane i < n_w takes
+    //    candidate i, lanes 62 and 63 the values of tau_hi and tau_lo), then
+    //    the list: entries, fillers, header.
+    float xv = 0.0f;
+    uint32_t idx = 0u;
+    bool pen = false;
+    const bool cand = !overflow && static_cast<uint32_t>(lane) < n_w;
+    if (cand) {
+        const uint64_t y = cmp[lane];
+        xv = u2f(static_cast<uint32_t>(y >> 32));
+        idx = static_cast<uint32_t>(y);
+        if (rc.pen) {
+            const uint32_t off = idx - static_cast<uint32_t>(c0);
+            pen = ((s_pbits[off >> 5] >> (off & 31)) & 1u) != 0u;
+        }
+    } else if (lane == 62) {
+        xv = tau_hi != 0xffffffffu ? key_value(tau_hi) : 0.0f;
+    } else if (lane == 63) {
+        xv = tau_lo != 0xffffffffu ? key_value(tau_lo) : 0.0f;
+    }
+    float f = softcap(xv, rc.cap);
+    if (pen) f = penalize(f, rc.r);
+    const uint32_t fk = order_key(f);
+    const uint32_t bhi = tau_hi != 0xffffffffu ? wave::readlane(fk, 62) : kKeyNaN;
+    const uint32_t blo = tau_lo != 0xffffffffu ? wave::readlane(fk, 63) : kKeyNaN;
+    const uint64_t hword = overflow ? kPlOverflow : ((static_cast<uint64_t>(bhi) << 32) | blo);
+    const uint64_t eword = cand ? composite(fk, idx) : kPlFiller;
+    const uint32_t lj_own = static_cast<uint32_t>(chunk) * 4u + static_cast<uint32_t>(wave);
+    if (!merger) {
+        // Publish the list (header, then entries), then clear this wave's
+        // share of the row's other area (the next call's; no call reads it
+        // now): every word of it.
+        if (static_cast<uint32_t>(lane) < ne) store_shared(&prow[nl + lj_own * ne + static_cast<uint32_t>(lane)], eword);
+        if (lane == 0) store_shared(&prow[lj_own], hword);
+        const uint32_t lanes = static_cast<uint32_t>(a.cpr - 1) * static_cast<uint32_t>(kBlock);
+        for (uint32_t i = static_cast<uint32_t>(chunk) * kBlock + static_cast<uint32_t>(tid); i < kPollListWords; i += lanes)
+            store_shared(&pnext[i], uint64_t{0});
+        return;
+    }
+    // The merging chunk keeps its own four lists in LDS, laid out as in the
+    // area (no global stores ahead of its polling loads: one wait counter
+    // covers both): headers in own_h, entries contiguous in own_e.
+    uint64_t* own_h = sh.list;
+    uint64_t* own_e = sh.list + 4;
+    if (static_cast<uint32_t>(lane) < ne) own_e[static_cast<uint32_t>(wave) * ne + static_cast<uint32_t>(lane)] = eword;
+    if (lane == 0) own_h[wave] = hword;
+    __syncthreads();
+
+    // ---- Merge (the row's last chunk) ----
+    // 6. Poll: thread t reads header t % nl (each wave thus holds all nl) and
+    //    the entry words t + kBlock i of the area, contiguous across lanes.
+    //    The last four lists are this chunk's own, read from LDS. A list is
+    //    complete when all its words are non-zero.
+    const uint32_t lj = static_cast<uint32_t>(tid) % nl;
+    const uint32_t nent = nl * ne;
+    const uint32_t own0 = (nl - 4u) * ne;  // first entry word of the own lists
+    uint32_t eidx[kPlPer];
+    bool ev[kPlPer];
+#pragma unroll
+    for (uint32_t i = 0; i < kPlPer; ++i) {
+        const uint32_t u = static_cast<uint32_t>(tid) + kBlock * i;
+        ev[i] = u < nent;
+        eidx[i] = min(u, nent - 1u);
+    }
+    const bool hmine = lj >= nl - 4u;
+    uint64_t h = 0ull;
+    uint64_t e[kPlPer];
+    bool timed_out = true;
+    for (uint32_t it = 0; it < kPlSpins; ++it) {
+        // Unconditional loads (clamped positions): a load under a lane mask
+        // is followed by a wait for every load in flight.
+        h = load_shared(&prow[lj]);
+#pragma unroll
+        for (uint32_t i = 0; i < kPlPer; ++i) e[i] = load_shared(&prow[nl + eidx[i]]);
+        if (hmine) h = own_h[lj - (nl - 4u)];
+#pragma unroll
+        for (uint32_t i = 0; i < kPlPer; ++i)
+            if (eidx[i] >= own0) e[i] = own_e[eidx[i] - own0];
+        bool ok = h != 0ull;
+#pragma unroll
+        for (uint32_t i = 0; i < kPlPer; ++i) ok = ok && (!ev[i] || e[i] != 0ull);
+        const uint32_t flag = 20u + 4u * (it & 1u);  // alternate words: one barrier per round
+        const bool missing = __ballot(!ok) != 0ull;   // (every lane votes: outside the lane-0 branch)
+        if (lane == 0) sh.u32[flag + wave] = missing ? 1u : 0u;
+        __syncthreads();
+        if ((sh.u32[flag] | sh.u32[flag + 1] | sh.u32[flag + 2] | sh.u32[flag + 3]) == 0u) {
+            timed_out = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    // 7. The next call on this row takes the other area (which the other
+    //    chunks have cleared): the count goes up once, after the merge (every
+    //    chunk of the row has read it by now, having published its list).
+    auto bump_epoch = [&]() {
+        if (tid == 0) store_shared(prow_base + kPollEpochWord, static_cast<uint64_t>(epoch + 1u));
+    };
+
+    // 8. The row's bounds per level (every wave reduces the headers it
+    //    holds), the entries above each, and the largest final key.
+    const uint32_t bnd_hi = wave::max_u32(static_cast<uint32_t>(h >> 32));
+    const uint32_t bnd_lo = wave::max_u32(static_cast<uint32_t>(h));
+    uint32_t c_hi = 0u, c_lo = 0u, kmx = 0u;
+#pragma unroll
+    for (uint32_t i = 0; i < kPlPer; ++i) {
+        const uint32_t ky = ev[i] ? static_cast<uint32_t>(e[i] >> 32) : 0u;
+        c_hi += ky > bnd_hi ? 1u : 0u;
+        c_lo += ky > bnd_lo ? 1u : 0u;
+        kmx = max(kmx, ky);
+    }
+    const uint32_t s_hi = wave::incl_add(c_hi), s_lo = wave::incl_add(c_lo);
+    const uint32_t w_kmx = wave::max_u32(kmx);
+    if (lane == 63) {
+        sh.u32[8 + wave] = s_hi;
+        sh.u32[12 + wave] = s_lo;
+    }
+    if (lane == 0) sh.u32[28 + wave] = w_kmx;
+    __syncthreads();
+    uint32_t n_hi = 0u, n_lo = 0u, b_hi = 0u, b_lo = 0u;
+#pragma unroll
+    for (int w = 0; w < kBlock / 64; ++w) {
+        b_hi += w < wave ? sh.u32[8 + w] : 0u;
+        b_lo += w < wave ? sh.u32[12 + w] : 0u;
+        n_hi += sh.u32[8 + w];
+        n_lo += sh.u32[12 + w];
+    }
+    const uint32_t kmax = max(max(sh.u32[28], sh.u32[29]), max(sh.u32[30], sh.u32[31]));
+    const bool use_hi = n_hi >= k && n_hi <= static_cast<uint32_t>(kBlock);
+    const uint32_t n = use_hi ? n_hi : n_lo;
+    if (!timed_out && n >= k && n <= static_cast<uint32_t>(kBlock)) {
+        // 9. The entries above the chosen bound into stage[0, n), each at its
+        //    wave's base plus its lanes' prefix.
+        const uint32_t bnd = use_hi ? bnd_hi : bnd_lo;
+        uint32_t pos = (use_hi ? b_hi + s_hi - c_hi : b_lo + s_lo - c_lo);
+#pragma unroll
+        for (uint32_t i = 0; i < kPlPer; ++i)
+            if (ev[i] && static_cast<uint32_t>(e[i] >> 32) > bnd) sh.stage[pos++] = e[i];
+        __syncthreads();
+        // 10. Rank by counting; the top k and their expf terms by rank.
+        const float maximum = key_value(kmax);
+        const float inv_temp = 1.0f / p.temperature;
+        float* ex = reinterpret_cast<float*>(sh.list);
+        if (static_cast<uint32_t>(tid) < n) {
+            const uint64_t x = sh.stage[tid];
+            const float t = expf_glibc_tab((key_value(composite_key(x)) - maximum) * inv_temp,
+                                           [&](uint32_t i) { return sh.exp_tab[i]; });
+            const ulonglong2* p2 = reinterpret_cast<const ulonglong2*>(sh.stage);
+            uint32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+            const uint32_t full = n / 8u;
+            uint32_t j = 0;
+            for (; j + 2u <= full; j += 2u) {
+                const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
+                const ulonglong2 q4 = p2[4 * j + 4], q5 = p2[4 * j + 5], q6 = p2[4 * j + 6], q7 = p2[4 * j + 7];
+                r0 = add_greater4(r0, q0.x, q0.y, q1.x, q1.y, x);
+                r1 = add_greater4(r1, q2.x, q2.y, q3.x, q3.y, x);
+                r2 = add_greater4(r2, q4.x, q4.y, q5.x, q5.y, x);
+                r3 = add_greater4(r3, q6.x, q6.y, q7.x, q7.y, x);
+            }
+            if (j < full) {
+                const ulonglong2 q0 = p2[4 * j + 0], q1 = p2[4 * j + 1], q2 = p2[4 * j + 2], q3 = p2[4 * j + 3];
+                r0 = add_greater4(r0, q0.x, q0.y, q1.x, q1.y, x);
+                r1 = add_greater4(r1, q2.x, q2.y, q3.x, q3.y, x);
+                ++j;
+            }
+            if (8u * j < n) {
+                const uint32_t b = 8u * j;
+                uint64_t q[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) q[i] = b + static_cast<uint32_t>(i) < n ? sh.stage[b + static_cast<uint32_t>(i)] : 0ull;
+                r2 = add_greater4(r2, q[0], q[1], q[2], q[3], x);
+                r3 = add_greater4(r3, q[4], q[5], q[6], q[7], x);
+            }
+            const uint32_t rk = (r0 + r1) + (r2 + r3);
+            if (rk < k) {
+                sh.top[rk] = x;
+                ex[rk] = t;
+            }
+        }
+        __syncthreads();
+        if (wave != 0) {
+            bump_epoch();
+            return;
+        }
+        // 11. generation.cpp:89-126 over the k terms (wave 0).
+        const bool live = static_cast<uint32_t>(lane) < k;
+        const float et = live ? ex[lane] : 0.0f;
+        const bool bad = live && (!(et >= 0.0f) || __builtin_isinf(et));
+        const int lsb = (live && et > 0.0f && !bad) ? lsb_exponent(et) : INT_MAX;
+        const double s = wave_sum(static_cast<double>(et));
+        const int mn = wave_min_i(lsb);
+        const int ex2 = static_cast<int>((d2u(s) >> 52) & 0x7ffu) - 1023;
+        double den;
+        // Exact when every term is a multiple of 2^mn and the sum fits 53 bits
+        // above it: any order then equals the sequential sum.
+        if (!__any(bad) && s > 0.0 && !__builtin_isinf(s) && mn >= ex2 - 51) {
+            den = s;
+        } else {
+            den = 0.0;
+            for (uint32_t i = 0; i < k; ++i) den += static_cast<double>(readlane_f(et, static_cast<int>(i)));
+        }
+        const float inv_denom = static_cast<float>(1.0 / den);
+        const float pr = et * inv_denom;
+        float* scratch = ex + 64;  // 128 floats for the sequential chains
+        uint32_t wpos;
+        bool near;
+        if (!__any(live && __builtin_isnan(pr))) {
+            scan_walk_wave(pr, k, p, u, scratch, wpos, near);
+        } else {
+            scan_and_walk([&](uint32_t g) { return g == 0 ? pr : 0.0f; }, k, p, u, wpos, near);
+        }
+        const float ppos = readlane_f(pr, static_cast<int>(wpos));
+        if (lane == 0)
+            emit_row(a, row, static_cast<int32_t>(composite_index(sh.top[wpos])), ppos,
+                     near ? GE_FLAG_NEAR_BOUNDARY : 0);
+        bump_epoch();
+        return;
+    }
+    bump_epoch();
+    if (timed_out) {
+        if (tid == 0) emit_row(a, row, -1, 0.0f, GE_FLAG_TIMEOUT);
+        return;
+    }
+    // 12. Fallback (fewer than k entries above the bound, or an overflowing
+    //     list): exact rescans of every chunk (chunk_slow stages at most 2k
+    //     entries, within kStage), merged into the top k.
+    __syncthreads();
+    uint32_t nt = 0;
+    for (int c = 0; c < a.cpr; ++c) {
+        bool rok;
+        const uint32_t nlist = rescan_chunk<T, EPT>(rc, c, k, s_pbits, sh, rok);
+        if (!rok) {
+            if (tid == 0) emit_row(a, row, -1, 0.0f, GE_FLAG_UNSUPPORTED);
+            return;
+        }
+        nt = absorb_list(sh, nt, nlist, k);
+    }
+    merge_finish<T>(a, sh, rc, p, false, min(nt, k), u, 0.0f, sh.top, reinterpret_cast<float*>(sh.stage));
+}
+
+template <typename T>
+hipError_t launch_stream_t(const DevArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((stream_kernel<T, kMaxEpt>), dim3(static_cast<unsigned>(a.rows * a.cpr)), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_select(const DevArgs& a, hipStream_t stream, int ept) {
     if (a.dtype == GE_DTYPE_BF16)
         return ept == 16 ? launch_t<uint16_t, 16>(a, stream) : launch_t<uint16_t, 64>(a, stream);
     return ept == 16 ? launch_t<float, 16>(a, stream) : launch_t<float, 64>(a, stream);
+}
+
+hipError_t launch_stream(const DevArgs& a, hipStream_t stream) {
+    return a.dtype == GE_DTYPE_BF16 ? launch_stream_t<uint16_t>(a, stream) : launch_stream_t<float>(a, stream);
 }
 
 }  // namespace ge

@@ -19,13 +19,16 @@ constexpr int kPlanBlock = 256;     // threads per workgroup of the selection pa
 constexpr int kPlanMaxTopK = 1024;  // largest k of the selection path
 constexpr int kPlanMaxChunks = 256; // chunks per row
 constexpr int64_t kPlanMaxChunkLen = static_cast<int64_t>(kPlanBlock) * 64;
+constexpr int kPlanStreamMaxTopK = 64;     // largest k of the single-pass selection kernel
+constexpr int kPlanStreamMaxChunks = 16;   // chunks per row it handles
 
-// What a call may use: its row and vocab capacity and whether a full-order
-// workspace exists.
+// What a call may use: its row and vocab capacity, whether a full-order
+// workspace exists and whether the single-pass kernel's list area does.
 struct CallCapacity {
     int max_rows;
     int max_vocab;
     bool full_order;
+    bool stream;
 };
 
 // The kernels a valid call launches and the selection pass's geometry.
@@ -33,6 +36,7 @@ struct CallPlan {
     bool run_select;
     bool run_full;
     bool run_greedy;  // every row greedy (shared parameters, temperature <= 0)
+    bool run_stream;  // the selection rows take the single-pass kernel instead
     int ept;        // logits per thread of the selection or greedy pass (16 or 64)
     int cpr;        // chunks per row
     bool vec_ok;    // rows 16-byte aligned: vector loads
@@ -119,6 +123,20 @@ inline int plan_call(const ge_sample_args& x, const CallCapacity& cap, CallPlan&
                          static_cast<long long>(kPlanMaxChunkLen * kPlanMaxChunks));
     const int64_t esize = x.dtype == GE_DTYPE_BF16 ? 2 : 4;
     plan.vec_ok = (reinterpret_cast<uintptr_t>(x.logits) % 16 == 0) && ((x.row_stride * esize) % 16 == 0);
+    // The single-pass kernel: shared parameters with 1 <= k <= 64 and
+    // temperature > 0, a penalty that cannot raise a value (r >= 1, or no
+    // history), 64 logits per thread and 2 to 16 chunks per row (the chunks
+    // other than the merging one clear the list area of the row's next call).
+    plan.run_stream = false;
+    if (plan.run_select && cap.stream && !x.row_params && plan.ept == 64 && plan.cpr >= 2 &&
+        plan.cpr <= kPlanStreamMaxChunks) {
+        const ge_sample_params& p = x.params;
+        const uint32_t v = static_cast<uint32_t>(x.vocab);
+        const uint32_t k = p.top_k ? (p.top_k < v ? p.top_k : v) : v;
+        const bool has_history = x.ring != nullptr || x.history != nullptr;
+        plan.run_stream = p.temperature > 0.0f && k >= 1u && k <= static_cast<uint32_t>(kPlanStreamMaxTopK) &&
+                          (p.repetition_penalty >= 1.0f || !has_history);
+    }
     return GE_OK;
 }
 

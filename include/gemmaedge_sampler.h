@@ -52,6 +52,8 @@ extern "C" {
 #define GE_FLAG_UNSUPPORTED 2    /* row's parameters need a path this build lacks; token = -1 */
 #define GE_FLAG_STOP 4           /* the token is one of the stop tokens; done[row] was set */
 #define GE_FLAG_DONE 8           /* done[row] was set on entry: nothing sampled, token = -1 */
+#define GE_FLAG_TIMEOUT 16       /* a bounded wait for the row's other workgroups ran out (about 4 s;
+                                    not reached in a correct run): token = -1 */
 
 /* Where a sampled stop token goes (ge_sample_args.stop_mode). The reference
  * has both orders: Gemma4Session::generate appends the token to its output
