@@ -2788,19 +2788,16 @@ __device__ __forceinline__ uint32_t pl_entries(uint32_t nl) {
     return min(static_cast<uint32_t>(kPollListWords) / nl - 1u, kPlMaxEntries);
 }
 
-// Lane-maximum ranks of the two levels for a row with effective top-k k over
-// cpr chunks: with mu = k / cpr, about (mu + sd + 2) / 4 and (mu + 2 sd + 4) / 4
-// per wave (sd = sqrt(mu)). Any values are correct (they only set how many
-// entries are listed); these keep the lists short while level lo leaves at
-// least k entries above its bound in nearly every row (simulated on the
-// benchmark distributions). Deterministic, so every workgroup of a row agrees.
-__device__ __forceinline__ void pl_levels(uint32_t k, int cpr, uint32_t entries, uint32_t& qhi, uint32_t& qlo) {
+// Lane-maximum rank of the chunk bound for a row with effective top-k k over
+// cpr chunks: with mu = k / cpr, about (mu + 2 sqrt(mu) + 4) / 4 per wave. Any
+// value is correct (it only sets how many entries are listed); this one keeps
+// the lists short while leaving at least k entries above the row's bound in
+// nearly every row (simulated on the benchmark distributions).
+// Deterministic, so every workgroup of a row agrees.
+__device__ __forceinline__ uint32_t pl_rank(uint32_t k, int cpr, uint32_t entries) {
     const float mu = spec_mu(k, cpr);
-    const float sd = __builtin_amdgcn_sqrtf(mu);
-    qlo = static_cast<uint32_t>(ceilf((mu + 2.0f * sd + 4.0f) * 0.25f));
-    qhi = static_cast<uint32_t>(ceilf((mu + sd + 2.0f) * 0.25f));
-    qlo = min(max(qlo, 1u), max(min(16u, entries / 2u), 1u));
-    qhi = min(max(qhi, 1u), qlo);
+    const uint32_t q = static_cast<uint32_t>(ceilf((mu + 2.0f * __builtin_amdgcn_sqrtf(mu) + 4.0f) * 0.25f));
+    return min(max(q, 1u), max(min(16u, entries / 2u), 1u));
 }
 
 template <typename T, int EPT>
@@ -2924,26 +2921,20 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
 #pragma unroll
         for (int i = 0; i < NW; ++i) asm volatile("" : "+v"(d[i]));
     }
-    // 3. The wave's q_hi-th and q_lo-th largest lane maxima (lanes without a
-    //    number count as 0); 0 means fewer such lanes: no bound from this wave.
-    uint32_t qhi, qlo;
-    pl_levels(k, a.cpr, ne, qhi, qlo);
+    // 3. The wave's q-th largest lane maximum (lanes without a number count
+    //    as 0); 0 means fewer such lanes: no bound from this wave.
+    const uint32_t qlo = pl_rank(k, a.cpr, ne);
     uint32_t key = order_key(lmf);
     key = key > kKeyNaN ? key : 0u;
-    uint32_t thi = 0u, tlo = 0u;
+    uint32_t tlo = 0u;
     for (uint32_t i = 0; i < qlo; ++i) {
         const uint32_t mx = wave::max_u32(key);
         const uint64_t eq = __ballot(key == mx);
         if (lane == __ffsll(static_cast<unsigned long long>(eq)) - 1) key = 0u;
-        if (i + 1u == qhi) thi = mx;
         tlo = mx;
     }
-    if (lane == 0) {
-        sh.u32[8 + wave] = thi ? thi : 0xffffffffu;
-        sh.u32[12 + wave] = tlo ? tlo : 0xffffffffu;
-    }
+    if (lane == 0) sh.u32[12 + wave] = tlo ? tlo : 0xffffffffu;
     __syncthreads();  // (also orders the bitmap's marks before the reads below)
-    const uint32_t tau_hi = min(min(sh.u32[8], sh.u32[9]), min(sh.u32[10], sh.u32[11]));
     const uint32_t tau_lo = min(min(sh.u32[12], sh.u32[13]), min(sh.u32[14], sh.u32[15]));
     const bool merger = chunk == a.cpr - 1;
 
@@ -2986,8 +2977,8 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
     }
     wave_lds_sync();
     // 5. Final keys (one softcap round for the wave: lane i < n_w takes
-    //    candidate i, lanes 62 and 63 the values of tau_hi and tau_lo), then
-    //    the list: entries, fillers, header.
+    //    candidate i, lane 63 the value of tau), then the list: entries,
+    //    fillers, and the header [largest final key | capped tau].
     float xv = 0.0f;
     uint32_t idx = 0u;
     bool pen = false;
@@ -3000,17 +2991,15 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
             const uint32_t off = idx - static_cast<uint32_t>(c0);
             pen = ((s_pbits[off >> 5] >> (off & 31)) & 1u) != 0u;
         }
-    } else if (lane == 62) {
-        xv = tau_hi != 0xffffffffu ? key_value(tau_hi) : 0.0f;
     } else if (lane == 63) {
         xv = tau_lo != 0xffffffffu ? key_value(tau_lo) : 0.0f;
     }
     float f = softcap(xv, rc.cap);
     if (pen) f = penalize(f, rc.r);
     const uint32_t fk = order_key(f);
-    const uint32_t bhi = tau_hi != 0xffffffffu ? wave::readlane(fk, 62) : kKeyNaN;
+    const uint32_t wmax = wave::max_u32(cand ? fk : 0u);
     const uint32_t blo = tau_lo != 0xffffffffu ? wave::readlane(fk, 63) : kKeyNaN;
-    const uint64_t hword = overflow ? kPlOverflow : ((static_cast<uint64_t>(bhi) << 32) | blo);
+    const uint64_t hword = overflow ? kPlOverflow : ((static_cast<uint64_t>(wmax) << 32) | blo);
     const uint64_t eword = cand ? composite(fk, idx) : kPlFiller;
     const uint32_t lj_own = static_cast<uint32_t>(chunk) * 4u + static_cast<uint32_t>(wave);
     if (!merger) {
@@ -3031,6 +3020,8 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
     uint64_t* own_e = sh.list + 4;
     if (static_cast<uint32_t>(lane) < ne) own_e[static_cast<uint32_t>(wave) * ne + static_cast<uint32_t>(lane)] = eword;
     if (lane == 0) own_h[wave] = hword;
+    if (tid < 32) sh.hist[tid] = 0u;       // the merge's threshold histogram
+    if (tid == 0) sh.u32[kSegCount] = 0u;  // and its entry counter
     __syncthreads();
 
     // ---- Merge (the row's last chunk) ----
@@ -3083,45 +3074,46 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
         if (tid == 0) store_shared(prow_base + kPollEpochWord, static_cast<uint64_t>(epoch + 1u));
     };
 
-    // 8. The row's bounds per level (every wave reduces the headers it
-    //    holds), the entries above each, and the largest final key.
-    const uint32_t bnd_hi = wave::max_u32(static_cast<uint32_t>(h >> 32));
-    const uint32_t bnd_lo = wave::max_u32(static_cast<uint32_t>(h));
-    uint32_t c_hi = 0u, c_lo = 0u, kmx = 0u;
+    // 8. The row's bound B (the largest capped bound) and largest final key
+    //    kmax, from the headers every wave holds. The entries above B go to
+    //    a 32-bin histogram of (kmax - key) >> sh: bins 0..j hold exactly the
+    //    entries above kmax - (j + 1) << sh, so the first bin whose running
+    //    count reaches k sets the smallest certified threshold on this grid
+    //    (any threshold at or above B is valid), and only about k entries
+    //    are ranked instead of every entry above B.
+    const uint32_t bnd = wave::max_u32(static_cast<uint32_t>(h));
+    const uint32_t kmax = wave::max_u32(static_cast<uint32_t>(h >> 32));
+    const uint32_t span = kmax > bnd ? kmax - bnd - 1u : 0u;
+    const int bsh = max(32 - __clz(static_cast<int>(span)) - 5, 0);
 #pragma unroll
     for (uint32_t i = 0; i < kPlPer; ++i) {
-        const uint32_t ky = ev[i] ? static_cast<uint32_t>(e[i] >> 32) : 0u;
-        c_hi += ky > bnd_hi ? 1u : 0u;
-        c_lo += ky > bnd_lo ? 1u : 0u;
-        kmx = max(kmx, ky);
+        const uint32_t ky = static_cast<uint32_t>(e[i] >> 32);
+        if (ev[i] && ky > bnd) atomicAdd(&sh.hist[(kmax - ky) >> bsh], 1u);
     }
-    const uint32_t s_hi = wave::incl_add(c_hi), s_lo = wave::incl_add(c_lo);
-    const uint32_t w_kmx = wave::max_u32(kmx);
-    if (lane == 63) {
-        sh.u32[8 + wave] = s_hi;
-        sh.u32[12 + wave] = s_lo;
-    }
-    if (lane == 0) sh.u32[28 + wave] = w_kmx;
     __syncthreads();
-    uint32_t n_hi = 0u, n_lo = 0u, b_hi = 0u, b_lo = 0u;
+    const uint32_t hb = lane < 32 ? sh.hist[lane] : 0u;
+    const uint32_t cum = wave::incl_add(hb);
+    const uint64_t reach = __ballot(lane < 32 && cum >= k);
+    const int jsel = reach ? __ffsll(static_cast<unsigned long long>(reach)) - 1 : 32;
+    const uint32_t n = reach ? wave::readlane(cum, jsel) : 0u;
+    if (!timed_out && kmax > bnd && n >= k && n <= static_cast<uint32_t>(kBlock)) {
+        // 9. The selected entries into stage[0, n): per-thread counts, a
+        //    wave scan, one LDS counter per wave.
+        uint32_t c = 0u;
+        bool sel[kPlPer];
 #pragma unroll
-    for (int w = 0; w < kBlock / 64; ++w) {
-        b_hi += w < wave ? sh.u32[8 + w] : 0u;
-        b_lo += w < wave ? sh.u32[12 + w] : 0u;
-        n_hi += sh.u32[8 + w];
-        n_lo += sh.u32[12 + w];
-    }
-    const uint32_t kmax = max(max(sh.u32[28], sh.u32[29]), max(sh.u32[30], sh.u32[31]));
-    const bool use_hi = n_hi >= k && n_hi <= static_cast<uint32_t>(kBlock);
-    const uint32_t n = use_hi ? n_hi : n_lo;
-    if (!timed_out && n >= k && n <= static_cast<uint32_t>(kBlock)) {
-        // 9. The entries above the chosen bound into stage[0, n), each at its
-        //    wave's base plus its lanes' prefix.
-        const uint32_t bnd = use_hi ? bnd_hi : bnd_lo;
-        uint32_t pos = (use_hi ? b_hi + s_hi - c_hi : b_lo + s_lo - c_lo);
+        for (uint32_t i = 0; i < kPlPer; ++i) {
+            const uint32_t ky = static_cast<uint32_t>(e[i] >> 32);
+            sel[i] = ev[i] && ky > bnd && ((kmax - ky) >> bsh) <= static_cast<uint32_t>(jsel);
+            c += sel[i] ? 1u : 0u;
+        }
+        const uint32_t incl = wave::incl_add(c);
+        uint32_t base = 0u;
+        if (lane == 63 && incl != 0u) base = atomicAdd(&sh.u32[kSegCount], incl);
+        uint32_t pos = wave::readlane(base, 63) + incl - c;
 #pragma unroll
         for (uint32_t i = 0; i < kPlPer; ++i)
-            if (ev[i] && static_cast<uint32_t>(e[i] >> 32) > bnd) sh.stage[pos++] = e[i];
+            if (sel[i]) sh.stage[pos++] = e[i];
         __syncthreads();
         // 10. Rank by counting; the top k and their expf terms by rank.
         const float maximum = key_value(kmax);
