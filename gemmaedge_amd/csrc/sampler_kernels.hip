@@ -158,8 +158,10 @@ __device__ __forceinline__ int lsb_exponent(float e) {
     const uint32_t b = f2u(e);
     const uint32_t ex = b >> 23;
     const uint32_t man = b & 0x7fffffu;
-    if (ex == 0) return -149 + __builtin_ctz(man);
-    return static_cast<int>(ex) - 150 + __builtin_ctz(man | 0x800000u);
+    // Subnormals (ex == 0) count as exponent 1 without the implicit bit:
+    // selects, no branch.
+    const uint32_t m = ex ? (man | 0x800000u) : man;
+    return static_cast<int>(ex ? ex : 1u) - 150 + __builtin_ctz(m);
 }
 
 // Largest list a chunk publishes (the top-m by raw value; m may exceed k by
@@ -1537,12 +1539,14 @@ __device__ __forceinline__ void scan_and_walk_fast(P&& seg_prob, const float* pr
 // generation.cpp:103-126 for at most 64 probabilities in one wave's
 // registers (lane j holds p_j, j < keff; none NaN, so they are
 // non-increasing). The sequential fp32 sums are fully unrolled in blocks of
-// 16 steps: every lane runs the same chain with p_j broadcast from lane j
-// (v_readlane, off the add chain), lane j keeps the sum after step j, and one
-// ballot per block finds the stop, with no replay and no per-step branch. The
-// double boundary sums come from a wave prefix sum when it is exact (every
-// term a multiple of 2^-52; the partial sums are below 2), else from a
-// sequential replay.
+// 16 steps: every lane runs the same chain with p_j broadcast from LDS, lane
+// j keeps the sum after step j, and one ballot per block finds the stop, with
+// no replay and no per-step branch. The draw's walk runs over the same LDS
+// copy (the min-p-masked values; it never looks past keep - 1, so the
+// entries past keep need no masking) and reuses block 0's broadcast. The
+// double boundary sums come from a wave prefix sum of the same values when it
+// is exact (every term a multiple of 2^-52; the partial sums are below 2),
+// else from a sequential replay; both are independent of the chains.
 __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge_sample_params& p, float u,
                                                float* lds, uint32_t& pos_out, bool& near_out) {
     const int lane = __lane_id();
@@ -1557,15 +1561,25 @@ __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge
     // top-p: the first j in [1, limit) with cum_j >= top_p. Entries past the
     // limit add exact zeros.
     const float pl = lane < static_cast<int>(limit) ? pr : 0.0f;
-    lds[lane] = pl;  // lds[64, 128): the draw's copy
-    lds[64 + lane] = 0.0f;
+    lds[lane] = pl;
+    // Boundary sums (positions up to pos < keep <= limit only): exact wave
+    // prefix when every term of the limit's prefix is a multiple of 2^-52;
+    // computed in the shadow of block 0's LDS read.
+    bool incl_exact = false;
+    double incl = 0.0;
     float cum = 0.0f, mass = 0.0f, cl = 0.0f;
     uint32_t keep = limit;
     bool stopped = false;
+    F16 q0;
     static_for<0, 4>([&](auto B) {
         constexpr int b = decltype(B)::value * 16;
         if (stopped || static_cast<uint32_t>(b) >= limit) return;
         const F16 q = lds16(lds + b);
+        if constexpr (b == 0) {
+            q0 = q;
+            incl_exact = wave_min_i(pl > 0.0f ? lsb_exponent(pl) : INT_MAX) >= -52;
+            incl = wave_incl_f64(static_cast<double>(pl));
+        }
         static_for<0, 16>([&](auto J) {
             constexpr int j = b + decltype(J)::value;
             cum = cum + q.v[decltype(J)::value];
@@ -1584,27 +1598,15 @@ __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge
     // Draw: uniform_real_distribution(0, mass), then the subtract walk; the
     // fall-through returns entry keep - 1 (generation.cpp:126).
     const float choice0 = u * mass + 0.0f;
-    lds[64 + lane] = lane < static_cast<int>(keep) ? pr : 0.0f;
     float choice = choice0, chl = 0.0f;
     uint32_t pos = keep - 1u;
     bool found = false;
-    // Boundary sums for the near flag, c_at = sum_{i <= pos} (double)p_i in
-    // order and c_before up to pos - 1: an inclusive double scan over the kept
-    // entries is exact (any order gives the sequential sum) when every kept
-    // p_i is a multiple of 2^-52, their total being below 2. It does not
-    // depend on pos, so it runs inside the walk's first block, in the shadow
-    // of that block's LDS read; the sequential sum is the fallback.
-    const float pk = lane < static_cast<int>(keep) ? pr : 0.0f;
-    double incl = 0.0;
-    bool incl_exact = false;
     static_for<0, 4>([&](auto B) {
         constexpr int b = decltype(B)::value * 16;
         if (found || static_cast<uint32_t>(b) >= keep) return;
-        const F16 q = lds16(lds + 64 + b);
-        if constexpr (b == 0) {
-            incl_exact = wave_min_i(pk > 0.0f ? lsb_exponent(pk) : INT_MAX) >= -52;
-            incl = wave_incl_f64(static_cast<double>(pk));
-        }
+        F16 q;
+        if constexpr (b == 0) q = q0;
+        else q = lds16(lds + b);
         static_for<0, 16>([&](auto J) {
             constexpr int j = b + decltype(J)::value;
             choice = choice - q.v[decltype(J)::value];
@@ -1624,7 +1626,7 @@ __device__ __forceinline__ void scan_walk_wave(float pr, uint32_t keff, const ge
         double dc = 0.0;
         for (uint32_t i = 0; i <= pos; ++i) {
             c_before = dc;
-            dc = dc + static_cast<double>(readlane_f(pk, static_cast<int>(i)));
+            dc = dc + static_cast<double>(readlane_f(pl, static_cast<int>(i)));
         }
         c_at = dc;
     }
@@ -2324,7 +2326,7 @@ __device__ __forceinline__ bool merge_lean(const DevArgs& a, SelShared& sh, cons
     }
     const float inv_denom = static_cast<float>(1.0 / den);
     const float pr = e * inv_denom;
-    float* scratch = ex + 64;  // 128 floats for the sequential chains
+    float* scratch = ex + 64;  // 64 floats for the sequential chains
     uint32_t pos;
     bool near;
     if (!__any(live && __builtin_isnan(pr))) {
@@ -2939,10 +2941,16 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
     const bool merger = chunk == a.cpr - 1;
 
     // 4. Stage this wave's candidates: lane l keeps its c-th at seg[64 c + l]
-    //    (c < kPlCand), then they move to cmp[0, n_w) in (c, lane) order.
+    //    (c < kPlCand), then they move to cmp[0, n_w) in (c, lane) order. A
+    //    group of 4 slots is examined only when some lane's group maximum
+    //    reaches the bound; inside, every slot's word is written, to the
+    //    lane's next candidate position or to its own dummy word: no branch
+    //    per slot.
     const float floor_v = tlo ? key_value(tau_lo) : -INFINITY;
     uint64_t* seg = sh.stage + wave * kSeg;
-    uint64_t* cmp = seg + kPlCand * 64;
+    uint64_t* cmp = seg + kPlCand * 64;            // compacted candidates (at most kPlMaxEntries)
+    constexpr uint32_t kDummy = kSeg - 64;          // per-lane dummy words
+    static_assert(kPlCand * 64 + kPlMaxEntries <= kDummy, "staging layout");
     const uint32_t ebase = static_cast<uint32_t>(c0 + tid * W);
     uint32_t cnt = 0;
 #pragma unroll
@@ -2952,11 +2960,12 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
         for (int j = 0; j < 4; ++j) {
             const int s = 4 * g + j;
             const float x = value(s);
-            if (x >= floor_v) {
-                const uint32_t e = ebase + static_cast<uint32_t>((s / W) * kBlock * W + s % W);
-                if (cnt < kPlCand) seg[64u * cnt + static_cast<uint32_t>(lane)] = (static_cast<uint64_t>(f2u(x)) << 32) | e;
-                ++cnt;
-            }
+            const bool c = x >= floor_v;
+            const uint32_t e = ebase + static_cast<uint32_t>((s / W) * kBlock * W + s % W);
+            const uint32_t slot = (c && cnt < kPlCand) ? 64u * cnt + static_cast<uint32_t>(lane)
+                                                       : kDummy + static_cast<uint32_t>(lane);
+            seg[slot] = (static_cast<uint64_t>(f2u(x)) << 32) | e;
+            cnt += c ? 1u : 0u;
         }
     }
     const uint64_t m0 = __ballot(cnt > 0u), m1 = __ballot(cnt > 1u), m2 = __ballot(cnt > 2u), m3 = __ballot(cnt > 3u);
@@ -2964,7 +2973,7 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
     const uint32_t p2 = static_cast<uint32_t>(__popcll(m2)), p3 = static_cast<uint32_t>(__popcll(m3));
     const uint32_t n_w = p0 + p1 + p2 + p3;
     const bool overflow = __ballot(cnt > kPlCand) != 0ull || n_w > ne;
-    {
+    if (!overflow) {
         uint64_t y0 = 0, y1 = 0, y2 = 0, y3 = 0;
         if (cnt > 0u) y0 = seg[lane];
         if (cnt > 1u) y1 = seg[64 + lane];
@@ -3115,7 +3124,13 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
         for (uint32_t i = 0; i < kPlPer; ++i)
             if (sel[i]) sh.stage[pos++] = e[i];
         __syncthreads();
-        // 10. Rank by counting; the top k and their expf terms by rank.
+        // 10. Rank by counting; the top k and their expf terms by rank. Up to
+        //     64 entries: wave 0 alone (one entry per lane), no barrier.
+        const bool one_wave = n <= 64u;
+        if (one_wave && wave != 0) {
+            bump_epoch();
+            return;
+        }
         const float maximum = key_value(kmax);
         const float inv_temp = 1.0f / p.temperature;
         float* ex = reinterpret_cast<float*>(sh.list);
@@ -3155,10 +3170,14 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
                 ex[rk] = t;
             }
         }
-        __syncthreads();
-        if (wave != 0) {
-            bump_epoch();
-            return;
+        if (one_wave) {
+            wave_lds_sync();
+        } else {
+            __syncthreads();
+            if (wave != 0) {
+                bump_epoch();
+                return;
+            }
         }
         // 11. generation.cpp:89-126 over the k terms (wave 0).
         const bool live = static_cast<uint32_t>(lane) < k;
@@ -3179,7 +3198,7 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
         }
         const float inv_denom = static_cast<float>(1.0 / den);
         const float pr = et * inv_denom;
-        float* scratch = ex + 64;  // 128 floats for the sequential chains
+        float* scratch = ex + 64;  // 64 floats for the sequential chains
         uint32_t wpos;
         bool near;
         if (!__any(live && __builtin_isnan(pr))) {
