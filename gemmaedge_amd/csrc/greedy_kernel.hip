@@ -74,7 +74,12 @@ __device__ __forceinline__ uint32_t pick_word(const uint32_t (&d)[N], uint32_t i
 // (vocabularies below 2^24; the largest word is still the best key) and a
 // tag: 0x80 | the call epoch's low 7 bits (zero-filled words carry none). A
 // chunk with no candidate (key 0) publishes the tag alone.
-constexpr uint32_t kPollSpins = 1u << 22;  // about 4 s of polling: never reached with every chunk resident
+// The poll is bounded: about 4 s, never reached with every chunk resident
+// (they wait for nothing); a wait that runs out gives token -1 with
+// GE_FLAG_TIMEOUT. A word stored after that (a chunk stalled for seconds)
+// is left in place; its tag makes a later call ignore it until the 7-bit
+// epoch wraps (128 calls on the row).
+constexpr uint32_t kPollSpins = 1u << 22;
 __device__ __forceinline__ uint64_t poll_word(uint64_t b, uint32_t tag) {
     if (b == 0ull) return tag;
     const uint32_t idx = composite_index(b);
@@ -263,13 +268,14 @@ __global__ __launch_bounds__(kBlock) void greedy_kernel(DevArgs a) {
 
     // The NaN rule and the outputs (one lane of the row's last chunk):
     // std::max_element (generation.cpp:66-70) keeps index 0 when its final
-    // value is NaN (NaN < x is false): token 0's final value is NaN iff its
-    // raw value is, unless the penalty is NaN and 0 is penalised. softcap(x)
-    // is NaN iff x is, except c * tanhf(inf / c) with c = inf.
+    // value is NaN (NaN < x is false): its capped value is NaN, or 0 is in
+    // the history and the penalty makes it NaN (a NaN penalty, -inf * 0,
+    // 0 * inf, inf / inf).
     auto finish = [&](uint64_t b) {
         int32_t token = static_cast<int32_t>(composite_index(b));
-        bool nan0 = __builtin_isnan(x0) || (__builtin_isinf(x0) && __builtin_isnan(softcap(x0, cap)));
-        if (!nan0 && pen && __builtin_isnan(r))
+        const float f0 = softcap(x0, cap);
+        bool nan0 = __builtin_isnan(f0);
+        if (!nan0 && pen && __builtin_isnan(penalize(f0, r)))
             for (int j = 0; j < H && !nan0; ++j) nan0 = hist[j] == 0;
         if (nan0) token = 0;
         emit_row(a, row, token, 1.0f, 0);
@@ -305,11 +311,12 @@ __global__ __launch_bounds__(kBlock) void greedy_kernel(DevArgs a) {
         }
         // Clear the words (zero carries no tag): a later call whose chunks
         // outnumber this one's never reads a word left from an older call.
+        // After a wait that ran out, every word of the row is cleared.
         uint64_t wb = 0ull;
 #pragma unroll
         for (int j = 0; j < kWpc; ++j) {
             const int q = j * 64 + lane;
-            if (q < nw) __hip_atomic_store(&pw[q], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (q < nw || !all) __hip_atomic_store(&pw[q], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             wb = max64(wb, w[j]);
         }
         const uint64_t rbest = wave_max_u64(wb);
@@ -317,7 +324,7 @@ __global__ __launch_bounds__(kBlock) void greedy_kernel(DevArgs a) {
             __hip_atomic_store(&pw[kPollWords], static_cast<uint64_t>(epoch + 1u), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
             if (all) finish(poll_composite(rbest));
-            else emit_row(a, row, -1, 0.0f, GE_FLAG_UNSUPPORTED);  // a chunk never ran: no token
+            else emit_row(a, row, -1, 0.0f, GE_FLAG_TIMEOUT);  // a chunk's word never came: no token
         }
         return;
     }

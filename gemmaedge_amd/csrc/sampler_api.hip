@@ -330,11 +330,13 @@ __global__ void clear_words(uint32_t* p, int n) {
 
 // The array's address on `device` (current), found once per device; its
 // ticket area is cleared on `stream` the first time (a kernel, not a memset).
+// The device's gfx950 check is made at that first call too, not per call.
 int scratch_on(int device, hipStream_t stream, void** out) {
     static std::mutex mu;
     static void* ptr[kMaxDevices] = {};
     std::lock_guard<std::mutex> lock(mu);
     if (!ptr[device]) {
+        if (!device_is_gfx950(device)) return fail(GE_ERR_NO_DEVICE, "device %d is not gfx950", device);
         void* p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
@@ -389,7 +391,6 @@ int ge_sample_noalloc(void* stream, const ge_sample_args* args) {
     int device = -1;
     if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices)
         return fail(GE_ERR_NO_DEVICE, "no current device");
-    if (!device_is_gfx950(device)) return fail(GE_ERR_NO_DEVICE, "device %d is not gfx950", device);
     void* p = nullptr;
     const int rc = scratch_on(device, static_cast<hipStream_t>(stream), &p);
     if (rc != GE_OK) return rc;

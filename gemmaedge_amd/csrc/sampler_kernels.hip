@@ -2058,12 +2058,13 @@ __device__ __forceinline__ void merge_finish(const DevArgs& a, SelShared& sh, co
     if (greedy) {
         if (tid == 0) {
             // std::max_element (generation.cpp:66-70) keeps index 0 when its
-            // value is NaN (NaN < x is false). Token 0's final value is NaN
-            // iff its raw value is, unless the penalty itself is NaN and 0
-            // is in the history.
+            // final value is NaN (NaN < x is false): its capped value is NaN,
+            // or 0 is in the history and the penalty makes it NaN (a NaN
+            // penalty, -inf * 0, 0 * inf, inf / inf).
             int32_t token = static_cast<int32_t>(composite_index(top[0]));
-            bool nan0 = __builtin_isnan(softcap(x0, rc.cap));
-            if (!nan0 && rc.pen && __builtin_isnan(rc.r))
+            const float f0 = softcap(x0, rc.cap);
+            bool nan0 = __builtin_isnan(f0);
+            if (!nan0 && rc.pen && __builtin_isnan(penalize(f0, rc.r)))
                 for (int j = 0; j < rc.H && !nan0; ++j) nan0 = rc.hist[j] == 0;
             if (nan0) token = 0;
             write_row(a, row, token, 1.0f, 0);

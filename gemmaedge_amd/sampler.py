@@ -37,6 +37,7 @@ GE_FLAG_NEAR_BOUNDARY = 1
 GE_FLAG_UNSUPPORTED = 2
 GE_FLAG_STOP = 4
 GE_FLAG_DONE = 8
+GE_FLAG_TIMEOUT = 16
 
 GE_STOP_AFTER_PUSH = 0   # Gemma4Session::generate (src/generation.cpp:461-465)
 GE_STOP_BEFORE_PUSH = 1  # CLI decode loop (src/main.cpp:140-143)

@@ -20,8 +20,9 @@
 //   GEMMAEDGE_SOFTCAP              float   SamplingExtras::softcap (normally the model's value)
 //   GEMMAEDGE_REPETITION_PENALTY   float   SamplingExtras::repetition_penalty
 // A value must parse completely (leading and trailing spaces allowed); a
-// float is decimal and finite as a float, an integer has no sign and fits
-// its field.
+// float is decimal and finite as a float (a decimal below the float range
+// gives its rounded subnormal or zero, as a cast of the decimal would), an
+// integer has no sign and fits its field.
 #pragma once
 
 #include <cerrno>
@@ -47,9 +48,10 @@ inline bool parse_float(const char* name, float& out) {
     for (const char* q = v; *q; ++q)
         if (*q == 'x' || *q == 'X') return false;  // decimal only (strtof also reads hex)
     char* end = nullptr;
-    errno = 0;
+    // strtof sets ERANGE on underflow too; only a non-finite result (overflow)
+    // is rejected, so an underflowing value is taken as its rounded value.
     const float x = std::strtof(v, &end);
-    if (end == v || errno == ERANGE || !std::isfinite(x)) return false;
+    if (end == v || !std::isfinite(x)) return false;
     if (*skip_space(end) != '\0') return false;
     out = x;
     return true;

@@ -107,15 +107,23 @@ void ge_oracle_expf_bits(uint32_t lo, size_t n, uint32_t* out) {
     }
 }
 
-void ge_oracle_transform_row(const void* logits, int dtype, size_t vocab,
-                             const int32_t* history, size_t history_len,
-                             const ge_oracle_params* p, float* out) {
+}  // extern "C"
+
+namespace {
+
+// Softcap + penalty stage for one row; the softcap loop runs on sc_threads
+// OpenMP threads, as the reference's does (`#pragma omp parallel for`,
+// src/generation.cpp:433; elementwise, so the values do not depend on it).
+void transform_row(const void* logits, int dtype, size_t vocab, const int32_t* history, size_t history_len,
+                   const ge_oracle_params* p, float* out, int sc_threads) {
     for (size_t i = 0; i < vocab; ++i) out[i] = load_logit(logits, dtype, i);
     // src/generation.cpp:431-437: logits[i] = softcap * tanh(logits[i] / softcap)
     // when final_logit_softcap > 0 (f32 division, glibc tanhf, f32 multiply).
     if (p->softcap > 0.0f) {
         const float softcap = p->softcap;
-        for (size_t i = 0; i < vocab; ++i) out[i] = softcap * std::tanh(out[i] / softcap);
+        const std::ptrdiff_t n = static_cast<std::ptrdiff_t>(vocab);
+#pragma omp parallel for num_threads(sc_threads) schedule(static) if (sc_threads > 1)
+        for (std::ptrdiff_t i = 0; i < n; ++i) out[i] = softcap * std::tanh(out[i] / softcap);
     }
     // Repetition penalty (absent in the reference; CTRL rule, Keskar et al. 2019):
     // each UNIQUE history id t in [0, vocab) gets v > 0 ? v / r : v * r, once.
@@ -131,6 +139,16 @@ void ge_oracle_transform_row(const void* logits, int dtype, size_t vocab,
             out[t] = v > 0.0f ? v / r : v * r;
         }
     }
+}
+
+}  // namespace
+
+extern "C" {
+
+void ge_oracle_transform_row(const void* logits, int dtype, size_t vocab,
+                             const int32_t* history, size_t history_len,
+                             const ge_oracle_params* p, float* out) {
+    transform_row(logits, dtype, vocab, history, history_len, p, out, 1);
 }
 
 // src/generation.cpp:60-127 with the total order above.
@@ -231,9 +249,12 @@ int ge_oracle_run(const void* logits, int dtype, int rows, size_t vocab, size_t 
                   ge_oracle_result* results, int nthreads) {
     if (vocab == 0 || rows < 0) return -1;
     const size_t esize = dtype == GE_ORACLE_BF16 ? 2 : 4;
-    unsigned nt = nthreads > 0 ? static_cast<unsigned>(nthreads)
-                               : std::max(1u, std::thread::hardware_concurrency());
-    nt = std::min<unsigned>(nt, static_cast<unsigned>(std::max(rows, 1)));
+    const unsigned want = nthreads > 0 ? static_cast<unsigned>(nthreads)
+                                       : std::max(1u, std::thread::hardware_concurrency());
+    const unsigned nt = std::min<unsigned>(want, static_cast<unsigned>(std::max(rows, 1)));
+    // Threads left over when rows are fewer than threads run each row's
+    // softcap loop (a single row: all of them, as in the reference).
+    const int sc_threads = static_cast<int>(std::max(1u, want / nt));
     auto work = [&](unsigned tid) {
         std::vector<float> final_values(vocab);
         for (int row = static_cast<int>(tid); row < rows; row += static_cast<int>(nt)) {
@@ -245,7 +266,7 @@ int ge_oracle_run(const void* logits, int dtype, int rows, size_t vocab, size_t 
                 h = history + history_offsets[row];
                 hl = static_cast<size_t>(history_offsets[row + 1] - history_offsets[row]);
             }
-            ge_oracle_transform_row(base, dtype, vocab, h, hl, p, final_values.data());
+            transform_row(base, dtype, vocab, h, hl, p, final_values.data(), sc_threads);
             ge_oracle_result r;
             ge_oracle_sample_final(final_values.data(), vocab, p, uniforms ? uniforms[row] : 0.0f, &r);
             if (tokens) tokens[row] = r.token;

@@ -254,6 +254,14 @@ void check_env() {
     }
     setenv("GEMMAEDGE_TOP_K", "0", 1);
     expect(gemmaedge::sampling_config_from_env(d).top_k == 0u, "env: top_k 0 (disabled) taken");
+    // Below the float range: the rounded subnormal or signed zero (the same
+    // cases as tests/test_config_env.py).
+    const struct { const char* text; float want; } under[] = {{"1e-40", 1e-40f}, {"1e-50", 0.0f}, {"-1e-46", -0.0f}};
+    for (const auto& u : under) {
+        setenv("GEMMAEDGE_MIN_P", u.text, 1);
+        const float got = gemmaedge::sampling_config_from_env(d).min_p;
+        expect(as_bits(got) == as_bits(u.want), "env: underflow takes the rounded value");
+    }
     for (const char* n : names) unsetenv(n);
 }
 

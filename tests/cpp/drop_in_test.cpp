@@ -14,10 +14,21 @@
 // (prompt + generated ids) passed to the penalty overload, and the reference's
 // stop tokens {1, 106} (include/gemmaedge/generation.h:66).
 //
+// The env mode reads the whole configuration through
+// include/gemmaedge/sampling_env.h (GEMMAEDGE_* variables) and samples the
+// rows as the stream mode does. The bench mode times sample_token as the
+// reference's decode loop calls it (a host std::vector in, a token out:
+// src/generation.cpp:460), once with the three-argument signature on
+// pre-capped logits and once with the penalty overload (softcap 30, penalty
+// 1.1 over a history), and prints per-call wall-clock p50 / p99 / mean.
+//
 //   drop_in_test                                  (known answers only)
 //   drop_in_test ROWS.bin ROWS VOCAB T K P MINP SEED [SOFTCAP PENALTY HIST.bin H]
 //   drop_in_test generate ROWS.bin ROWS VOCAB SEED PROMPT.bin NPROMPT T0,T1,... lib|cli
+//   drop_in_test env ROWS.bin ROWS VOCAB [HIST.bin H]
+//   drop_in_test bench ROWS.bin ROWS VOCAB CALLS HIST.bin H
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <fstream>
@@ -28,6 +39,7 @@
 #include <vector>
 
 #include "gemmaedge/sampling.h"
+#include "gemmaedge/sampling_env.h"
 
 namespace {
 
@@ -101,12 +113,87 @@ std::vector<gemmaedge::TokenId> generate_loop(const float* rows_f, std::size_t r
     return generated;
 }
 
+// Per-call wall-clock microseconds of `calls` sample_token calls over the
+// rows in turn (one engine across them), after 20 untimed calls.
+template <typename Call>
+void time_calls(const char* name, const float* rows_f, std::size_t rows, std::size_t vocab, std::size_t calls,
+                Call&& call) {
+    std::vector<float> row(vocab);
+    std::vector<double> us;
+    us.reserve(calls);
+    for (std::size_t i = 0; i < calls + 20; ++i) {
+        row.assign(rows_f + (i % rows) * vocab, rows_f + (i % rows + 1) * vocab);
+        const auto t0 = std::chrono::steady_clock::now();
+        const gemmaedge::TokenId t = call(row, i % rows);
+        const auto t1 = std::chrono::steady_clock::now();
+        require(t >= 0, "negative token");
+        if (i >= 20) us.push_back(std::chrono::duration<double, std::micro>(t1 - t0).count());
+    }
+    std::sort(us.begin(), us.end());
+    double mean = 0.0;
+    for (double v : us) mean += v;
+    mean /= static_cast<double>(us.size());
+    std::printf("%s p50_us=%.2f p99_us=%.2f mean_us=%.2f calls=%zu\n", name, us[us.size() / 2],
+                us[std::min(us.size() - 1, us.size() * 99 / 100)], mean, us.size());
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     try {
         test_sampling();
-        if (argc >= 2 && std::string(argv[1]) == "generate") {
+        if (argc >= 2 && std::string(argv[1]) == "env") {
+            require(argc == 5 || argc == 7, "env ROWS.bin ROWS VOCAB [HIST.bin H]");
+            const auto data = read_file(argv[2]);
+            const std::size_t rows = std::stoul(argv[3]);
+            const std::size_t vocab = std::stoul(argv[4]);
+            require(data.size() == rows * vocab * sizeof(float), "row file size mismatch");
+            const gemmaedge::SamplingConfig config = gemmaedge::sampling_config_from_env(gemmaedge::SamplingConfig{});
+            const gemmaedge::SamplingExtras extras = gemmaedge::sampling_extras_from_env(gemmaedge::SamplingExtras{});
+            std::vector<gemmaedge::TokenId> history;
+            std::size_t hl = 0;
+            if (argc == 7) {
+                const auto h = read_file(argv[5]);
+                hl = std::stoul(argv[6]);
+                require(h.size() == rows * hl * sizeof(std::int32_t), "history file size mismatch");
+                history.resize(rows * hl);
+                std::copy(h.begin(), h.end(), reinterpret_cast<char*>(history.data()));
+            }
+            const float* rows_f = reinterpret_cast<const float*>(data.data());
+            std::mt19937_64 random(config.seed);
+            std::vector<float> row(vocab);
+            for (std::size_t r = 0; r < rows; ++r) {
+                row.assign(rows_f + r * vocab, rows_f + (r + 1) * vocab);
+                std::printf("%d\n", gemmaedge::sample_token(row, config, random, hl ? history.data() + r * hl : nullptr,
+                                                             hl, extras));
+            }
+        } else if (argc >= 2 && std::string(argv[1]) == "bench") {
+            require(argc == 8, "bench ROWS.bin ROWS VOCAB CALLS HIST.bin H");
+            const auto data = read_file(argv[2]);
+            const std::size_t rows = std::stoul(argv[3]);
+            const std::size_t vocab = std::stoul(argv[4]);
+            const std::size_t calls = std::stoul(argv[5]);
+            require(rows > 0 && data.size() == rows * vocab * sizeof(float), "row file size mismatch");
+            const auto h = read_file(argv[6]);
+            const std::size_t hl = std::stoul(argv[7]);
+            require(h.size() == rows * hl * sizeof(std::int32_t), "history file size mismatch");
+            std::vector<gemmaedge::TokenId> history(rows * hl);
+            std::copy(h.begin(), h.end(), reinterpret_cast<char*>(history.data()));
+            const float* rows_f = reinterpret_cast<const float*>(data.data());
+            gemmaedge::SamplingConfig config;  // the reference defaults: T 1.0, top-k 64, top-p 0.95
+            std::mt19937_64 random(config.seed);
+            time_calls("reference_signature", rows_f, rows, vocab, calls,
+                       [&](const std::vector<float>& row, std::size_t) {
+                           return gemmaedge::sample_token(row, config, random);
+                       });
+            gemmaedge::SamplingExtras extras;
+            extras.softcap = 30.0f;
+            extras.repetition_penalty = 1.1f;
+            time_calls("penalty_overload", rows_f, rows, vocab, calls,
+                       [&](const std::vector<float>& row, std::size_t r) {
+                           return gemmaedge::sample_token(row, config, random, history.data() + r * hl, hl, extras);
+                       });
+        } else if (argc >= 2 && std::string(argv[1]) == "generate") {
             require(argc == 10, "generate ROWS.bin ROWS VOCAB SEED PROMPT.bin NPROMPT TEMPS lib|cli");
             const auto data = read_file(argv[2]);
             const std::size_t rows = std::stoul(argv[3]);

@@ -43,3 +43,12 @@ def test_malformed_integer_ignored(v):
 
 def test_top_k_zero_disables():
     assert SamplingConfig.from_env(environ={"GEMMAEDGE_TOP_K": "0"}).top_k == 0
+
+
+@pytest.mark.parametrize("v,want", [("1e-40", 1e-40), ("1e-50", 0.0), ("-1e-46", -0.0)])
+def test_underflow_takes_the_rounded_value(v, want):
+    # Below the float range: the rounded subnormal (or signed zero), the same
+    # value the C++ parser stores (asan_check.cpp checks the same cases).
+    import numpy as np
+    got = SamplingConfig.from_env(environ={"GEMMAEDGE_MIN_P": v}).min_p
+    assert np.float32(got).tobytes() == np.float32(want).tobytes()

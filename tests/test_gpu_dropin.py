@@ -102,3 +102,41 @@ def test_generate_loop_matches_oracle(tmp_path, mode):
         hist.append(tok)
     assert len(want) == stop_step + (1 if mode == "lib" else 0)
     assert got == want
+
+
+@pytest.mark.parametrize("env", [
+    {"GEMMAEDGE_TEMPERATURE": "0.7", "GEMMAEDGE_TOP_K": "40", "GEMMAEDGE_TOP_P": "0.9", "GEMMAEDGE_MIN_P": "0.02",
+     "GEMMAEDGE_SEED": "77", "GEMMAEDGE_SOFTCAP": "30", "GEMMAEDGE_REPETITION_PENALTY": "1.15"},
+    {"GEMMAEDGE_TEMPERATURE": " 0 ", "GEMMAEDGE_SOFTCAP": "30.0", "GEMMAEDGE_REPETITION_PENALTY": "1.3"},
+    {"GEMMAEDGE_TOP_K": "not-a-number", "GEMMAEDGE_SEED": "5", "GEMMAEDGE_TOP_P": "1e-50"},
+])
+def test_env_config_matches_oracle(tmp_path, env):
+    """The configuration surface (include/gemmaedge/sampling_env.h) driving
+    GPU samples: drop_in_test env reads every field through
+    sampling_config_from_env / sampling_extras_from_env (malformed values keep
+    the default, an underflowing decimal gives its finite value); the oracle
+    uses the same fields, parsed by SamplingConfig.from_env."""
+    from gemmaedge_amd import SamplingConfig
+
+    rng = np.random.default_rng(61)
+    rows, vocab, hl = 8, 262144, 64
+    x = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
+    hist = rng.integers(0, vocab, size=(rows, hl)).astype(np.int32)
+    x.tofile(tmp_path / "rows.bin")
+    hist.tofile(tmp_path / "hist.bin")
+    full = dict(os.environ)
+    for k in list(full):
+        if k.startswith("GEMMAEDGE_"):
+            del full[k]
+    full.update(env)
+    print("[dropin] env", env, flush=True)
+    r = subprocess.run([BIN, "env", str(tmp_path / "rows.bin"), str(rows), str(vocab), str(tmp_path / "hist.bin"),
+                        str(hl)], capture_output=True, text=True, timeout=120, env=full)
+    assert r.returncode == 0, r.stderr
+    got = [int(t) for t in r.stdout.split()]
+    cfg = SamplingConfig.from_env(SamplingConfig(softcap=0.0, repetition_penalty=1.0), environ=full)
+    u = W.mt_uniforms(cfg.seed, rows) if cfg.temperature > 0 else np.zeros(rows, np.float32)
+    ora = O.run(x, O.make_params(temperature=cfg.temperature, top_k=cfg.top_k, top_p=cfg.top_p, min_p=cfg.min_p,
+                                 softcap=cfg.softcap, repetition_penalty=cfg.repetition_penalty),
+                history=hist.reshape(-1), offsets=(np.arange(rows + 1) * hl).astype(np.int32), uniforms=u)
+    assert got == ora.tokens.tolist()

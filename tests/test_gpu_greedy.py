@@ -9,6 +9,8 @@ and chunks that hold several tokens of the winning tie class (rescanned)."""
 import numpy as np
 import pytest
 
+import ge_oracle as O
+
 from gemmaedge_amd import workloads as W
 from gpu_util import assert_parity, run_gpu, run_oracle, small_workload
 
@@ -90,6 +92,32 @@ def test_nan_rules(sampler):
                        history=np.array([0, 3], np.int32), offsets=np.array([0, 2], np.int32))
     gpu, _ = _check(sampler, w, "NaN penalty on token 0")
     assert gpu[0][0] == 0
+    # A finite penalty that still makes token 0's final value NaN: -inf * 0
+    # (r = 0), 0 * inf and inf / inf (r = inf), without a softcap; and a
+    # penalised token 0 whose value stays a number (0 stays 0 under r = 2).
+    for x0, r, nan in ((-np.inf, 0.0, True), (0.0, np.inf, True), (np.inf, np.inf, True), (0.0, 2.0, False)):
+        row = base.copy()
+        row[0] = x0
+        w = small_workload(f"nanpen-{x0}-{r}", row, dict(temperature=0.0, softcap=0.0, repetition_penalty=r),
+                           history=np.array([5, 0], np.int32), offsets=np.array([0, 2], np.int32))
+        gpu, _ = _check(sampler, w, f"token 0 = {x0}, penalty {r}")
+        assert (gpu[0][0] == 0) == nan
+    # The same rule through the selection kernel's k = 1 path (per-row
+    # parameters route greedy rows there).
+    import torch
+
+    from gemmaedge_amd import SamplingConfig
+    rows = np.stack([base.copy() for _ in range(2)])
+    rows[0, 0] = -np.inf
+    hist = np.array([0, 9, 0, 4], np.int32)
+    offs = np.array([0, 2, 4], np.int32)
+    cfgs = [SamplingConfig(temperature=0.0, softcap=0.0, repetition_penalty=0.0),
+            SamplingConfig(temperature=0.0, softcap=0.0, repetition_penalty=np.inf)]
+    tokens, _, _ = sampler.sample(torch.from_numpy(rows).cuda(), cfgs, uniforms=torch.zeros(2, device="cuda"),
+                                  history=torch.from_numpy(hist).cuda(), history_offsets=torch.from_numpy(offs).cuda())
+    params = [O.make_params(temperature=0.0, softcap=0.0, repetition_penalty=c.repetition_penalty) for c in cfgs]
+    ora = O.run(rows, params, history=hist, offsets=offs, uniforms=np.zeros(2, np.float32))
+    assert tokens.cpu().numpy().tolist() == ora.tokens.tolist()
 
 
 def test_batch_and_bf16(sampler):

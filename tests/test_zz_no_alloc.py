@@ -1,9 +1,14 @@
 """ge_sample_noalloc (the allocation-free entry point) against ge_sample, through
 the C ABI: two calls in a row on the same GPU, the second with a smaller input
 (fewer rows, another dtype and parameters), each compared bit for bit (tokens,
-probabilities, flags) with ge_sample on identical inputs; then the capacity
-errors. The entry point has no counterpart in the reference; its output must
-equal the handle path's, which the parity tests tie to the oracle."""
+probabilities, flags) with ge_sample on identical inputs; the same under HIP
+graph capture (one captured call replayed over new inputs, eager work between
+replays, every replay compared with ge_sample); greedy rows, which take the
+ticket path here (no polled words); per-row parameters with a row whose k is
+above 1024, which this entry point flags GE_FLAG_UNSUPPORTED while the other
+rows match; then the capacity errors. The entry point has no counterpart in
+the reference; its output must equal the handle path's, which the parity
+tests tie to the oracle."""
 import ctypes
 
 import numpy as np
@@ -14,7 +19,7 @@ from gemmaedge_amd import workloads as W
 pytestmark = pytest.mark.gpu
 
 
-def _args(S, w, logits, hist, offs, uni, outs):
+def _args(S, w, logits, hist, offs, uni, outs, row_params=None):
     a = S.SampleArgs()
     a.logits = logits.data_ptr()
     a.dtype = S.GE_DTYPE_BF16 if w.dtype == "bf16" else S.GE_DTYPE_F32
@@ -22,6 +27,8 @@ def _args(S, w, logits, hist, offs, uni, outs):
     a.params = S.SamplingConfig(**w.params).params()
     if hist is not None:
         a.history, a.history_offsets = hist.data_ptr(), offs.data_ptr()
+    if row_params is not None:
+        a.row_params = row_params.data_ptr()
     a.uniforms = uni.data_ptr()
     a.tokens_out, a.probs_out, a.flags_out = (t.data_ptr() for t in outs)
     return a
@@ -68,6 +75,108 @@ def test_noalloc_matches_handle_path_twice():
         np.testing.assert_array_equal(gt, rt)
         np.testing.assert_array_equal(gp, rp)
         np.testing.assert_array_equal(gf, rf)
+    s.close()
+
+
+def _compare(S, L, s, w, logits, hist, offs, uni, row_params=None, label=""):
+    """One ge_sample and one ge_sample_noalloc call on the same device inputs;
+    returns both outputs as (tokens, prob bits, flags)."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    ref_outs, got_outs = _outs(torch, w.rows), _outs(torch, w.rows)
+    ref = _args(S, w, logits, hist, offs, uni, ref_outs, row_params)
+    got = _args(S, w, logits, hist, offs, uni, got_outs, row_params)
+    print(f"[noalloc] {label or w.name} rows={w.rows} {w.dtype} {w.params}", flush=True)
+    assert s.sample_raw(ref, stream) == 0, S.last_error()
+    assert L.ge_sample_noalloc(ctypes.c_void_p(stream.cuda_stream), ctypes.byref(got)) == 0, S.last_error()
+    torch.cuda.synchronize()
+    return _bits(ref_outs), _bits(got_outs)
+
+
+def test_noalloc_under_graph_replay():
+    import torch
+
+    from gemmaedge_amd import sampler as S
+
+    L = S.load_library()
+    steps = [W.c2(seed=40 + i) for i in range(4)]  # one shape, new logits, histories and uniforms
+    s = S.Sampler(max_rows=64, max_vocab=W.VOCAB, max_history=2048)
+    logits, hist, offs, uni = W.to_device(steps[0])
+    outs = _outs(torch, steps[0].rows)
+    a = _args(S, steps[0], logits, hist, offs, uni, outs)
+    cur = torch.cuda.current_stream()
+    # An eager call first: the array's address is looked up outside the capture.
+    assert L.ge_sample_noalloc(ctypes.c_void_p(cur.cuda_stream), ctypes.byref(a)) == 0, S.last_error()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(cur)
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            rc = L.ge_sample_noalloc(ctypes.c_void_p(side.cuda_stream), ctypes.byref(a))
+    assert rc == 0, S.last_error()
+    torch.cuda.synchronize()
+    for i, w in enumerate(steps):
+        print(f"[noalloc] graph replay {i}: {w.name} seed={w.seed}", flush=True)
+        for dst, src in zip((logits, hist, offs, uni), W.to_device(w)):
+            dst.copy_(src)
+        outs[0].fill_(-7)
+        outs[1].zero_()
+        outs[2].fill_(-7)
+        g.replay()
+        _ = (logits * 2.0).sum()  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        got = _bits(outs)
+        ref_outs = _outs(torch, w.rows)
+        assert s.sample_raw(_args(S, w, logits, hist, offs, uni, ref_outs), cur) == 0, S.last_error()
+        torch.cuda.synchronize()
+        ref = _bits(ref_outs)
+        assert (ref[0] >= 0).all()
+        for r, x in zip(ref, got):
+            np.testing.assert_array_equal(x, r, err_msg=f"replay {i}")
+    s.close()
+
+
+def test_noalloc_greedy_rows():
+    from gemmaedge_amd import sampler as S
+
+    L = S.load_library()
+    s = S.Sampler(max_rows=64, max_vocab=W.VOCAB, max_history=2048)
+    cases = [W.c1(greedy=True)]
+    for rows in (3, 16):
+        w = W.c2(seed=60 + rows, rows=rows)
+        w.params = dict(w.params, temperature=0.0)
+        w.name = f"C2-greedy-rows{rows}"
+        cases.append(w)
+    for w in cases:
+        ref, got = _compare(S, L, s, w, *W.to_device(w))
+        assert (ref[0] >= 0).all()
+        for r, x in zip(ref, got):
+            np.testing.assert_array_equal(x, r, err_msg=w.name)
+    s.close()
+
+
+def test_noalloc_row_params_flags_large_k():
+    import torch
+
+    from gemmaedge_amd import sampler as S
+
+    L = S.load_library()
+    s = S.Sampler(max_rows=64, max_vocab=W.VOCAB, max_history=2048)
+    w = W.c2(seed=70, rows=4)
+    per_row = [S.SamplingConfig(**w.params) for _ in range(w.rows)]
+    per_row[2] = S.SamplingConfig(**dict(w.params, top_k=0))  # k = vocab: the full-order kernels
+    per_row[3] = S.SamplingConfig(**dict(w.params, temperature=0.0))
+    arr = (S.SampleParams * w.rows)(*[c.params() for c in per_row])
+    rp = torch.frombuffer(bytearray(arr), dtype=torch.uint8).cuda()
+    ref, got = _compare(S, L, s, w, *W.to_device(w), row_params=rp, label="C2-row-params")
+    assert (ref[0] >= 0).all()
+    assert ref[2][2] == 0
+    keep = np.array([0, 1, 3])
+    for r, x in zip(ref, got):
+        np.testing.assert_array_equal(x[keep], r[keep])
+    assert got[0][2] == -1 and got[1][2] == 0 and got[2][2] == S.GE_FLAG_UNSUPPORTED
     s.close()
 
 
