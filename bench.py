@@ -39,7 +39,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, GB/s
-PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "select_kernel_C2_traffic.txt")
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "stream_kernel_C2_traffic.txt")
+DROP_IN_BIN = os.path.join(ROOT, "tests", "cpp", "bin", "drop_in_test")
 
 
 def log(*a):
@@ -51,8 +52,8 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--extras", default="C1,C2cold,C3,C4,C4f32,C5",
-                    help="comma list of extra configs to report (C1,C2cold,C3,C4,C4f32,C5) or ''")
+    ap.add_argument("--extras", default="C1,C2cold,C3,C4,C4f32,C5,dropin",
+                    help="comma list of extra configs to report (C1,C2cold,C3,C4,C4f32,C5,dropin) or ''")
     ap.add_argument("--c5-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -238,6 +239,30 @@ def cpu_baseline_leg(w, seconds: float, gpu_out):
     return base, parity_of(gpu_out, ora)
 
 
+def reference_c1(w, seconds=2.0):
+    """The reference's own gemmaedge::sample_token (oracle/_ref, compiled from
+    its src/generation.cpp when that checkout was present at build time) on
+    C1's row after the oracle's softcap, with C1's T, k, p and no penalty (the
+    reference has none): one thread, as its decode loop calls it. None when
+    the library was not built."""
+    O = _oracle()
+    if not O.ref_available():
+        return None
+    p = O.make_params(**dict(w.params, repetition_penalty=1.0))
+    capped = O.transform_row(w.logits[0], p)[None, :].astype(np.float32)
+    kw = dict(temperature=w.params["temperature"], top_k=w.params["top_k"], top_p=w.params["top_p"],
+              min_p=w.params["min_p"], seed=1)
+    O.ref_sample_sequence(capped, **kw)
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        O.ref_sample_sequence(capped, **kw)
+        reps += 1
+    dt = time.perf_counter() - t0
+    return {"us_per_token": dt / reps * 1e6, "threads": 1, "kind": "reference",
+            "sample": f"{reps} calls of the reference's sample_token on C1's capped row ({dt:.2f} s), "
+                      "oracle/_ref/libge_ref.so; softcap not included, the shim's copy of the row into a std::vector is"}
+
+
 def bench_c1(torch, sampler, W):
     """Batch-1 latency (C1 and its greedy run). Returns (extras, {name: (workload, outputs)})."""
     out, runs = {}, {}
@@ -312,6 +337,71 @@ def bench_c2_cold(torch, sampler, w, copies=5, steps=100):
                         "kernel_us": us, "GBps": gbs, "frac_peak": gbs / HBM_PEAK_GBS}}
 
 
+def copy_peak(torch, nbytes=64 * 2**20, buffers=6, copies=60):
+    """Cold device-copy rate: `buffers` source/destination pairs of `nbytes`
+    each (6 x 2 x 64 MiB = 805 MB, beyond the 256 MB Infinity Cache), copy i
+    moving pair i % buffers, all captured in one graph. GB/s counts bytes read
+    plus bytes written."""
+    n = nbytes // 4
+    src = [torch.empty(n, dtype=torch.float32, device="cuda").fill_(float(i)) for i in range(buffers)]
+    dst = [torch.empty_like(x) for x in src]
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            for i in range(copies):
+                dst[i % buffers].copy_(src[i % buffers])
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / copies
+    ok = all(bool(torch.equal(d, s_)) for d, s_ in zip(dst, src))
+    del g, src, dst
+    torch.cuda.empty_cache()
+    return {"GBps": 2 * nbytes / (us * 1e-6) / 1e9, "us_per_copy": us, "bytes_per_copy": 2 * nbytes,
+            "buffers": buffers, "resident_bytes": 2 * buffers * nbytes, "copies_checked": ok,
+            "note": "torch copy_ (read + write), pair i % 6 per copy, one graph replay"}
+
+
+def drop_in_latency(W, calls=400):
+    """Wall-clock latency of gemmaedge::sample_token as the reference's decode
+    loop calls it (a host std::vector<float> of V logits in, a token out:
+    host-to-device copy, launch, device-to-host read), timed by
+    tests/cpp/bin/drop_in_test in a child process over 4 C1-shaped rows."""
+    import subprocess
+    import tempfile
+
+    if not os.path.exists(DROP_IN_BIN):
+        return {"status": f"{os.path.relpath(DROP_IN_BIN, ROOT)} not built"}
+    rows = [W.c1(seed=s) for s in (1, 2, 3, 4)]
+    x = np.concatenate([w.logits for w in rows]).astype(np.float32)
+    h = np.concatenate([w.history for w in rows]).astype(np.int32)
+    with tempfile.TemporaryDirectory() as d:
+        xf, hf = os.path.join(d, "rows.bin"), os.path.join(d, "hist.bin")
+        x.tofile(xf)
+        h.tofile(hf)
+        r = subprocess.run([DROP_IN_BIN, "bench", xf, str(len(rows)), str(x.shape[1]), str(calls), hf,
+                            str(h.size // len(rows))], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": f"exit {r.returncode}: {r.stderr[-300:]}"}
+    out = {}
+    for line in r.stdout.splitlines():
+        parts = line.split()
+        if len(parts) > 1 and all("=" in q for q in parts[1:]):
+            out[parts[0]] = {k: float(v) for k, v in (q.split("=") for q in parts[1:])}
+    out["note"] = ("wall clock per call, host vector in, token out: reference_signature = "
+                   "sample_token(logits, config, rng) with T 1.0, k 64, p 0.95; penalty_overload adds "
+                   "softcap 30 and penalty 1.1 over 128 ids")
+    return out
+
+
 def c5_sweep(torch, sampler, W, steps):
     """Batch-1 decode sweep: one captured graph (the sampling launch) replayed
     per step; the history ring and its length live on the device and grow by
@@ -374,8 +464,43 @@ def c5_sweep(torch, sampler, W, steps):
     torch.cuda.synchronize()
     gpu_out = (step_tokens.cpu().numpy(), step_probs.cpu().numpy(), step_flags.cpu().numpy())
     us = np.array([e0.elapsed_time(e1) * 1000.0 for e0, e1 in ev])
-    out = {"steps": steps, "p50_us": float(np.median(us)), "p99_us": float(np.percentile(us, 99)),
-           "mean_us": float(np.mean(us)), "history_len_final": int(ring_len.item())}
+    out = {"steps": steps,
+           "graph_replay_per_step": {
+               "p50_us": float(np.median(us)), "p99_us": float(np.percentile(us, 99)),
+               "mean_us": float(np.mean(us)),
+               "note": "one-node graph replay per step between HIP events: includes the runtime's graph launch"},
+           "history_len_final": int(ring_len.item())}
+
+    # Device-timed steps: the same decode loop as direct ge_sample launches
+    # (step i reads its logits and uniform in place), queued in blocks behind
+    # a spin kernel so that no host gap falls inside an event pair; the events
+    # bracket the sampler's own launch on the device.
+    dev_tokens = torch.empty(steps, dtype=torch.int32, device="cuda")
+    dev_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    ring.zero_()
+    ring_len.zero_()
+    torch.cuda.synchronize()
+    block = 128
+    for lo in range(0, steps, block):
+        torch.cuda._sleep(int(4e7))
+        for i in range(lo, min(steps, lo + block)):
+            a.logits = all_logits[i].data_ptr()
+            a.uniforms = uni_all[i:i + 1].data_ptr()
+            a.tokens_out = dev_tokens[i:i + 1].data_ptr()
+            dev_ev[i][0].record(stream)
+            rc = lib.ge_sample(sampler._h, ctypes.c_void_p(stream.cuda_stream), ctypes.byref(a))
+            dev_ev[i][1].record(stream)
+            if rc != 0:
+                raise RuntimeError(S.last_error())
+    torch.cuda.synchronize()
+    dus = np.array([e0.elapsed_time(e1) * 1000.0 for e0, e1 in dev_ev])
+    top = np.argsort(dus)[-8:]
+    log("C5 device-timed slowest steps: " + ", ".join(f"{int(i)}:{dus[i]:.1f}us" for i in top))
+    out["device_per_step"] = {
+        "p50_us": float(np.median(dus)), "p99_us": float(np.percentile(dus, 99)),
+        "mean_us": float(np.mean(dus)), "max_us": float(np.max(dus)),
+        "tokens_match": bool(torch.equal(dev_tokens, step_tokens)),
+        "note": "direct launches queued behind a spin kernel, HIP events around each launch"}
 
     # The same decode loop with every step captured in one graph: launch i
     # reads step i's logits and uniform in place and appends to the device
@@ -395,16 +520,24 @@ def c5_sweep(torch, sampler, W, steps):
                 if rc != 0:
                     raise RuntimeError(S.last_error())
     torch.cuda.synchronize()
-    for _ in range(2):  # the first replay uploads the graph; the second is timed
+    # The first replay uploads the graph. The second is timed as replayed; the
+    # third behind a spin kernel, so that the runtime's submission of the
+    # graph's nodes is done before the first event (the device's own time).
+    timed = []
+    for spin in (False, False, True):
         ring.zero_()
         ring_len.zero_()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if spin:
+            torch.cuda._sleep(int(1e8))
         e0.record(stream)
         g_all.replay()
         e1.record(stream)
         torch.cuda.synchronize()
-    out["one_graph_us_per_step"] = e0.elapsed_time(e1) * 1000.0 / steps
+        timed.append(e0.elapsed_time(e1) * 1000.0 / steps)
+    out["one_graph_us_per_step"] = timed[2]
+    out["one_graph_us_per_step_with_submission"] = timed[1]
     out["one_graph_tokens_match"] = bool(torch.equal(graph_tokens, step_tokens))
     # For the oracle: step i's history is the tokens sampled before it (the
     # window never wraps: steps <= ring capacity).
@@ -469,6 +602,9 @@ def main():
     log(f"C2: {ms * 1e3:.2f} us/step, {launch_us:.2f} us/launch (events), isolated {np.mean(d):.2f} us, "
         f"{achieved:.0f} GB/s")
     gpu_out = b.run_once()
+    log("cold copy peak")
+    cp = copy_peak(torch)
+    log(f"copy peak {cp['GBps']:.0f} GB/s")
 
     extras = {}
     runs = {}  # name -> (workload, gpu outputs[, history, offsets]) for the same-run parity
@@ -489,6 +625,8 @@ def main():
             elif name == "C5":
                 c5, run = c5_sweep(torch, sampler, W, args.c5_steps)
                 e, r = {"C5": c5}, {"C5": run}
+            elif name == "dropin":
+                e, r = {"C1_drop_in": drop_in_latency(W)}, {}
             else:
                 raise ValueError(f"unknown extra {name}")
             extras.update(e)
@@ -517,11 +655,17 @@ def main():
                                     "threads": nthreads,
                                     "sample": f"one pass over the {rw.rows} decode steps ({first:.2f} s)"}
         if "C1" in runs:
-            # The reference samples one row per token on one thread (its
-            # softcap loop alone is OpenMP-parallel): batch 1, single thread.
-            r1 = cpu_rate(runs["C1"][0], 2.0, 1)
+            # Batch 1 as the reference runs it: the softcap loop OpenMP-parallel
+            # over the host's threads (generation.cpp:433), the rest of the
+            # sampler on one thread; and the whole token on one thread.
+            # The "C1" entry above is the first (its softcap over `nthreads`).
+            w1 = runs["C1"][0]
+            r1 = cpu_rate(w1, 2.0, 1)
             per_config["C1_single_thread"] = {"us_per_token": r1["us_per_row"], "threads": 1,
                                               "sample": r1["sample"]}
+            ref = reference_c1(w1)
+            if ref is not None:
+                per_config["C1_reference_sample_token"] = ref
         cpu["per_config"] = per_config
 
     result = {
@@ -541,7 +685,9 @@ def main():
                                "top-p 0.9, penalty 1.15, H=2048", "rows": w.rows, "vocab": w.vocab},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(),
-                     "kernel": "select_kernel<float,64>", "kernel_us_mean": launch_us,
+                     "copy_peak_GBps": cp["GBps"], "frac_of_copy_peak": achieved / cp["GBps"],
+                     "copy_peak": cp,
+                     "kernel": "stream_kernel<float,64>", "kernel_us_mean": launch_us,
                      "kernel_us_isolated_p50": float(np.median(d)), "bytes_per_launch": bytes_launch},
         "cpu_baseline": cpu,
         "parity": parity,

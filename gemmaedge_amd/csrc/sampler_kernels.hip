@@ -42,6 +42,7 @@
 // No MFMA: nothing here is a contraction. The bound is HBM bandwidth.
 #include <hip/hip_runtime.h>
 
+#include <cfloat>
 #include <climits>
 #include <cstddef>
 #include <type_traits>
@@ -317,10 +318,27 @@ __device__ __forceinline__ uint32_t block_kth(uint32_t lo, uint32_t hi, uint32_t
     return bucket + (d2 << shift2);
 }
 
+// hist[bin] += 1 for every active lane with `in`; when all of them share the
+// first one's bin (equal or sorted keys: -inf-masked rows, long runs), one
+// atomic adds the count instead of 64 to one address, which LDS serialises.
+__device__ __forceinline__ void hist_add_wave(uint32_t* hist, bool in, uint32_t bin) {
+    const uint64_t act = __ballot(in);
+    if (act == 0ull) return;
+    const int first = __ffsll(static_cast<unsigned long long>(act)) - 1;
+    const uint32_t b0 = wave::readlane(bin, first);
+    if (__ballot(in && bin == b0) == act) {
+        if (__lane_id() == first) atomicAdd(&hist[b0], static_cast<uint32_t>(__popcll(act)));
+    } else if (in) {
+        atomicAdd(&hist[bin], 1u);
+    }
+}
+
 // The exact k-th largest of the keys (>= 1) that `visit` presents: 8-bit
 // radix digits from the highest bit where lo and hi differ, narrowed until
 // every bit is fixed. Returns 0 if fewer than k keys lie in [lo, hi].
-// Block-uniform; uses sh.hist and sh.u32[20..22].
+// Block-uniform; uses sh.hist and sh.u32[20..22]. `visit` may call its
+// function from divergent code: the counts are wave-aggregated over the
+// lanes that are active.
 template <typename Visit>
 __device__ __forceinline__ uint32_t block_kth_exact(uint32_t lo, uint32_t hi, uint32_t k, Visit&& visit, SelShared& sh) {
     const int tid = threadIdx.x;
@@ -337,8 +355,7 @@ __device__ __forceinline__ uint32_t block_kth_exact(uint32_t lo, uint32_t hi, ui
         __syncthreads();
         const uint32_t dmask = (1u << width) - 1u;
         visit([&](uint32_t key) {
-            if (key >= lo && key <= hi && (key & fixed) == prefix)
-                atomicAdd(&sh.hist[(key >> shift) & dmask], 1u);
+            hist_add_wave(sh.hist, key >= lo && key <= hi && (key & fixed) == prefix, (key >> shift) & dmask);
         });
         __syncthreads();
         if (tid < 64) find_bin_desc(sh.hist, need, &sh.u32[20]);
@@ -500,6 +517,39 @@ struct LeanList {
     bool fs;
 };
 
+// Batches of the rescans' loads: SBE elements per thread (whole groups of W;
+// a template argument of the routines below, 0 for one group) are requested
+// before any is used. Loads at clamped addresses and unconditional: a load
+// under a lane mask is followed by a wait for every load in flight, which
+// made every element's load a round trip of its own. Larger batches hold
+// more registers: the single-pass kernel's rescans use 16 elements, the
+// select kernel's (already at its register limit) one group.
+constexpr int kSlowBatchStream = 8;
+
+// Groups v0 .. v0 + SB - 1 of this thread (group v: elements e0 .. e0 + W - 1,
+// e0 = c0 + (v * kBlock + tid) * W); elements at or past cend read as NaN.
+template <typename T, int W, int SB>
+__device__ __forceinline__ void load_groups(const T* rowp, int c0, int cend, int tid, int v0, float (&x)[SB][W]) {
+    if (c0 + (v0 + SB) * kBlock * W <= cend) {  // the whole batch in range (block-uniform)
+#pragma unroll
+        for (int b = 0; b < SB; ++b) {
+            const int e0 = c0 + ((v0 + b) * kBlock + tid) * W;
+#pragma unroll
+            for (int j = 0; j < W; ++j) x[b][j] = load_one(rowp, e0 + j);
+        }
+    } else {
+#pragma unroll
+        for (int b = 0; b < SB; ++b) {
+            const int e0 = c0 + ((v0 + b) * kBlock + tid) * W;
+#pragma unroll
+            for (int j = 0; j < W; ++j) {
+                const float t = load_one(rowp, min(e0 + j, cend - 1));
+                x[b][j] = e0 + j < cend ? t : NAN;
+            }
+        }
+    }
+}
+
 // Builds the chunk's penalty bitmap in pbits (one bit per element of
 // [c0, c0 + CHUNK)) from the row's history. Block-uniform (barriers).
 template <int CHUNK>
@@ -523,15 +573,15 @@ __device__ __forceinline__ void build_penalty_bitmap(const RowCtx& rc, int c0, i
 // Exact top-m of one chunk, for the rare cases: candidates that overflow LDS
 // in the streaming pass (massive ties, or a bound far below the m-th value)
 // and the merge's rescans. Same contract as chunk_topm. It keeps registers
-// low: runtime loops over one 16-byte group per thread at a time, reloading
-// the chunk from memory (L2 / MALL) in every pass.
+// low: runtime loops over batches of kSlowBatch elements per thread,
+// reloading the chunk from memory (L2 / MALL) in every pass.
 //   1. R = the exact m-th largest non-penalised raw order key (radix select);
 //   2. lo..hi = the raw keys whose softcapped value equals R's (its class);
 //   3. candidates: every non-penalised element above the class, the
 //      m - (that count) lowest-index members of the class (counted in index
 //      order), and every penalised token that can reach the class;
 //   4. final values, top m, sorted.
-template <typename T, int EPT>
+template <typename T, int EPT, int SBE>
 __device__ __forceinline__ uint64_t chunk_slow(const RowCtx& rc, int c0, uint32_t m, uint32_t* pbits,
                                                SelShared& sh, uint32_t& n_out, bool& ok) {
     constexpr int W = sizeof(T) == 4 ? 4 : 8;
@@ -547,21 +597,20 @@ __device__ __forceinline__ uint64_t chunk_slow(const RowCtx& rc, int c0, uint32_
     auto is_pen = [&](int e) -> bool {
         return rc.pen && ((pbits[(e - c0) >> 5] >> ((e - c0) & 31)) & 1u);
     };
-    // Group v of this thread: elements e0 .. e0 + W - 1, e0 = c0 + (v * kBlock + tid) * W.
-    auto load_group = [&](int v, float (&x)[W]) {
-        const int e0 = c0 + (v * kBlock + tid) * W;
-#pragma unroll
-        for (int j = 0; j < W; ++j) x[j] = e0 + j < cend ? load_one(rowp, e0 + j) : NAN;
-    };
+    constexpr int SB = SBE / W < 1 ? 1 : (SBE / W < NV ? SBE / W : NV);  // groups per batch
+    static_assert(NV % SB == 0, "batches of whole groups");
     auto visit_np = [&](auto&& f) {
 #pragma unroll 1
-        for (int v = 0; v < NV; ++v) {
-            float x[W];
-            load_group(v, x);
-            const int e0 = c0 + (v * kBlock + tid) * W;
+        for (int v0 = 0; v0 < NV; v0 += SB) {
+            float x[SB][W];
+            load_groups<T, W, SB>(rowp, c0, cend, tid, v0, x);
 #pragma unroll
-            for (int j = 0; j < W; ++j)
-                if (e0 + j < cend && !is_pen(e0 + j)) f(order_key(x[j]));
+            for (int b = 0; b < SB; ++b) {
+                const int e0 = c0 + ((v0 + b) * kBlock + tid) * W;
+#pragma unroll
+                for (int j = 0; j < W; ++j)
+                    if (e0 + j < cend && !is_pen(e0 + j)) f(order_key(x[b][j]));
+            }
         }
     };
     const uint32_t R = block_kth_exact(1u, 0xffffffffu, m, visit_np, sh);
@@ -597,13 +646,16 @@ __device__ __forceinline__ uint64_t chunk_slow(const RowCtx& rc, int c0, uint32_
     if (rc.pen) {
         auto visit_pen = [&](auto&& f) {
 #pragma unroll 1
-            for (int v = 0; v < NV; ++v) {
-                float x[W];
-                load_group(v, x);
-                const int e0 = c0 + (v * kBlock + tid) * W;
+            for (int v0 = 0; v0 < NV; v0 += SB) {
+                float x[SB][W];
+                load_groups<T, W, SB>(rowp, c0, cend, tid, v0, x);
 #pragma unroll
-                for (int j = 0; j < W; ++j)
-                    if (e0 + j < cend && is_pen(e0 + j)) f(pen_key(x[j]));
+                for (int b = 0; b < SB; ++b) {
+                    const int e0 = c0 + ((v0 + b) * kBlock + tid) * W;
+#pragma unroll
+                    for (int j = 0; j < W; ++j)
+                        if (e0 + j < cend && is_pen(e0 + j)) f(pen_key(x[b][j]));
+                }
             }
         };
         pk = block_kth_exact(1u, 0xffffffffu, m, visit_pen, sh);
@@ -617,70 +669,74 @@ __device__ __forceinline__ uint64_t chunk_slow(const RowCtx& rc, int c0, uint32_
     // positions are exclusive scans over the threads.
     uint32_t cls_before = 0, pcls_before = 0, n_c = 0;
 #pragma unroll 1
-    for (int v = 0; v < NV; ++v) {
-        float x[W];
-        load_group(v, x);
-        const int e0 = c0 + (v * kBlock + tid) * W;
-        uint32_t cls = 0, pen = 0, valid = 0;
+    for (int v0 = 0; v0 < NV; v0 += SB) {
+        float xb[SB][W];
+        load_groups<T, W, SB>(rowp, c0, cend, tid, v0, xb);
 #pragma unroll
-        for (int j = 0; j < W; ++j) {
-            const uint32_t key = order_key(x[j]);
-            const bool in = e0 + j < cend;
-            const bool pj = in && is_pen(e0 + j);
-            valid |= static_cast<uint32_t>(in) << j;
-            pen |= static_cast<uint32_t>(pj) << j;
-            cls |= static_cast<uint32_t>(in && !pj && key >= lo && key <= hi) << j;
-        }
-        uint32_t cls_total;
-        const uint32_t cbase = cls_before + block_excl_scan(static_cast<uint32_t>(__popc(cls)), cls_total, sh);
-        cls_before += cls_total;
-        uint32_t pcls = 0, pbig = 0;  // penalised: final key == pk / > pk
-        if (pen != 0u && pk != 0u) {
+        for (int b = 0; b < SB; ++b) {
+            const float (&x)[W] = xb[b];
+            const int e0 = c0 + ((v0 + b) * kBlock + tid) * W;
+            uint32_t cls = 0, pen = 0, valid = 0;
 #pragma unroll
             for (int j = 0; j < W; ++j) {
-                if (!((pen >> j) & 1u)) continue;
-                const uint32_t fk = pen_key(x[j]);
-                pcls |= static_cast<uint32_t>(fk == pk) << j;
-                pbig |= static_cast<uint32_t>(fk > pk) << j;
+                const uint32_t key = order_key(x[j]);
+                const bool in = e0 + j < cend;
+                const bool pj = in && is_pen(e0 + j);
+                valid |= static_cast<uint32_t>(in) << j;
+                pen |= static_cast<uint32_t>(pj) << j;
+                cls |= static_cast<uint32_t>(in && !pj && key >= lo && key <= hi) << j;
             }
-        }
-        uint32_t pbase = 0;
-        if (pk != 0u) {
-            uint32_t pcls_total;
-            pbase = pcls_before + block_excl_scan(static_cast<uint32_t>(__popc(pcls)), pcls_total, sh);
-            pcls_before += pcls_total;
-        }
-        uint32_t cand = 0;
+            uint32_t cls_total;
+            const uint32_t cbase = cls_before + block_excl_scan(static_cast<uint32_t>(__popc(cls)), cls_total, sh);
+            cls_before += cls_total;
+            uint32_t pcls = 0, pbig = 0;  // penalised: final key == pk / > pk
+            if (pen != 0u && pk != 0u) {
 #pragma unroll
-        for (int j = 0; j < W; ++j) {
-            const uint32_t key = order_key(x[j]);
-            bool c;
-            if ((pen >> j) & 1u) {
-                c = pk == 0u || ((pbig >> j) & 1u) ||
-                    (((pcls >> j) & 1u) && pbase + static_cast<uint32_t>(__popc(pcls & ((1u << j) - 1u))) < pq);
-            } else if ((cls >> j) & 1u) {
-                c = cbase + static_cast<uint32_t>(__popc(cls & ((1u << j) - 1u))) < q;
-            } else {
-                c = ((valid >> j) & 1u) && key > hi;
+                for (int j = 0; j < W; ++j) {
+                    if (!((pen >> j) & 1u)) continue;
+                    const uint32_t fk = pen_key(x[j]);
+                    pcls |= static_cast<uint32_t>(fk == pk) << j;
+                    pbig |= static_cast<uint32_t>(fk > pk) << j;
+                }
             }
-            cand |= static_cast<uint32_t>(c) << j;
-        }
-        uint32_t cand_total;
-        const uint32_t pos = n_c + block_excl_scan(static_cast<uint32_t>(__popc(cand)), cand_total, sh);
-        if (n_c + cand_total > static_cast<uint32_t>(kStage)) {
-            ok = false;
-            n_out = 0;
-            return ~0ull;
-        }
-        uint32_t o = pos;
+            uint32_t pbase = 0;
+            if (pk != 0u) {
+                uint32_t pcls_total;
+                pbase = pcls_before + block_excl_scan(static_cast<uint32_t>(__popc(pcls)), pcls_total, sh);
+                pcls_before += pcls_total;
+            }
+            uint32_t cand = 0;
 #pragma unroll
-        for (int j = 0; j < W; ++j) {
-            if ((cand >> j) & 1u) {
-                const uint32_t tag = static_cast<uint32_t>(e0 + j) | (((pen >> j) & 1u) ? kPenTag : 0u);
-                sh.stage[o++] = (static_cast<uint64_t>(tag) << 32) | f2u(x[j]);
+            for (int j = 0; j < W; ++j) {
+                const uint32_t key = order_key(x[j]);
+                bool c;
+                if ((pen >> j) & 1u) {
+                    c = pk == 0u || ((pbig >> j) & 1u) ||
+                        (((pcls >> j) & 1u) && pbase + static_cast<uint32_t>(__popc(pcls & ((1u << j) - 1u))) < pq);
+                } else if ((cls >> j) & 1u) {
+                    c = cbase + static_cast<uint32_t>(__popc(cls & ((1u << j) - 1u))) < q;
+                } else {
+                    c = ((valid >> j) & 1u) && key > hi;
+                }
+                cand |= static_cast<uint32_t>(c) << j;
             }
+            uint32_t cand_total;
+            const uint32_t pos = n_c + block_excl_scan(static_cast<uint32_t>(__popc(cand)), cand_total, sh);
+            if (n_c + cand_total > static_cast<uint32_t>(kStage)) {
+                ok = false;
+                n_out = 0;
+                return ~0ull;
+            }
+            uint32_t o = pos;
+#pragma unroll
+            for (int j = 0; j < W; ++j) {
+                if ((cand >> j) & 1u) {
+                    const uint32_t tag = static_cast<uint32_t>(e0 + j) | (((pen >> j) & 1u) ? kPenTag : 0u);
+                    sh.stage[o++] = (static_cast<uint64_t>(tag) << 32) | f2u(x[j]);
+                }
+            }
+            n_c += cand_total;
         }
-        n_c += cand_total;
     }
     __syncthreads();
     for (uint32_t i = tid; i < n_c; i += kBlock) {
@@ -724,15 +780,15 @@ __device__ __forceinline__ uint32_t append_penalised(SelShared& sh, uint32_t n_c
 // Exact raw top-m of one chunk for the rare cases of the streaming pass
 // (candidates that overflow LDS: massive ties, NaN-heavy or partial chunks).
 // Same contract as chunk_topm; the penalty bitmap pbits is already built.
-// Runtime loops over one 16-byte group per thread, reloading the chunk from
-// memory (L2 / MALL) in every pass:
+// Runtime loops over batches of kSlowBatch elements per thread, reloading the
+// chunk from memory (L2 / MALL) in every pass:
 //   1. R = the exact m-th largest raw order key (radix select);
 //   2. Lq = the (m - #above R)-th largest entry low word among the keys
 //      equal to R (low words are distinct), so that exactly m entries are
 //      >= raw_entry(R, Lq);
 //   3. stage those (and, with a penalty below 1, every penalised element),
 //      sort, keep the top m.
-template <typename T, int EPT>
+template <typename T, int EPT, int SBE>
 __device__ __forceinline__ uint64_t chunk_slow_raw(const RowCtx& rc, int c0, uint32_t m, const uint32_t* pbits,
                                                    SelShared& sh, uint64_t* slot, uint32_t stride,
                                                    uint32_t& n_top, uint32_t& n_out, bool& ok) {
@@ -747,20 +803,20 @@ __device__ __forceinline__ uint64_t chunk_slow_raw(const RowCtx& rc, int c0, uin
     auto is_pen = [&](int e) -> bool {
         return rc.pen && ((pbits[(e - c0) >> 5] >> ((e - c0) & 31)) & 1u);
     };
-    auto load_group = [&](int v, float (&x)[W]) {
-        const int e0 = c0 + (v * kBlock + tid) * W;
-#pragma unroll
-        for (int j = 0; j < W; ++j) x[j] = e0 + j < cend ? load_one(rowp, e0 + j) : NAN;
-    };
+    constexpr int SB = SBE / W < 1 ? 1 : (SBE / W < NV ? SBE / W : NV);  // groups per batch
+    static_assert(NV % SB == 0, "batches of whole groups");
     auto visit_keys = [&](auto&& f) {
 #pragma unroll 1
-        for (int v = 0; v < NV; ++v) {
-            float x[W];
-            load_group(v, x);
-            const int e0 = c0 + (v * kBlock + tid) * W;
+        for (int v0 = 0; v0 < NV; v0 += SB) {
+            float x[SB][W];
+            load_groups<T, W, SB>(rowp, c0, cend, tid, v0, x);
 #pragma unroll
-            for (int j = 0; j < W; ++j)
-                if (e0 + j < cend) f(order_key(x[j]));
+            for (int b = 0; b < SB; ++b) {
+                const int e0 = c0 + ((v0 + b) * kBlock + tid) * W;
+#pragma unroll
+                for (int j = 0; j < W; ++j)
+                    if (e0 + j < cend) f(order_key(x[b][j]));
+            }
         }
     };
     const uint32_t R = block_kth_exact(1u, 0xffffffffu, m, visit_keys, sh);
@@ -772,14 +828,17 @@ __device__ __forceinline__ uint64_t chunk_slow_raw(const RowCtx& rc, int c0, uin
         const uint32_t q = m - above;  // >= 1
         auto visit_lows = [&](auto&& f) {
 #pragma unroll 1
-            for (int v = 0; v < NV; ++v) {
-                float x[W];
-                load_group(v, x);
-                const int e0 = c0 + (v * kBlock + tid) * W;
+            for (int v0 = 0; v0 < NV; v0 += SB) {
+                float x[SB][W];
+                load_groups<T, W, SB>(rowp, c0, cend, tid, v0, x);
 #pragma unroll
-                for (int j = 0; j < W; ++j)
-                    if (e0 + j < cend && order_key(x[j]) == R)
-                        f(raw_entry_low(static_cast<uint32_t>(e0 + j), is_pen(e0 + j)));
+                for (int b = 0; b < SB; ++b) {
+                    const int e0 = c0 + ((v0 + b) * kBlock + tid) * W;
+#pragma unroll
+                    for (int j = 0; j < W; ++j)
+                        if (e0 + j < cend && order_key(x[b][j]) == R)
+                            f(raw_entry_low(static_cast<uint32_t>(e0 + j), is_pen(e0 + j)));
+                }
             }
         };
         lq = block_kth_exact(1u, 0xffffffffu, q, visit_lows, sh);
@@ -787,30 +846,34 @@ __device__ __forceinline__ uint64_t chunk_slow_raw(const RowCtx& rc, int c0, uin
     const uint64_t thr = R != 0u ? ((static_cast<uint64_t>(R) << 32) | lq) : 0ull;
     uint32_t n_c = 0;
 #pragma unroll 1
-    for (int v = 0; v < NV; ++v) {
-        float x[W];
-        load_group(v, x);
-        const int e0 = c0 + (v * kBlock + tid) * W;
-        uint64_t ent[W];
-        uint32_t cand = 0;
+    for (int v0 = 0; v0 < NV; v0 += SB) {
+        float xb[SB][W];
+        load_groups<T, W, SB>(rowp, c0, cend, tid, v0, xb);
 #pragma unroll
-        for (int j = 0; j < W; ++j) {
-            const bool in = e0 + j < cend;
-            const bool pj = in && is_pen(e0 + j);
-            ent[j] = raw_entry(order_key(x[j]), static_cast<uint32_t>(e0 + j), pj);
-            cand |= static_cast<uint32_t>(in && (ent[j] >= thr || (pen_all && pj))) << j;
-        }
-        uint32_t total;
-        uint32_t pos = n_c + block_excl_scan(static_cast<uint32_t>(__popc(cand)), total, sh);
-        if (n_c + total > static_cast<uint32_t>(kStage)) {
-            ok = false;
-            n_top = n_out = 0;
-            return kGuaranteeFailed;
-        }
+        for (int b = 0; b < SB; ++b) {
+            const float (&x)[W] = xb[b];
+            const int e0 = c0 + ((v0 + b) * kBlock + tid) * W;
+            uint64_t ent[W];
+            uint32_t cand = 0;
 #pragma unroll
-        for (int j = 0; j < W; ++j)
-            if ((cand >> j) & 1u) sh.stage[pos++] = ent[j];
-        n_c += total;
+            for (int j = 0; j < W; ++j) {
+                const bool in = e0 + j < cend;
+                const bool pj = in && is_pen(e0 + j);
+                ent[j] = raw_entry(order_key(x[j]), static_cast<uint32_t>(e0 + j), pj);
+                cand |= static_cast<uint32_t>(in && (ent[j] >= thr || (pen_all && pj))) << j;
+            }
+            uint32_t total;
+            uint32_t pos = n_c + block_excl_scan(static_cast<uint32_t>(__popc(cand)), total, sh);
+            if (n_c + total > static_cast<uint32_t>(kStage)) {
+                ok = false;
+                n_top = n_out = 0;
+                return kGuaranteeFailed;
+            }
+#pragma unroll
+            for (int j = 0; j < W; ++j)
+                if ((cand >> j) & 1u) sh.stage[pos++] = ent[j];
+            n_c += total;
+        }
     }
     __syncthreads();
     n_top = select_top(sh.stage, n_c, m, sh.list);
@@ -1067,7 +1130,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     // tau <= kKeyNaN: fewer than m real logits in some wave; no pruning.
     const bool allpass = tau <= kKeyNaN;
     if (allpass && cend - c0 > kStage) {
-        return chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
+        return chunk_slow_raw<T, EPT, 0>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
     }
     const float floor_v = key_value(max(tau, kKeyNegInf));  // raw >= floor_v <=> key >= tau
 
@@ -1143,7 +1206,7 @@ __device__ __forceinline__ uint64_t chunk_topm(const RowCtx& rc, int c0, uint32_
     }
     if (seg_over) {
         // Massive ties or a loose bound: the exact routine.
-        return chunk_slow_raw<T, EPT>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
+        return chunk_slow_raw<T, EPT, 0>(rc, c0, m, pbits, sh, slot, stride, n_top, n_out, ok);
     }
     if (n_c <= 64u && !pen_all && !ll.fs) {
         // 5. The usual case: wave 0 ranks the candidates by counting (exact
@@ -2519,11 +2582,11 @@ __device__ __forceinline__ void merge_all_fs(const DevArgs& a, SelShared& sh, co
     nt = select_top(sh.stage, n, k, sh.top);
 }
 
-template <typename T, int EPT>
+template <typename T, int EPT, int SBE = 0>
 __device__ __forceinline__ uint32_t rescan_chunk(const RowCtx& rc, int c, uint32_t k, uint32_t* pbits,
                                                  SelShared& sh, bool& ok) {
     uint32_t n_out;
-    (void)chunk_slow<T, EPT>(rc, c * (kBlock * EPT), k, pbits, sh, n_out, ok);
+    (void)chunk_slow<T, EPT, SBE>(rc, c * (kBlock * EPT), k, pbits, sh, n_out, ok);
     return n_out;
 }
 
@@ -2924,11 +2987,13 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
 #pragma unroll
         for (int i = 0; i < NW; ++i) asm volatile("" : "+v"(d[i]));
     }
-    // 3. The wave's q-th largest lane maximum (lanes without a number count
-    //    as 0); 0 means fewer such lanes: no bound from this wave.
+    // 3. The wave's q-th largest lane maximum (lanes whose maximum is NaN or
+    //    -inf count as 0); 0 means fewer such lanes: no bound from this wave.
+    //    (-inf is no bound: a row masked with -inf would otherwise list
+    //    every masked element and overflow.)
     const uint32_t qlo = pl_rank(k, a.cpr, ne);
     uint32_t key = order_key(lmf);
-    key = key > kKeyNaN ? key : 0u;
+    key = key > kKeyNegInf ? key : 0u;
     uint32_t tlo = 0u;
     for (uint32_t i = 0; i < qlo; ++i) {
         const uint32_t mx = wave::max_u32(key);
@@ -2947,7 +3012,8 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
     //    reaches the bound; inside, every slot's word is written, to the
     //    lane's next candidate position or to its own dummy word: no branch
     //    per slot.
-    const float floor_v = tlo ? key_value(tau_lo) : -INFINITY;
+    // A wave without a bound of its own lists every element above -inf.
+    const float floor_v = tlo ? key_value(tau_lo) : -FLT_MAX;
     uint64_t* seg = sh.stage + wave * kSeg;
     uint64_t* cmp = seg + kPlCand * 64;            // compacted candidates (at most kPlMaxEntries)
     constexpr uint32_t kDummy = kSeg - 64;          // per-lane dummy words
@@ -2988,7 +3054,9 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
     wave_lds_sync();
     // 5. Final keys (one softcap round for the wave: lane i < n_w takes
     //    candidate i, lane 63 the value of tau), then the list: entries,
-    //    fillers, and the header [largest final key | capped tau].
+    //    fillers, and the header [largest final key | capped tau]. With no
+    //    bound in any wave, every element above -inf is listed and the
+    //    bound is the capped -inf (NaN and -inf are what is left out).
     float xv = 0.0f;
     uint32_t idx = 0u;
     bool pen = false;
@@ -3002,13 +3070,13 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
             pen = ((s_pbits[off >> 5] >> (off & 31)) & 1u) != 0u;
         }
     } else if (lane == 63) {
-        xv = tau_lo != 0xffffffffu ? key_value(tau_lo) : 0.0f;
+        xv = tau_lo != 0xffffffffu ? key_value(tau_lo) : -INFINITY;
     }
     float f = softcap(xv, rc.cap);
     if (pen) f = penalize(f, rc.r);
     const uint32_t fk = order_key(f);
     const uint32_t wmax = wave::max_u32(cand ? fk : 0u);
-    const uint32_t blo = tau_lo != 0xffffffffu ? wave::readlane(fk, 63) : kKeyNaN;
+    const uint32_t blo = wave::readlane(fk, 63);
     const uint64_t hword = overflow ? kPlOverflow : ((static_cast<uint64_t>(wmax) << 32) | blo);
     const uint64_t eword = cand ? composite(fk, idx) : kPlFiller;
     const uint32_t lj_own = static_cast<uint32_t>(chunk) * 4u + static_cast<uint32_t>(wave);
@@ -3220,13 +3288,44 @@ __global__ __launch_bounds__(kBlock, 4) void stream_kernel(DevArgs a) {
         return;
     }
     // 12. Fallback (fewer than k entries above the bound, or an overflowing
-    //     list): exact rescans of every chunk (chunk_slow stages at most 2k
-    //     entries, within kStage), merged into the top k.
+    //     list). Every listed entry goes into the top k; then a chunk is
+    //     rescanned exactly (chunk_slow stages at most 2k entries, within
+    //     kStage) only when an element it left out could still enter: its
+    //     bound word, (capped tau) << 32 | 0xffffffff (at least the composite
+    //     key of any element it left out), is above the running k-th entry;
+    //     a chunk with an overflowing list always is. absorb_list drops the
+    //     entries a rescan finds again.
     __syncthreads();
-    uint32_t nt = 0;
+    if (tid < a.cpr) sh.gam[tid] = 0ull;
+    if (tid == 0) sh.u32[kSegCount] = 0u;
+    __syncthreads();
+    if (static_cast<uint32_t>(tid) < nl)  // thread t < nl holds header t
+        lds_max_u64(&sh.gam[static_cast<uint32_t>(tid) / 4u],
+                    h == kPlOverflow ? kPlOverflow : ((h << 32) | 0xffffffffull));
+    lds_wait();
+    {
+        uint32_t c = 0u;
+        bool keep[kPlPer];
+#pragma unroll
+        for (uint32_t i = 0; i < kPlPer; ++i) {
+            keep[i] = ev[i] && e[i] != kPlFiller;
+            c += keep[i] ? 1u : 0u;
+        }
+        const uint32_t incl = wave::incl_add(c);
+        uint32_t base = 0u;
+        if (lane == 63 && incl != 0u) base = atomicAdd(&sh.u32[kSegCount], incl);
+        uint32_t pos = wave::readlane(base, 63) + incl - c;
+#pragma unroll
+        for (uint32_t i = 0; i < kPlPer; ++i)
+            if (keep[i]) sh.stage[pos++] = e[i];
+    }
+    __syncthreads();
+    uint32_t nt = select_top(sh.stage, sh.u32[kSegCount], k, sh.top);
     for (int c = 0; c < a.cpr; ++c) {
+        const uint64_t kth = nt < k ? 0ull : sh.top[k - 1u];
+        if (!(sh.gam[c] > kth)) continue;
         bool rok;
-        const uint32_t nlist = rescan_chunk<T, EPT>(rc, c, k, s_pbits, sh, rok);
+        const uint32_t nlist = rescan_chunk<T, EPT, kSlowBatchStream>(rc, c, k, s_pbits, sh, rok);
         if (!rok) {
             if (tid == 0) emit_row(a, row, -1, 0.0f, GE_FLAG_UNSUPPORTED);
             return;

@@ -207,7 +207,8 @@ def test_clustered_top_k_takes_the_rescan(sampler, rows):
 
 def test_repeated_rescans_are_stable(sampler):
     # Regression: every row of sorted logits takes the merge's rescan
-    # fallback; repeated launches on one handle must all match (a scratch
+    # fallback; repeated launches on one handle, with no host wait between
+    # the kernels of consecutive launches, must all match (a scratch
     # word shared between two LDS helpers once let waves disagree on the
     # fallback decision in about 1% of launches).
     import torch
@@ -226,11 +227,14 @@ def test_repeated_rescans_are_stable(sampler):
                     history=hist, offsets=offs, uniforms=uni)
         cfg = SamplingConfig(temperature=T, top_k=k, top_p=p, softcap=30.0, repetition_penalty=1.15)
         du = torch.from_numpy(uni).cuda()
-        bad = 0
-        for _ in range(40):
-            t, _, _ = sampler.sample(dx, cfg, uniforms=du, history=dh, history_offsets=do)
-            bad += int(np.count_nonzero(t.cpu().numpy() != ora.tokens))
-        assert bad == 0, f"k={k}: {bad} mismatching row-launches over 40 launches"
+        # Shared parameters take the single-pass kernel (polled lists); the
+        # same parameters per row take select_kernel (lists and tickets).
+        for label, c in (("shared", cfg), ("per-row", [cfg] * rows)):
+            bad = 0
+            for _ in range(40):
+                t, _, _ = sampler.sample(dx, c, uniforms=du, history=dh, history_offsets=do)
+                bad += int(np.count_nonzero(t.cpu().numpy() != ora.tokens))
+            assert bad == 0, f"k={k} {label}: {bad} mismatching row-launches over 40 launches"
 
 
 def test_penalty_below_one_with_long_histories(sampler):

@@ -42,28 +42,21 @@ def _row_params(torch, params):
     return torch.frombuffer(bytearray(arr), dtype=torch.uint8).cuda()
 
 
-@pytest.mark.parametrize("mode", ["after_push", "before_push"])
-def test_multi_session_ring_graph_with_stop(mode):
+def _run_session(label, mode, params, stop_at, cap, steps, seed, shared=False, vocab=262144):
+    """Captures one ge_sample over len(params) rows with a device ring, stop
+    tokens and done flags, replays it `steps` times and checks every replay,
+    the final ring, ring_len and done against the oracle. shared=True passes
+    params[0] as the call's shared parameters (no row_params)."""
     import torch
 
     from gemmaedge_amd import Sampler
     from gemmaedge_amd import sampler as S
 
-    rows, vocab, cap, steps = 8, 262144, 24, 44
+    rows = len(params)
     stop_mode = S.GE_STOP_AFTER_PUSH if mode == "after_push" else S.GE_STOP_BEFORE_PUSH
-    base = dict(softcap=30.0, min_p=0.0)
-    params = [dict(base, temperature=1.0, top_k=64, top_p=0.95, repetition_penalty=1.1),
-              dict(base, temperature=0.7, top_k=40, top_p=0.9, repetition_penalty=1.15),
-              dict(base, temperature=0.0, top_k=64, top_p=0.95, repetition_penalty=1.3),  # greedy
-              dict(base, temperature=1.3, top_k=512, top_p=0.99, repetition_penalty=1.05),
-              dict(base, temperature=1.0, top_k=1, top_p=1.0, repetition_penalty=1.0),
-              dict(base, temperature=0.9, top_k=200, top_p=0.8, repetition_penalty=0.9),   # r < 1
-              dict(base, temperature=1.0, top_k=64, top_p=0.95, repetition_penalty=1.1, min_p=0.05),
-              dict(base, temperature=1.2, top_k=1024, top_p=0.95, repetition_penalty=1.2)]
-    stop_at = {(1, 9): 106, (4, 17): 1, (6, 30): 106}
-    x = _peaked_steps(11, steps, rows, vocab, stop_at=stop_at)
-    u_all = W.mt_uniforms(31, steps * rows).reshape(steps, rows)
-    print(f"[sessions] {mode}: rows={rows} V={vocab} cap={cap} steps={steps}", flush=True)
+    x = _peaked_steps(seed, steps, rows, vocab, stop_at=stop_at)
+    u_all = W.mt_uniforms(seed + 20, steps * rows).reshape(steps, rows)
+    print(f"[sessions] {label} {mode}: rows={rows} V={vocab} cap={cap} steps={steps} shared={shared}", flush=True)
 
     s = Sampler(max_rows=rows, max_vocab=vocab, max_history=cap)
     logits = torch.empty((rows, vocab), dtype=torch.float32, device="cuda")
@@ -75,11 +68,12 @@ def test_multi_session_ring_graph_with_stop(mode):
     tokens = torch.empty(rows, dtype=torch.int32, device="cuda")
     probs = torch.empty(rows, dtype=torch.float32, device="cuda")
     flags = torch.empty(rows, dtype=torch.int32, device="cuda")
-    rp = _row_params(torch, params)
     a = S.SampleArgs()
     a.logits, a.dtype, a.rows, a.vocab, a.row_stride = logits.data_ptr(), S.GE_DTYPE_F32, rows, vocab, vocab
     a.params = S.SamplingConfig(**params[0]).params()
-    a.row_params = rp.data_ptr()
+    rp = None if shared else _row_params(torch, params)
+    if rp is not None:
+        a.row_params = rp.data_ptr()
     a.ring, a.ring_len, a.ring_capacity = ring.data_ptr(), ring_len.data_ptr(), cap
     a.uniforms, a.tokens_out, a.probs_out, a.flags_out = (uni.data_ptr(), tokens.data_ptr(),
                                                           probs.data_ptr(), flags.data_ptr())
@@ -111,11 +105,12 @@ def test_multi_session_ring_graph_with_stop(mode):
         got_p = probs.cpu().numpy().view(np.uint32)
         got_f = flags.cpu().numpy()
         live = [r for r in range(rows) if not finished[r]]
-        hs = [np.array(pushed[r][-cap:], np.int32) for r in live]
-        offs = np.concatenate([[0], np.cumsum([h.size for h in hs])]).astype(np.int32)
-        ora = O.run(x[i, live], [oparams[r] for r in live],
-                    history=np.concatenate(hs) if offs[-1] else np.zeros(0, np.int32), offsets=offs,
-                    uniforms=u_all[i, live], nthreads=4)
+        if live:
+            hs = [np.array(pushed[r][-cap:], np.int32) for r in live]
+            offs = np.concatenate([[0], np.cumsum([h.size for h in hs])]).astype(np.int32)
+            ora = O.run(x[i, live], [oparams[r] for r in live],
+                        history=np.concatenate(hs) if offs[-1] else np.zeros(0, np.int32), offsets=offs,
+                        uniforms=u_all[i, live], nthreads=4)
         for j, r in enumerate(live):
             assert got_t[r] == ora.tokens[j], f"step {i} row {r}: gpu {got_t[r]} oracle {ora.tokens[j]}"
             assert got_p[r] == ora.probs.view(np.uint32)[j], f"step {i} row {r} prob"
@@ -129,7 +124,7 @@ def test_multi_session_ring_graph_with_stop(mode):
         for r in range(rows):
             if r not in live:
                 assert got_t[r] == -1 and got_f[r] == S.GE_FLAG_DONE, f"step {i} row {r} done"
-    assert stopped_rows >= {1, 4, 6}
+    assert stopped_rows >= {r for (r, _) in stop_at}
     np.testing.assert_array_equal(ring_len.cpu().numpy(), [len(p) for p in pushed])
     np.testing.assert_array_equal(done.cpu().numpy(), [1 if f else 0 for f in finished])
     rg = ring.cpu().numpy()
@@ -140,6 +135,36 @@ def test_multi_session_ring_graph_with_stop(mode):
             want[t % cap] = pushed[r][t]
         np.testing.assert_array_equal(rg[r], want, err_msg=f"ring row {r}")
     s.close()
+
+
+@pytest.mark.parametrize("mode", ["after_push", "before_push"])
+def test_multi_session_ring_graph_with_stop(mode):
+    base = dict(softcap=30.0, min_p=0.0)
+    params = [dict(base, temperature=1.0, top_k=64, top_p=0.95, repetition_penalty=1.1),
+              dict(base, temperature=0.7, top_k=40, top_p=0.9, repetition_penalty=1.15),
+              dict(base, temperature=0.0, top_k=64, top_p=0.95, repetition_penalty=1.3),  # greedy
+              dict(base, temperature=1.3, top_k=512, top_p=0.99, repetition_penalty=1.05),
+              dict(base, temperature=1.0, top_k=1, top_p=1.0, repetition_penalty=1.0),
+              dict(base, temperature=0.9, top_k=200, top_p=0.8, repetition_penalty=0.9),   # r < 1
+              dict(base, temperature=1.0, top_k=64, top_p=0.95, repetition_penalty=1.1, min_p=0.05),
+              dict(base, temperature=1.2, top_k=1024, top_p=0.95, repetition_penalty=1.2)]
+    stop_at = {(1, 9): 106, (4, 17): 1, (6, 30): 106}
+    _run_session("per-row", mode, params, stop_at, cap=24, steps=44, seed=11)
+
+
+@pytest.mark.parametrize("mode", ["after_push", "before_push"])
+@pytest.mark.parametrize("rows", [3, 12])
+def test_greedy_sessions_shared_params(mode, rows):
+    """Shared parameters with temperature 0: every row takes the greedy kernel,
+    with its polled last-chunk merge at 3 rows (64 chunks each, all resident)
+    and its ticket merge at 12. The penalty over the wrapping ring makes each
+    row's argmax move as its own tokens recur; the device ring append, the
+    stop check and the done rows are the greedy kernel's own."""
+    p = dict(temperature=0.0, top_k=64, top_p=0.95, min_p=0.0, softcap=30.0, repetition_penalty=1.3)
+    stop_at = {(1, 7): 106, (rows - 1, 15): 1}
+    if rows > 4:
+        stop_at[(5, 22)] = 106
+    _run_session("greedy", mode, [p] * rows, stop_at, cap=8, steps=30, seed=17 + rows, shared=True)
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])

@@ -81,10 +81,20 @@ def _logits(rng, kind, rows, V):
         for r in range(rows):
             x[r, rng.choice(V, 10, replace=False)] = rng.standard_normal(10).astype(np.float32) * 3
         return x
+    if kind == "maskedwide":  # more finite logits than k, the rest -inf (constrained decoding)
+        x = np.full((rows, V), -np.inf, np.float32)
+        for r in range(rows):
+            x[r, rng.choice(V, 300, replace=False)] = rng.standard_normal(300).astype(np.float32) * 3
+        return x
+    if kind == "halfmasked":  # -inf over a contiguous half of the row
+        x = (rng.standard_normal((rows, V)) * 3).astype(np.float32)
+        x[:, V // 4: V // 4 + V // 2] = -np.inf
+        return x
     raise ValueError(kind)
 
 
-KINDS = ["normal", "peaks", "ties", "plateau", "zeros", "desc", "asc", "hot", "nan", "nanwave", "masked"]
+KINDS = ["normal", "peaks", "ties", "plateau", "zeros", "desc", "asc", "hot", "nan", "nanwave", "masked",
+         "maskedwide", "halfmasked"]
 VOCABS = [262144, 262143, 200001, 152064, 100003, 40000, 16384, 16385]
 
 
