@@ -1628,6 +1628,244 @@ struct DecideShared {
     int item;
 };
 
+// ---- the double denominator's tile maps (sorted rows) ----------------------
+//
+// When a sorted row's double sum over its top k does not certify (its terms
+// span more than the 53 bits above their lowest set bit), the reference's
+// sequential sum (generation.cpp:97) has to be replayed. Inside one binade
+// of the accumulator a run of elements is a parity map (chain_math.h), and
+// maps compose. So the items are cut into tiles of block_chain's size, each
+// in kMapSub parts, and a workgroup per part composes the part's map for the
+// top kMapBins binades the sum can be in (fo_denmap_kernel, before
+// fo_decide_kernel). The decide kernel then applies one map per part; from a
+// part whose map leaves the accumulator's binade (or whose binade has no
+// map) it replays the rest of the tile with block_chain. The maps live in
+// the row's share of the tile area (fo_tiles), which the many-workgroup sort
+// has finished with by then.
+constexpr int kMapTile = kDThreads * bchain::kPer;  // items per tile: block_chain's tile
+constexpr int kMapSub = 4;                           // parts per tile, one workgroup each
+constexpr int kMapSubItems = kMapTile / kMapSub;
+constexpr int kMapThreads = 256;
+constexpr int kMapPer = kMapSubItems / kMapThreads;  // items per thread
+constexpr int kMapBins = 3;                          // binades bhi - 2 .. bhi (bhi: the sum's, plus one)
+constexpr int kMapRowGroups = 16;                    // grid rows: row r is served by grid row r % 16
+constexpr int kMapPartWords = kMapBins * 4;          // 4 u32 (e, o) per binade
+using DMap = chain::ParityMap<uint64_t>;
+constexpr uint64_t kMapCap = bchain::F64Acc::kCap;
+static_assert(kMapSubItems % kMapThreads == 0, "whole items per thread");
+static_assert(kMapTile == 4096 && kMapSub * kMapPartWords <= 256 + 1 + 4, "a tile's maps fit its share of the tile area");
+
+// Words of one row's maps.
+__host__ __device__ constexpr int64_t map_row_words(int vocab) {
+    return static_cast<int64_t>((vocab + kMapTile - 1) / kMapTile) * kMapSub * kMapPartWords;
+}
+
+// Whether a sorted row's denominator needs no replay: its certificate (the
+// parallel sum S, the lowest set bit of every term, NaN) from the meta words
+// (a NaN term makes the sum NaN: no replay either).
+__device__ __forceinline__ bool den_certified(const uint32_t* meta, double& S) {
+    S = __builtin_bit_cast(double, (static_cast<uint64_t>(meta[kMetaSumHi]) << 32) | meta[kMetaSumLo]);
+    const int minlsb = static_cast<int>(meta[kMetaMinLsb]);
+    const bool nan = meta[kMetaAnyNan] != 0u;
+    return nan || S == 0.0 || minlsb >= exp_of(S) - 51;
+}
+
+// The largest binade the sequential sum can reach: that of the parallel sum
+// S plus one (the two differ by far less than a binade).
+__device__ __forceinline__ int den_top_binade(double S) { return exp_of(S) + 1; }
+
+// Whether part `part` (tile * kMapSub + p) of row `row` needs its maps: a
+// sorted row of this pass whose sum does not certify, with items in the part.
+__device__ __forceinline__ bool map_part_needed(const DevArgs& a, int row, int part) {
+    uint32_t k;
+    if (!full_order_row(params_of(a, row), a.vocab, k) || row_done(a, row) || k <= 1u) return false;
+    const uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * kMetaWords;
+    if (meta[kMetaStatus] != (a.fo_fallback ? kStatusFallback : kStatusOk)) return false;
+    if (part * kMapSubItems >= static_cast<int>(meta[kMetaItems])) return false;
+    double S;
+    return !den_certified(meta, S);
+}
+
+// The maps of one part (block-uniform): its items' elements in [1, k)
+// (element 0, the maximum's term, starts the sum), composed for each binade
+// 2^b, b in [bhi - 2, bhi], that the sum can be in while the part is added;
+// a binade below a lower bound of the sum before the part gets a saturated
+// map (the decide kernel then replays).
+__device__ __forceinline__ void map_part(const DevArgs& a, int row, int part, uint64_t (&wmap)[2][kMapThreads / 64]) {
+    const int tid = threadIdx.x;
+    const int lane = __lane_id();
+    const int wave = tid >> 6;
+    const int V = a.vocab;
+    uint32_t k = 0;
+    (void)full_order_row(params_of(a, row), V, k);
+    const uint32_t* meta = a.fo_meta + static_cast<int64_t>(row) * kMetaWords;
+    const int G = static_cast<int>(meta[kMetaItems]);
+    double S;
+    (void)den_certified(meta, S);
+    const int i0 = part * kMapSubItems;
+    const uint32_t* pre = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
+    const float* aux = a.fo_aux + static_cast<int64_t>(row) * a.fo_items_stride;
+    uint32_t* out = a.fo_tiles + static_cast<int64_t>(row) * fo_tile_words(fo_split_tiles(V)) +
+                    static_cast<int64_t>(part) * kMapPartWords;
+    // Lower bounds of the sum before this part (terms only fall along the
+    // list): its elements times the part's first term; and the whole sum
+    // less every later element at that term (S within 2^-30 of the
+    // sequential sum, with room to spare).
+    const uint32_t e_before = min(max(pre[i0], 1u), k);
+    const double t0 = static_cast<double>(aux[i0]);
+    const double lb1 = static_cast<double>(e_before) * t0;
+    const double lb2 = S * (1.0 - 0x1p-30) - static_cast<double>(k - e_before) * t0 * (1.0 + 0x1p-30);
+    const double lb = max(lb1, lb2);
+    const int blo = lb >= 1.0 ? exp_of(lb) : 0;
+    const int bhi = den_top_binade(S);
+    // This thread's items (clamped loads: items past G hold no element).
+    uint32_t pb[kMapPer + 1];
+    uint32_t ab[kMapPer];
+    const int ib = i0 + tid * kMapPer;
+#pragma unroll
+    for (int j = 0; j <= kMapPer; ++j) pb[j] = min(pre[min(ib + j, G)], k);
+#pragma unroll
+    for (int j = 0; j < kMapPer; ++j) ab[j] = f2u(aux[min(ib + j, G - 1)]);
+    for (int slot = 0; slot < kMapBins; ++slot) {
+        const int b = bhi - (kMapBins - 1) + slot;
+        DMap tot{kMapCap, kMapCap};
+        if (b >= blo && b >= 0) {
+            const int uexp = b - 52;
+            DMap f{0, 0};
+#pragma unroll
+            for (int j = 0; j < kMapPer; ++j) {
+                const uint32_t lo = max(pb[j], 1u);
+                const uint32_t nt = pb[j + 1] > lo ? pb[j + 1] - lo : 0u;
+                uint64_t D;
+                bool tie, odd0, big;
+                chain::step_bits64(ab[j], uexp, D, tie, odd0, big);
+                f = chain::compose<uint64_t, kMapCap>(f, chain::run_map<uint64_t, kMapCap>(nt, D, tie, odd0, big));
+            }
+            const DMap x = map_wave_excl<uint64_t, kMapCap>(f);
+            if (lane == 63) {
+                const DMap wt = chain::compose<uint64_t, kMapCap>(x, f);
+                wmap[0][wave] = wt.e;
+                wmap[1][wave] = wt.o;
+            }
+            __syncthreads();
+            tot = DMap{0, 0};
+#pragma unroll
+            for (int w = 0; w < kMapThreads / 64; ++w)
+                tot = chain::compose<uint64_t, kMapCap>(tot, DMap{wmap[0][w], wmap[1][w]});
+            __syncthreads();
+        }
+        if (tid == 0) {
+            out[4 * slot + 0] = static_cast<uint32_t>(tot.e);
+            out[4 * slot + 1] = static_cast<uint32_t>(tot.e >> 32);
+            out[4 * slot + 2] = static_cast<uint32_t>(tot.o);
+            out[4 * slot + 3] = static_cast<uint32_t>(tot.o >> 32);
+        }
+    }
+}
+
+// Grid (parts, min(rows, kMapRowGroups)); grid row y serves rows y, y + 16,
+// ... (at most 64 of them: slices hold at most 256 rows), whose need the
+// lanes of wave 0 check side by side first, so a slice whose sums all
+// certify costs one round of loads per workgroup.
+__global__ __launch_bounds__(kMapThreads) void fo_denmap_kernel(DevArgs a) {
+    __shared__ uint64_t wmap[2][kMapThreads / 64];
+    __shared__ uint64_t need_rows;
+    const int lane = __lane_id();
+    const int part = static_cast<int>(blockIdx.x);
+    if ((threadIdx.x >> 6) == 0) {
+        const int r = static_cast<int>(blockIdx.y) + lane * static_cast<int>(gridDim.y);
+        const uint64_t m = __ballot(r < a.rows && map_part_needed(a, r, part));
+        if (lane == 0) need_rows = m;
+    }
+    __syncthreads();
+    uint64_t todo = need_rows;
+    while (todo) {
+        const int j = __ffsll(static_cast<unsigned long long>(todo)) - 1;
+        todo &= todo - 1ull;
+        map_part(a, static_cast<int>(blockIdx.y) + j * static_cast<int>(gridDim.y), part, wmap);
+    }
+}
+
+// The sequential double sum over elements [1, k) of a sorted row, from s =
+// the first term: the parts' maps (fo_denmap_kernel) for the accumulator's
+// binade are composed 64 parts at a time by a wave scan, which finds the
+// first part that would leave the binade (or whose binade has no map); the
+// rest of that part's tile is replayed exactly by block_chain, and the scan
+// resumes at the next tile. The parts' maps and end elements are first
+// staged in `stage` (LDS, ntiles * kMapSub * (kMapPartWords + 1) + 8
+// words). Block-uniform (block_chain holds barriers). Kept out of line:
+// inlined, it changed the decide kernel's code for every row (certified rows
+// 26 µs slower per launch of 256 C4-f32 rows).
+__device__ __attribute__((noinline)) double den_by_maps(const DevArgs& a, int row, const uint32_t* pre, const float* aux,
+                                                        int G, uint32_t k, double s2, double S, uint32_t* stage,
+                                                        bchain::Shared<kDThreads / 64>& bc) {
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = __lane_id();
+    const uint32_t* maps = a.fo_tiles + static_cast<int64_t>(row) * fo_tile_words(fo_split_tiles(a.vocab));
+    const int ntiles = (G + kMapTile - 1) / kMapTile;
+    const int nparts = ntiles * kMapSub;
+    uint32_t* pend = stage + nparts * kMapPartWords;  // end element of each part (clipped to k)
+    uint64_t* res = reinterpret_cast<uint64_t*>(stage + ((nparts * (kMapPartWords + 1) + 1) & ~1));  // scan result
+    for (int i = tid; i < nparts * kMapPartWords; i += kDThreads) stage[i] = maps[i];
+    for (int i = tid; i < nparts; i += kDThreads) pend[i] = min(pre[min((i + 1) * kMapSubItems, G)], k);
+    __syncthreads();
+    const int bhi = den_top_binade(S);
+    auto start_elem = [&](int q) { return q == 0 ? 1u : pend[q - 1]; };
+    int p = 0;  // next part; the sum holds every element before start_elem(p)
+    while (p < nparts && start_elem(p) < k) {
+        const bchain::F64Acc::Bin bn = bchain::F64Acc::binade(s2, __builtin_nan(""));
+        const int slot = bn.uexp + 52 - (bhi - (kMapBins - 1));
+        int crossing = p;  // first part not covered by a map
+        bool found = true;  // a part at `crossing` needs the replay (else: 64 parts applied)
+        if (slot >= 0 && slot < kMapBins) {
+            if (tid < 64) {
+                // Lane l: part p + l's map (identity past the last part);
+                // the scan gives each lane the composition of the parts
+                // before it, and the first lane whose part takes m past the
+                // binade's top is the crossing.
+                const int q = p + lane;
+                DMap f{0, 0};
+                if (q < nparts && start_elem(q) < k) {  // (parts past the last element have no maps written)
+                    const uint32_t* w = stage + q * kMapPartWords + 4 * slot;
+                    f = DMap{(static_cast<uint64_t>(w[1]) << 32) | w[0], (static_cast<uint64_t>(w[3]) << 32) | w[2]};
+                }
+                const DMap x = map_wave_excl<uint64_t, kMapCap>(f);
+                const uint64_t rx = chain::apply_from(x, bn.m);  // parts before lane l
+                const uint64_t ri = chain::apply_from(chain::compose<uint64_t, kMapCap>(x, f), bn.m);
+                const uint64_t out = __ballot(q < nparts && start_elem(q) < k && bn.m + ri > bn.hi);
+                const int n = min(64, nparts - p);
+                const int first = out ? __ffsll(static_cast<unsigned long long>(out)) - 1 : n;
+                const uint64_t rb = first < 64 ? wave::readlane64(rx, first) : wave::readlane64(ri, 63);
+                if (lane == 0) {
+                    res[0] = static_cast<uint64_t>(p + first);
+                    res[1] = rb;
+                    res[2] = out ? 1ull : 0ull;
+                }
+            }
+            __syncthreads();
+            crossing = static_cast<int>(res[0]);
+            found = res[2] != 0ull;
+            s2 = bchain::F64Acc::rebuild(s2, bn, bn.m + res[1]);
+            __syncthreads();  // res is read before the next round writes it
+        }
+        if (crossing >= nparts || start_elem(crossing) >= k) break;
+        if (!found) {
+            p = crossing;  // 64 parts applied, none left the binade
+            continue;
+        }
+        // Replay from part `crossing` to the end of its tile.
+        const int t = crossing / kMapSub;
+        const uint32_t tend = pend[t * kMapSub + kMapSub - 1];
+        ChainPos cp{crossing * kMapSubItems, start_elem(crossing)};
+        if (tend > cp.elem)
+            (void)bchain::block_chain<bchain::F64Acc, false, kDThreads>(pre, aux, 1.0f, G, cp, tend, s2,
+                                                                       __builtin_nan(""), bc);
+        p = (t + 1) * kMapSub;
+    }
+    __syncthreads();  // every thread has read the staged maps before the caller reuses the area
+    return s2;
+}
+
 template <typename T, typename Op>
 __device__ __forceinline__ T wave_reduce(T v, Op op) {
 #pragma unroll
@@ -1809,7 +2047,11 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         } else if (!certified) {
             ChainPos cp{0, 1};
             double s2 = static_cast<double>(p0);
-            if (k > 1) bchain::block_chain<bchain::F64Acc, false, kDThreads>(pre, aux, 1.0f, G, cp, k, s2, __builtin_nan(""), sh.bc);
+            if (k > 1 && a.fo_maps) {
+                s2 = den_by_maps(a, row, pre, aux, G, k, s2, Sp, sh.gx_ids, sh.bc);
+            } else if (k > 1) {
+                bchain::block_chain<bchain::F64Acc, false, kDThreads>(pre, aux, 1.0f, G, cp, k, s2, __builtin_nan(""), sh.bc);
+            }
             den = s2;
         }
         if (tid == 0) sh.den = den;
@@ -2327,6 +2569,11 @@ hipError_t sorted_pass(const DevArgs& a, hipStream_t stream) {
     const bool split = std::is_same<T, float>::value && !a.fo_fallback && a.fo_tiles != nullptr && !a.row_params &&
                        per64 <= kSplitMaxRows && per64 * fo_tile_words(fo_split_tiles(a.vocab)) <= a.fo_tiles_words;
     const int per = static_cast<int>(std::max<int64_t>(1, per64));
+    // The denominator's tile maps go to the tile area when it holds a slice.
+    const bool maps = a.fo_tiles != nullptr && map_row_words(a.vocab) <= fo_tile_words(fo_split_tiles(a.vocab)) &&
+                      static_cast<int64_t>(per) * fo_tile_words(fo_split_tiles(a.vocab)) <= a.fo_tiles_words &&
+                      per <= kMapRowGroups * 64 &&
+                      (a.vocab + kMapTile - 1) / kMapTile * kMapSub * (kMapPartWords + 1) + 8 <= kFoExtrasCap;
     for (int r0 = 0; r0 < a.rows; r0 += per) {
         DevArgs s = slice_rows(a, r0, std::min(per, a.rows - r0));
         s.fo_items_stride = stride;
@@ -2338,6 +2585,15 @@ hipError_t sorted_pass(const DevArgs& a, hipStream_t stream) {
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
+        s.fo_maps = 0;
+        if (maps) {
+            const int parts = (a.vocab + kMapTile - 1) / kMapTile * kMapSub;
+            const int groups = std::min(s.rows, kMapRowGroups);
+            hipLaunchKernelGGL(fo_denmap_kernel, dim3(parts, groups), dim3(kMapThreads), 0, stream, s);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            s.fo_maps = 1;
+        }
         hipLaunchKernelGGL((fo_decide_kernel<T, true>), dim3(s.rows), dim3(kDThreads), 0, stream, s);
         e = hipGetLastError();
         if (e != hipSuccess) return e;

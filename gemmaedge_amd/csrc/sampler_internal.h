@@ -86,6 +86,9 @@ struct DevArgs {
     // pass flagged. fo_row0: the first call row of a slice of rows.
     int32_t fo_fallback;
     int32_t fo_row0;
+    // fo_maps: the sorted rows' denominator tile maps are in fo_tiles (set by
+    // the host for the decide kernel of a slice whose map kernel ran).
+    int32_t fo_maps;
 };
 
 // Full-order path sizes.

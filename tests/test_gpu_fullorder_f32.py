@@ -59,6 +59,21 @@ def test_wide_range_rows_replay_the_double_denominator(sampler):
         _check(sampler, w)
 
 
+@pytest.mark.parametrize("scale", [1.0, 3.0, 8.0, 20.0])
+def test_denominator_tile_maps(sampler, scale):
+    # Sums that do not certify take one parity map per 4096-item tile and an
+    # exact replay of each tile where the accumulator crosses a binade: wide
+    # logit ranges (many crossings, terms far below the sum's ulp), k cutting
+    # a tile, and k below, at and above one tile.
+    rng = np.random.default_rng(int(scale * 10) + 7)
+    x = (rng.standard_normal((4, W.VOCAB)) * scale).astype(np.float32)
+    for k in (0, 1500, 4096, 5000, 100000):
+        for T in (1.0, 0.6):
+            w = small_workload(f"maps-s{scale}-k{k}-T{T}", x, dict(temperature=T, top_k=k, top_p=1.0, softcap=30.0),
+                               uniforms=np.array([0.3, 0.999, 0.6, 0.9999], np.float32))
+            _check(sampler, w)
+
+
 def test_special_values(sampler):
     rng = np.random.default_rng(42)
     V = 5003
