@@ -154,3 +154,53 @@ def test_stream_alternating_shapes(sampler):
     seq = [262144, 16384, 152064, 262144, 40000, 100003, 262144, 16385, 200001, 262144]
     for i, V in enumerate(seq):
         _check(sampler, _case(rng, 900 + i, kind="peaks", V=V))
+
+
+def test_stream_mixed_shapes_in_one_graph(sampler):
+    # Launches of different shapes on one handle captured back to back in one
+    # graph (no host wait between kernels), the graph replayed three times:
+    # every call's list area must be zero when it starts, whichever call of
+    # which shape ran before it, and every replay must give the same outputs.
+    import ctypes
+
+    import torch
+
+    from gemmaedge_amd import sampler as S
+
+    rng = np.random.default_rng(555)
+    seq = [262144, 16384, 152064, 262144, 40000, 262144, 100003, 16385]
+    cases = [_case(rng, 1200 + i, kind=str(rng.choice(["normal", "peaks", "ties"])), V=V) for i, V in enumerate(seq)]
+    dev = []
+    for w in cases:
+        logits, hist, offs, uni = W.to_device(w)
+        outs = (torch.empty(w.rows, dtype=torch.int32, device="cuda"),
+                torch.empty(w.rows, dtype=torch.float32, device="cuda"),
+                torch.empty(w.rows, dtype=torch.int32, device="cuda"))
+        a = S.SampleArgs()
+        a.logits, a.dtype, a.rows, a.vocab, a.row_stride = logits.data_ptr(), S.GE_DTYPE_F32, w.rows, w.vocab, w.vocab
+        a.params = S.SamplingConfig(**w.params).params()
+        if hist is not None:
+            a.history, a.history_offsets = hist.data_ptr(), offs.data_ptr()
+        a.uniforms = uni.data_ptr()
+        a.tokens_out, a.probs_out, a.flags_out = (t.data_ptr() for t in outs)
+        dev.append((w, (logits, hist, offs, uni), outs, a))
+    lib = S.load_library()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            cs = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for _, _, _, a in dev:
+                assert lib.ge_sample(sampler._h, cs, ctypes.byref(a)) == 0, S.last_error()
+    torch.cuda.synchronize()
+    oras = [run_oracle(w) for w, _, _, _ in dev]
+    for rep in range(3):
+        for _, _, outs, _ in dev:
+            outs[0].fill_(-7)
+        g.replay()
+        _ = sum(float(x[0].float().sum()) for _, x, _, _ in dev)  # eager work between replays
+        torch.cuda.synchronize()
+        for (w, _, outs, _), ora in zip(dev, oras):
+            gpu = tuple(x.cpu().numpy() for x in outs)
+            assert_parity(w, gpu, ora, f"{w.name} replay {rep}")
