@@ -880,8 +880,7 @@ __global__ __launch_bounds__(kThreads) void fo_sort_kernel(DevArgs a) {
 #pragma unroll
         for (int u = 0; u < kSortUnroll; ++u) {
             const int i = base + 64 * u + lane;
-            const bool act = i < whi;
-            const int ic = min(i, whi - 1);  // clamped: no conditional load (unused when !act)
+            const int ic = min(i, whi - 1);  // clamped: no conditional load (unused when i >= whi)
             cv[u] = ld_l2(s + ic);
             pv[u] = ld_l2(s + max(ic - 1, 0));
         }
@@ -1608,6 +1607,19 @@ constexpr int kDThreads = 512;
 constexpr int kDWaves = kDThreads / 64;
 constexpr int kStage = 8192;  // items whose count and probability are staged in LDS
 
+// bf16 rows: the token scan's speculative batch counts (decide step 5s).
+constexpr int kSpecGroups = 8;           // candidate groups, at most
+constexpr int kSpecBefore = 2;           // items picked: the crossing item - 2 ..
+constexpr int kSpecAfter = 3;            //   .. the crossing item + 3
+constexpr int kSpecBatch = kDThreads * 32;  // tokens per bf16 token-scan batch
+constexpr int kSpecBatches = 32;         // batches counted (rows up to 32 x 16384 tokens)
+constexpr int kSpecBlock = 64 * 32;      // tokens a counting wave takes per round
+constexpr uint32_t kSpecWaves = 0xFEu;   // the counting waves (wave 1 picks the groups)
+constexpr int kSpecCounters = __builtin_popcount(kSpecWaves);
+static_assert(kSpecBefore + 1 + kSpecAfter <= kSpecGroups, "the picked items fit the candidates");
+static_assert((kSpecWaves & 3u) == 2u, "wave 0 draws, wave 1 picks and counts");
+static_assert(kSpecBatch % kSpecBlock == 0, "a counting round lies in one batch");
+
 struct DecideShared {
     union {
         struct {
@@ -1626,6 +1638,17 @@ struct DecideShared {
     uint32_t blo, bhi, nan_group, near, gkey;
     int32_t token;
     int item;
+    // bf16 rows: the token scan's speculative batch counts (see the decide
+    // kernel's step 6s), made by waves 1.. while wave 0 draws.
+    uint32_t spec_cnt[kSpecGroups][kSpecBatches];
+    uint32_t spec_key[kSpecGroups], spec_blo[kSpecGroups], spec_bhi[kSpecGroups];
+    uint32_t spec_bdone[kSpecBatches];  // blocks of each batch counted
+    uint32_t spec_ulo, spec_uhi;  // the candidates' bins lie in [spec_ulo, spec_uhi]
+    uint32_t spec_n;              // candidate groups (0: none)
+    uint32_t spec_fwd;            // the predicted scan direction
+    uint32_t spec_nbat;           // batches to count, from that direction's end
+    uint32_t spec_ready;          // wave 1 has written the candidates
+    uint32_t spec_stop;           // wave 0 has drawn: the count pass stops
 };
 
 // ---- the double denominator's tile maps (sorted rows) ----------------------
@@ -2100,6 +2123,17 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     first_low = wave_reduce(first_low, [](int x, int y) { return min(x, y); });
     __syncthreads();  // every reader of sh.ired above is done
     if (lane == 0) sh.ired[wave] = first_low;
+    // step 5s (bf16 rows): the counts start at zero, nothing published
+    const bool spec_on = !kSorted && !any_nan && V <= kSpecBatches * kSpecBatch;
+    if (!kSorted) {
+        for (int i = tid; i < kSpecGroups * kSpecBatches; i += kDThreads) (&sh.spec_cnt[0][0])[i] = 0u;
+        if (tid < kSpecBatches) sh.spec_bdone[tid] = 0u;
+        if (tid == 0) {
+            sh.spec_n = 0u;
+            sh.spec_ready = 0u;
+            sh.spec_stop = 0u;
+        }
+    }
     __syncthreads();
     // Top-p cut, draw and near-boundary flag, then the selected value's
     // group. bf16 rows (a few thousand items at most): wave 0 alone, over LDS
@@ -2255,9 +2289,246 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             sh.forward = (rank <= (total - 1) / 2) ? 1u : 0u;
             sh.token = -1;
         }
-        // (the LDS staging area is no longer read; gx_ids reuses it)
+        // (the LDS staging area is no longer read, once step 5s has picked;
+        // gx_ids reuses it)
+        if (!kSorted && spec_on)
+            while (__builtin_amdgcn_readfirstlane(
+                       __hip_atomic_load(&sh.spec_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0)
+                __builtin_amdgcn_s_sleep(2);
         for (uint32_t x = xs + static_cast<uint32_t>(lane); x < xe; x += 64)
             sh.gx_ids[x - xs] = composite_index(extras[x]);
+    };
+
+    // 5s. bf16 rows: while wave 0 draws, the other waves count, per batch of
+    //     the token scan below, the tokens of the groups the draw is likely
+    //     to select. Wave 1 finds the item where the exact cumulative
+    //     probability crosses u * min(top_p, mass through the cuts) (the f32
+    //     chains end within a small fraction of an item of it), takes the
+    //     groups of the items around it, and from the element there predicts
+    //     the scan's direction and how many batches it passes before the
+    //     token (with a margin). The counting waves then count each group's
+    //     unpenalised tokens in those batches, from the scan's end inward, as
+    //     the scan's match would. The scan skips the counted batches before
+    //     the token's by those counts (plus the group's penalised ids there),
+    //     so it finds the token it would find anyway; a group not among the
+    //     candidates, or batches the count did not finish before wave 0 did,
+    //     are scanned as before. group() waits for the pick before it
+    //     reuses the LDS copies of the items.
+    auto spec_pick = [&](const auto& iv) {  // wave 1
+        int fl = lane < kDWaves ? sh.ired[lane] : INT_MAX;
+        fl = wave_reduce(fl, [](int x, int y) { return min(x, y); });
+        uint32_t keff = k;
+        if (q0 < minimum) keff = 1;
+        else if (fl != INT_MAX) keff = min(keff, pre[fl]);
+        const double u = static_cast<double>(a.uniforms[row]);
+        const double tp = static_cast<double>(p.top_p);
+        auto mass = [&](int i) -> double {  // i < G
+            const uint32_t st = min(iv.start(i), keff), en = min(iv.start(i + 1), keff);
+            return static_cast<double>(en - st) * static_cast<double>(iv.addend(i));
+        };
+        // the items in 64 runs, one per lane; then the crossing run, 64 at a time
+        const int B = (G + 63) / 64;
+        const int ib = min(lane * B, G), ie = min(ib + B, G);
+        double part = 0.0;
+        for (int i0 = ib; i0 < ie; i0 += 8) {
+            double m[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) m[j] = mass(min(i0 + j, ie - 1));  // clamped: no conditional load
+#pragma unroll
+            for (int j = 0; j < 8; ++j) part += i0 + j < ie ? m[j] : 0.0;
+        }
+        const double incl = wave::incl_f64(part);
+        const double total = wave::readlane_f64(incl, 63);
+        const double c = u * (total >= tp ? tp : total);
+        const uint64_t bl = __ballot(ib < ie && incl >= c);
+        int ic = -1;
+        double before = 0.0;
+        if (bl) {
+            const int L = static_cast<int>(__builtin_ctzll(bl));
+            double base = wave::readlane_f64(incl - part, L);
+            const int lb = L * B, le = min(lb + B, G);
+            for (int i0 = lb; i0 < le; i0 += 64) {
+                const int i = i0 + lane;
+                const double mi = i < le ? mass(i) : 0.0;
+                const double inc = base + wave::incl_f64(mi);
+                const uint64_t b = __ballot(i < le && inc >= c);
+                if (b) {
+                    const int f = static_cast<int>(__builtin_ctzll(b));
+                    ic = i0 + f;
+                    before = wave::readlane_f64(inc - mi, f);
+                    break;
+                }
+                base = wave::readlane_f64(inc, 63);
+            }
+            if (ic < 0) ic = le - 1;
+        }
+        uint32_t n = 0, ulo = kHighBin + 1, uhi = 0, fwd = 1, nbat = 0;
+        if (ic >= 0) {
+            const float cap = p.softcap;
+            auto item_key = [&](int i) { return order_key(u2f(static_cast<uint32_t>(items[i] >> 32))); };
+            // distinct keys of items ic - kSpecBefore .. ic + kSpecAfter, descending
+            const int ij = ic - kSpecBefore + lane;
+            const bool in = lane <= kSpecBefore + kSpecAfter && ij >= 0 && ij < G;
+            const uint32_t kj = in ? item_key(min(max(ij, 0), G - 1)) : 0u;
+            const uint32_t kp = __shfl_up(kj, 1);
+            const bool take = in && kj != kKeyNaN && !(lane > 0 && ij > 0 && kp == kj);
+            const uint64_t tm = __ballot(take);
+            n = static_cast<uint32_t>(__popcll(tm));
+            if (n > 0) {
+                const uint32_t khi = wave::readlane(kj, static_cast<int>(__builtin_ctzll(tm)));
+                const uint32_t klo = wave::readlane(kj, 63 - static_cast<int>(__builtin_clzll(tm)));
+                // the bins of keys [klo, khi]: [r0, r1)
+                const uint32_t r0 =
+                    wave_partition_point(kLowBin, kHighBin + 1, [&](uint32_t b) { return bin_key(b, cap) < klo; });
+                const uint32_t r1 =
+                    wave_partition_point(r0, kHighBin + 1, [&](uint32_t b) { return bin_key(b, cap) <= khi; });
+                const bool narrow = r1 - r0 <= 64;
+                const uint32_t bk = narrow && r0 + lane < r1 ? bin_key(r0 + lane, cap) : 0xFFFFFFFFu;
+                uint64_t rest = tm;
+                for (uint32_t c = 0; c < n; ++c) {
+                    const int l = static_cast<int>(__builtin_ctzll(rest));
+                    rest &= rest - 1;
+                    const uint32_t key = wave::readlane(kj, l);
+                    uint32_t blo, bhi;
+                    if (narrow) {  // bin_key is monotone: count the bins below / through key
+                        blo = r0 + static_cast<uint32_t>(__popcll(__ballot(r0 + lane < r1 && bk < key)));
+                        bhi = r0 + static_cast<uint32_t>(__popcll(__ballot(r0 + lane < r1 && bk <= key))) - 1;
+                    } else {
+                        blo = wave_partition_point(r0, r1, [&](uint32_t b) { return bin_key(b, cap) < key; });
+                        bhi = wave_partition_point(blo, r1, [&](uint32_t b) { return bin_key(b, cap) <= key; }) - 1;
+                    }
+                    if (lane == 0) {
+                        sh.spec_key[c] = key;
+                        sh.spec_blo[c] = blo;
+                        sh.spec_bhi[c] = bhi;
+                    }
+                    if (blo <= bhi) {
+                        ulo = min(ulo, blo);
+                        uhi = max(uhi, bhi);
+                    }
+                }
+            }
+            // The predicted element, its rank in its group (the items of
+            // one key, within a few items of ic), and the batches the scan
+            // would pass before reaching it: the members are spread over the
+            // row, so the want-th from the scan's end lies near V * (want + 1)
+            // / (total + 1). Margins: the chains' drift (about 1.5e-4 of
+            // probability, in elements of this item) and three binomial
+            // standard deviations, plus one batch. When the drift leaves the
+            // direction open, every batch.
+            const uint32_t key = item_key(ic);
+            const uint64_t mb = __ballot(ic - 1 - lane >= 0 && item_key(max(ic - 1 - lane, 0)) == key);
+            const uint64_t ma = __ballot(ic + 1 + lane < G && item_key(min(ic + 1 + lane, G - 1)) == key);
+            const int is = ic - (mb == ~0ull ? 64 : static_cast<int>(__builtin_ctzll(~mb)));
+            const int ie2 = ic + (ma == ~0ull ? 64 : static_cast<int>(__builtin_ctzll(~ma)));
+            const double q = static_cast<double>(aux[ic]);
+            const uint32_t cnt_ic = pre[ic + 1] - pre[ic];
+            double off = q > 0.0 ? (c - before) / q : 0.0;
+            off = off < 0.0 ? 0.0 : off;
+            const uint32_t within = off >= static_cast<double>(cnt_ic) ? cnt_ic - 1 : static_cast<uint32_t>(off);
+            const uint32_t first = pre[is], tot = pre[ie2 + 1] - first;
+            const uint32_t rank = pre[ic] + within - first;
+            fwd = rank <= (tot - 1) / 2 ? 1u : 0u;
+            const uint32_t want = fwd ? rank : tot - 1 - rank;
+            const double drift = q > 0.0 ? 1.5e-4 / q : static_cast<double>(tot);
+            const double mid = (static_cast<double>(tot) - 1.0) * 0.5;
+            const bool sure = static_cast<double>(rank) + drift <= mid || static_cast<double>(rank) - drift > mid;
+            const double pf = (static_cast<double>(want) + 1.0 + drift) / (static_cast<double>(tot) + 1.0);
+            const double pc = pf < 1.0 ? pf : 1.0;
+            const double hi = pc + 3.0 * __builtin_sqrt(pc * (1.0 - pc) / (static_cast<double>(tot) + 1.0));
+            const int nb = (V + kSpecBatch - 1) / kSpecBatch;
+            const double bats = hi * static_cast<double>(V) / kSpecBatch + 1.0;
+            // a direction the drift leaves open: every batch, for either end
+            nbat = !sure || bats >= static_cast<double>(nb) ? static_cast<uint32_t>(nb) : static_cast<uint32_t>(bats);
+        }
+        if (lane == 0) {
+            sh.spec_ulo = ulo;
+            sh.spec_uhi = uhi;
+            sh.spec_n = n;
+            sh.spec_fwd = fwd;
+            sh.spec_nbat = nbat;
+            __hip_atomic_store(&sh.spec_ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    };
+    auto spec_count = [&]() {  // the counting waves
+        while (__builtin_amdgcn_readfirstlane(
+                   __hip_atomic_load(&sh.spec_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0)
+            __builtin_amdgcn_s_sleep(2);
+        const uint32_t n = sh.spec_n;
+        const uint32_t ulo = sh.spec_ulo, uhi = sh.spec_uhi;
+        const bool fwd = sh.spec_fwd != 0;
+        const int nb = (V + kSpecBatch - 1) / kSpecBatch;
+        constexpr int kPerBatch = kSpecBatch / kSpecBlock;
+        const int nblk = static_cast<int>(sh.spec_nbat) * kPerBatch;  // blocks counted, from the scan's end
+        if (n == 0) return;
+        const uint32_t span = uhi - ulo;  // (no bin passes when every range is empty: ulo > uhi)
+        uint32_t cb[kSpecGroups], ch[kSpecGroups];
+#pragma unroll
+        for (int c = 0; c < kSpecGroups; ++c) {
+            cb[c] = c < static_cast<int>(n) ? sh.spec_blo[c] : 1u;
+            ch[c] = c < static_cast<int>(n) ? sh.spec_bhi[c] : 0u;
+        }
+        const uint16_t* rowp = static_cast<const uint16_t*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
+        const bool vec = a.vec_ok != 0;
+        auto block_of = [&](int j) { return fwd ? j : nb * kPerBatch - 1 - j; };
+        auto load32 = [&](int j, uint32_t* w, uint32_t& valid) {
+            const int lo = block_of(j) * kSpecBlock + lane * 32;
+            valid = 0;
+            if (vec && lo + 32 <= V) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(rowp + lo + q * 8);
+                    w[4 * q + 0] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+                }
+                valid = 0xFFFFFFFFu;
+            } else {
+                for (int h = 0; h < 16; ++h) w[h] = 0;
+                for (int h = 0; h < 32; ++h) {
+                    if (lo + h < V) {
+                        w[h >> 1] |= static_cast<uint32_t>(rowp[lo + h]) << ((h & 1) * 16);
+                        valid |= 1u << h;
+                    }
+                }
+            }
+        };
+        const int slot = __builtin_popcount(kSpecWaves & ((1u << wave) - 1u));
+        uint32_t cur[16], nxt[16];
+        uint32_t cval = 0, nval = 0;
+        if (slot < nblk) load32(slot, cur, cval);
+        for (int j = slot; j < nblk; j += kSpecCounters) {
+            if (__builtin_amdgcn_readfirstlane(
+                    __hip_atomic_load(&sh.spec_stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) != 0)
+                break;
+            const int blk = block_of(j);
+            const int lo = blk * kSpecBlock + lane * 32;
+            if (j + kSpecCounters < nblk) load32(j + kSpecCounters, nxt, nval);
+            uint32_t hits = 0;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                if (bin_of(cur[q] & 0xFFFFu) - ulo <= span) hits |= 1u << (2 * q);
+                if (bin_of(cur[q] >> 16) - ulo <= span) hits |= 2u << (2 * q);
+            }
+            hits &= cval;
+            if (pen && hits) hits &= ~bitmap[lo >> 5];  // 32 tokens at a multiple of 32: one word
+            const int batch = blk / kPerBatch;
+            while (hits) {
+                const int h = __builtin_ctz(hits);
+                hits &= hits - 1u;
+                uint32_t wv = 0;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) wv = (h >> 1) == q ? cur[q] : wv;
+                const uint32_t bin = bin_of((h & 1) ? wv >> 16 : wv & 0xFFFFu);
+                int c = -1;
+#pragma unroll
+                for (int cc = 0; cc < kSpecGroups; ++cc)
+                    if (bin >= cb[cc] && bin <= ch[cc]) c = cc;
+                if (c >= 0) atomicAdd(&sh.spec_cnt[c][batch], 1u);
+            }
+            if (lane == 0) atomicAdd(&sh.spec_bdone[batch], 1u);  // after this block's counts (LDS order)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) cur[q] = nxt[q];
+            cval = nval;
+        }
     };
     if constexpr (kSorted) {
         // Every value below is uniform across the block (block_chain's
@@ -2361,6 +2632,8 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         }
         if (wave == 0) group(GlobalView{pre, aux}, d);
     } else if (wave == 0) {
+        // the draw's serial chains first, when the counting waves share its SIMD
+        if (spec_on) __builtin_amdgcn_s_setprio(3);
         if (G <= kStage) {
             const LdsView v{sh.st.pre, sh.st.add};
             group(v, draw_wave(v));
@@ -2368,6 +2641,14 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             const GlobalView v{pre, aux};
             group(v, draw_wave(v));
         }
+        if (spec_on) __builtin_amdgcn_s_setprio(0);
+        if (spec_on && lane == 0) __hip_atomic_store(&sh.spec_stop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else if (spec_on && ((kSpecWaves >> wave) & 1u)) {
+        if (wave == 1) {
+            if (G <= kStage) spec_pick(LdsView{sh.st.pre, sh.st.add});
+            else spec_pick(GlobalView{pre, aux});
+        }
+        spec_count();
     }
     __syncthreads();
 
@@ -2457,13 +2738,36 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             return mm;
         };
         const int nb = (V + kBatch - 1) / kBatch;
+        // Batches the speculative counts (step 5s) show to hold fewer than
+        // `want` more tokens of the group are skipped.
+        int bi0 = 0;
+        if constexpr (!kF32) {
+            static_assert(kF32 || kBatch == kSpecBatch, "the counts are per token-scan batch");
+            if (spec_on && !nan_group) {
+                int c = -1;
+                for (uint32_t cc = 0; cc < sh.spec_n; ++cc)
+                    if (sh.spec_key[cc] == gkey) c = static_cast<int>(cc);
+                if (c >= 0) {
+                    while (bi0 + 1 < nb) {
+                        const int batch = fwd ? bi0 : nb - 1 - bi0;
+                        if (sh.spec_bdone[batch] != static_cast<uint32_t>(kSpecBatch / kSpecBlock)) break;
+                        const uint32_t b0 = static_cast<uint32_t>(batch * kBatch);
+                        const uint32_t b1 = static_cast<uint32_t>(min((batch + 1) * kBatch, V));
+                        const uint32_t cnt = sh.spec_cnt[c][batch] + gx_in(b0, b1);
+                        if (want < cnt) break;
+                        want -= cnt;
+                        ++bi0;
+                    }
+                }
+            }
+        }
         uint32_t cur[kW], nxt[kW];
         uint32_t cvalid = 0, nvalid = 0;
         {
-            const int batch = fwd ? 0 : nb - 1;
+            const int batch = fwd ? bi0 : nb - 1 - bi0;
             load16(batch * kBatch + tid * kPer, cur, cvalid);
         }
-        for (int bi = 0; bi < nb; ++bi) {
+        for (int bi = bi0; bi < nb; ++bi) {
             const int batch = fwd ? bi : nb - 1 - bi;
             const int lo = batch * kBatch + tid * kPer;
             if (bi + 1 < nb) {

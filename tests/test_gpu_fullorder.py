@@ -270,3 +270,56 @@ def test_values_with_more_than_32768_tokens(sampler):
         w = small_workload(f"spill-T{T}-p{p}", x, dict(temperature=T, top_k=0, top_p=p, softcap=30.0),
                            uniforms=W.mt_uniforms(int(T * 10), x.shape[0]), dtype="bf16")
         _check(sampler, w)
+
+
+def test_scan_skips_batches_by_speculative_counts(sampler):
+    """bf16 rows of many token-scan batches (16384 tokens each) where the
+    draw lands where the decide kernel's idle waves predicted, so the token
+    scan starts at a later batch from their per-batch counts: narrow N(0, 0.1)
+    rows (every group near the draw is counted), a vocabulary whose last batch
+    is partial, penalised ids inside the counted batches (the bitmap masks
+    them and the extras run adds those of the selected value back), heavy ties
+    (groups of thousands of tokens, penalised ones among them), cuts that end
+    the mass early (min-p, top-p) and draws at both ends (u = 0, u -> 1)."""
+    rng = np.random.default_rng(31)
+    u_edge = np.array([0.0, float(np.float32(1 - 2**-24)), 0.5, 0.25, 0.75, 0.999], np.float32)
+    for V in (W.VOCAB, 100003):
+        x = (rng.standard_normal((6, V)) * 0.1).astype(np.float32)
+        x[3] = np.round(x[3] * 40) / 40  # ~30 distinct values
+        xb = _bf16(x)
+        H = 2000
+        hist = rng.integers(0, V, size=6 * H).astype(np.int32)
+        offs = (np.arange(7) * H).astype(np.int32)
+        for pen in (1.0, 1.3, 0.8):
+            for top_p, min_p in ((0.9, 0.0), (1.0, 0.0), (0.95, 0.5), (0.3, 0.0)):
+                for uni in (W.mt_uniforms(int(pen * 10) + int(top_p * 100) + V % 7, 6), u_edge):
+                    w = small_workload(f"spec-V{V}-r{pen}-p{top_p}-m{min_p}", xb,
+                                       dict(temperature=1.3, top_k=0, top_p=top_p, min_p=min_p, softcap=30.0,
+                                            repetition_penalty=pen),
+                                       history=hist, offsets=offs, uniforms=uni, dtype="bf16")
+                    _check(sampler, w)
+
+
+def test_scan_skips_batches_on_unaligned_rows(sampler):
+    # a 2-byte row offset: the counting waves and the scan take scalar loads
+    import torch
+
+    from gemmaedge_amd import SamplingConfig
+
+    rng = np.random.default_rng(32)
+    V = 70001
+    x = _bf16((rng.standard_normal((4, V)) * 0.1).astype(np.float32))
+    flat = torch.from_numpy(np.concatenate([[0], x.ravel()]).astype(np.uint16).view(np.int16)).cuda()
+    logits = flat[1:].view(torch.bfloat16).view(4, V)
+    hist = rng.integers(0, V, size=4 * 500).astype(np.int32)
+    offs = (np.arange(5) * 500).astype(np.int32)
+    uni = W.mt_uniforms(33, 4)
+    cfg = SamplingConfig(temperature=1.3, top_k=0, top_p=0.9, softcap=30.0, repetition_penalty=1.2)
+    tokens, probs, _ = sampler.sample(logits, cfg, uniforms=torch.from_numpy(uni).cuda(),
+                                      history=torch.from_numpy(hist).cuda(),
+                                      history_offsets=torch.from_numpy(offs).cuda())
+    torch.cuda.synchronize()
+    ora = O.run(x, O.make_params(temperature=1.3, top_k=0, top_p=0.9, softcap=30.0, repetition_penalty=1.2),
+                history=hist, offsets=offs, uniforms=uni)
+    assert np.array_equal(tokens.cpu().numpy(), ora.tokens)
+    assert np.array_equal(probs.cpu().numpy().view(np.uint32), ora.probs.view(np.uint32))
