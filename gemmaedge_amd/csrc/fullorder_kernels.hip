@@ -2683,7 +2683,10 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             while (b0 < b1) { const uint32_t m = (b0 + b1) >> 1; if (sh.gx_ids[m] < hi) b0 = m + 1; else b1 = m; }
             return b0 - a0;
         };
-        auto load16 = [&](int lo, uint32_t* w, uint32_t& valid) {
+        // Any batch: its words, the valid tokens, and the history bitmap's
+        // word over them.
+        auto load16 = [&](int lo, uint32_t* w, uint32_t& valid, uint32_t& bw) {
+            bw = pen ? bitmap[min(lo, V - 1) >> 5] : 0u;  // clamped: no conditional load
             valid = 0;
             if (vec && lo + kPer <= V) {
 #pragma unroll
@@ -2703,12 +2706,24 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                 }
             }
         };
+        // A batch wholly inside a 16-byte aligned row: a fixed set of loads
+        // with no branch around them. The bitmap is all zero when no history
+        // applies: its first word serves.
+        auto load_full = [&](int lo, uint32_t* w, uint32_t& valid, uint32_t& bw) {
+            bw = bitmap[pen ? lo >> 5 : 0];
+#pragma unroll
+            for (int q = 0; q < kW / 4; ++q) {
+                const uint4 v = *reinterpret_cast<const uint4*>(rowp + lo + q * kPerVec);
+                w[4 * q + 0] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+            }
+            valid = kPer == 32 ? 0xFFFFFFFFu : 0xFFFFu;
+        };
         // Group members among the 16 tokens at lo (bf16: not counting the
         // penalised ones, which the extras run supplies).
-        auto match16 = [&](int lo, const uint32_t* w, uint32_t valid) -> uint32_t {
+        auto match16 = [&](int lo, const uint32_t* w, uint32_t valid, uint32_t bw) -> uint32_t {
             uint32_t mm = 0;
             // kPer (<= 32) tokens at a multiple of kPer lie in one bitmap word
-            const uint32_t pw = (pen && valid) ? (bitmap[lo >> 5] >> (lo & 31)) & valid : 0u;
+            const uint32_t pw = (pen && valid) ? (bw >> (lo & 31)) & valid : 0u;
             if constexpr (kF32) {
 #pragma unroll
                 for (int h = 0; h < kPer; ++h) {
@@ -2720,7 +2735,13 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                 if (!nan_group) {
                     for (uint32_t b = pw; b; b &= b - 1u) {
                         const int h = __builtin_ctz(b);
-                        const float f = penalize(softcap(load_value(rowp, lo + h), cap), rpen);
+                        // the token's value from the loaded words (a select
+                        // chain: a per-lane index into registers)
+                        uint32_t wv = 0;
+#pragma unroll
+                        for (int q = 0; q < kW; ++q) wv = (sizeof(T) == 4 ? h : h >> 1) == q ? w[q] : wv;
+                        const float x = sizeof(T) == 4 ? u2f(wv) : u2f(((wv >> ((h & 1) * 16)) & 0xFFFFu) << 16);
+                        const float f = penalize(softcap(x, cap), rpen);
                         if (order_key(f) == gkey) mm |= 1u << h;
                     }
                 }
@@ -2761,20 +2782,11 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                 }
             }
         }
-        uint32_t cur[kW], nxt[kW];
-        uint32_t cvalid = 0, nvalid = 0;
-        {
-            const int batch = fwd ? bi0 : nb - 1 - bi0;
-            load16(batch * kBatch + tid * kPer, cur, cvalid);
-        }
-        for (int bi = bi0; bi < nb; ++bi) {
-            const int batch = fwd ? bi : nb - 1 - bi;
-            const int lo = batch * kBatch + tid * kPer;
-            if (bi + 1 < nb) {
-                const int nbatch = fwd ? bi + 1 : nb - 2 - bi;
-                load16(nbatch * kBatch + tid * kPer, nxt, nvalid);
-            }
-            const uint32_t mm = match16(lo, cur, cvalid);
+        auto batch_lo = [&](int bi) { return (fwd ? bi : nb - 1 - bi) * kBatch + tid * kPer; };
+        // One batch; true when it holds the token (the scan ends there).
+        auto scan_batch = [&](int bi, const uint32_t* w, uint32_t valid, uint32_t bw) -> bool {
+            const int lo = batch_lo(bi);
+            const uint32_t mm = match16(lo, w, valid, bw);
             const uint32_t hi = static_cast<uint32_t>(min(lo + kPer, V));
             uint32_t cnt = static_cast<uint32_t>(__popc(mm));
             if constexpr (!kF32) cnt += lo < V ? gx_in(static_cast<uint32_t>(lo), hi) : 0u;
@@ -2787,7 +2799,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                     int found = -1;
                     for (int s2 = 0; s2 < kPer && found < 0; ++s2) {
                         const int h = fwd ? s2 : kPer - 1 - s2;
-                        if (!((cvalid >> h) & 1u)) continue;
+                        if (!((valid >> h) & 1u)) continue;
                         const uint32_t idx = static_cast<uint32_t>(lo + h);
                         uint32_t here = (mm >> h) & 1u;
                         if constexpr (!kF32) {
@@ -2800,11 +2812,53 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                     }
                     sh.token = found;
                 }
-                break;
+                return true;
             }
             want -= tot;
-            for (int h = 0; h < kW; ++h) cur[h] = nxt[h];
-            cvalid = nvalid;
+            return false;
+        };
+        // Scan indices [b0, b1) with two buffers in turn, the next batch's
+        // loads in flight while this one is matched and scanned, and no
+        // register copy between batches.
+        auto pipelined = [&](auto&& loader, int b0, int b1) -> bool {
+            if (b0 >= b1) return false;
+            uint32_t wa[kW], wb[kW];
+            uint32_t va = 0, vb = 0, bwa = 0, bwb = 0;
+            loader(batch_lo(b0), wa, va, bwa);
+            for (int bi = b0; bi < b1; bi += 2) {
+                // (distinct markers keep the compiler from folding the two
+                // halves into one loop body over a single buffer)
+                asm volatile("; token scan: buffer b in flight");
+                if (bi + 1 < b1) loader(batch_lo(bi + 1), wb, vb, bwb);
+                if (scan_batch(bi, wa, va, bwa)) return true;
+                if (bi + 1 >= b1) break;
+                asm volatile("; token scan: buffer a in flight");
+                if (bi + 2 < b1) loader(batch_lo(bi + 2), wa, va, bwa);
+                if (scan_batch(bi + 1, wb, vb, bwb)) return true;
+            }
+            return false;
+        };
+        if (vec) {
+            // the last batch (scan index nb - 1 forward, 0 backward) may be
+            // partial: it takes the general loads, the full ones the fixed set
+            const bool partial = V % kBatch != 0;
+            int b0 = bi0, b1 = nb;
+            bool done = false;
+            if (partial && !fwd && b0 == 0) {
+                uint32_t w[kW], v = 0, bw = 0;
+                load16(batch_lo(0), w, v, bw);
+                done = scan_batch(0, w, v, bw);
+                b0 = 1;
+            }
+            if (partial && fwd) b1 = nb - 1;
+            if (!done) done = pipelined(load_full, b0, b1);
+            if (!done && partial && fwd && bi0 <= nb - 1) {
+                uint32_t w[kW], v = 0, bw = 0;
+                load16(batch_lo(nb - 1), w, v, bw);
+                (void)scan_batch(nb - 1, w, v, bw);
+            }
+        } else {
+            (void)pipelined(load16, bi0, nb);
         }
     }
     __syncthreads();
