@@ -491,14 +491,18 @@ GE_CHAIN_HD uint64_t asc_run_f32(double& s, double a, uint64_t n, double thr, bo
             continue;
         }
         const uint64_t rem = n - done;
-        const uint64_t jv = D ? static_cast<uint64_t>((kHiF - b.m) / D) : kNone;  // steps that stay in the binade
-        uint64_t jh = kNone;                                                       // steps to reach thr
+        // j = min(rem, steps that stay in the binade); the quotient only when
+        // the run would leave it (rem * D < 2^57: no wrap)
+        const uint32_t room = kHiF - b.m;
+        uint64_t j = rem;
+        if (D && rem * D > room) j = room / D;  // < rem here
+        // steps to reach thr, when that lies within the j steps
+        uint64_t jh = kNone;
         const uint32_t tm = threshold_bits(tb, b.uexp);
         if (tm != kNoThreshold) {
             if (b.m >= tm) jh = 1;
-            else if (D) jh = (tm - b.m + D - 1u) / D;
+            else if (D && b.m + j * D >= tm) jh = (tm - b.m + D - 1u) / D;
         }
-        uint64_t j = rem < jv ? rem : jv;
         if (jh < j) j = jh;
         sb = rebuild_bits(sb, b.m + static_cast<uint32_t>(j) * D);
         done += j;
@@ -555,9 +559,11 @@ GE_CHAIN_HD uint64_t desc_run_f32(double& c, double a, uint64_t n, bool& stop) {
             continue;
         }
         if (D == 0 && b.m >= b.lo) break;  // every remaining step leaves c unchanged
-        const uint64_t jv = (D && b.m >= b.lo) ? static_cast<uint64_t>((b.m - b.lo) / D) : 0;
+        // j = min(rem, steps that stay exact in the binade); the quotient only
+        // when the run would leave it
         const uint64_t rem = n - done;
-        const uint64_t j = rem < jv ? rem : jv;
+        uint64_t j = 0;
+        if (D && b.m >= b.lo) j = rem * D <= b.m - b.lo ? rem : (b.m - b.lo) / D;
         cb = rebuild_bits(cb, b.m - static_cast<uint32_t>(j) * D);
         done += j;
         if (done < n) {

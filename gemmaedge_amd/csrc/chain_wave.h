@@ -51,31 +51,75 @@ __device__ __forceinline__ chain::ParityMap<U> map_wave_excl(chain::ParityMap<U>
     return v;
 }
 
+// Segment totals that let a float chain pass whole steps without replaying
+// them (LDS, filled by other waves while the chain runs). Segment s holds the
+// items [s * seg, (s + 1) * seg), seg being the chain's items per step. For
+// an accumulator in the binade U = 2^uexp, tot[s] is the segment's increment
+// in ulps (the sum of each item's elements below the chain's end times its
+// rounded addend, capped at 2^24), and bit s of flags marks a segment that
+// holds a tie or an addend that leaves the binade (its increment then depends
+// on the accumulator). The table is ready once *built reaches need; a table
+// with tot == nullptr is none.
+struct SkipTable {
+    const uint32_t* tot;
+    const uint32_t* flags;
+    const uint32_t* built;
+    uint32_t need;
+    int uexp;
+};
+
 // The same walk for a float accumulator, in 32-bit integer arithmetic: the
 // accumulator is carried as its float bits, each item's increment comes from
 // the bit fields of its addend (chain_math.h step_bits), increments are capped
 // at 2^24 (more than any binade holds, so the cap never hides an exit) and
 // scanned as u32 with DPP. Each lane takes kPerLane consecutive items, so one
-// step covers 64 * kPerLane items.
+// step covers 64 * kPerLane items. With a skip table (ascending chains), steps
+// in the table's binade keep to its segments, and a segment that starts at an
+// item boundary there, holds no tie and neither leaves the binade, reaches
+// the threshold nor holds the chain's end is passed by adding its total.
 template <bool kDesc, typename View>
-__device__ bool wave_chain_f32(const View& iv, int G, ChainPos& cp, uint32_t L, double& s, double thr) {
+__device__ bool wave_chain_f32(const View& iv, int G, ChainPos& cp, uint32_t L, double& s, double thr,
+                               SkipTable skip = SkipTable{nullptr, nullptr, nullptr, 0u, 0}) {
     constexpr int kPerLane = View::kPerLane;
+    constexpr int kSeg = 64 * kPerLane;
     constexpr uint32_t kCap = 0x1000000u;
     const int lane = __lane_id();
     const uint32_t tb = f2u(static_cast<float>(thr));
     uint32_t sb = f2u(static_cast<float>(s));
+    bool ready = false;  // the table was seen complete (it stays so)
     while (cp.elem < L && cp.item < G) {
+        const chain::StepBits bb = chain::binade_bits(sb);
+        // in the table's binade: steps keep to its segments, and a segment
+        // may be passed whole
+        const bool in_table = skip.tot != nullptr && bb.uexp == skip.uexp;
+        if (in_table && cp.item % kSeg == 0 && !ready)
+            ready = __hip_atomic_load(skip.built, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= skip.need;
+        if (in_table && cp.item % kSeg == 0 && ready) {
+            const int sg = cp.item / kSeg;
+            const int next = min(cp.item + kSeg, G);
+            if (!((skip.flags[sg >> 5] >> (sg & 31)) & 1u) && cp.elem == iv.start(cp.item)) {
+                const uint32_t m2 = bb.m + skip.tot[sg];  // <= 2^24 + 2^24
+                const uint32_t tile_end = iv.start(next);
+                if (m2 <= chain::kHiF && m2 < chain::threshold_bits(tb, bb.uexp) && tile_end < L) {
+                    sb = (sb >> 23) <= 1u ? m2 : ((sb & 0x7F800000u) | (m2 & 0x7FFFFFu));
+                    cp.item = next;
+                    cp.elem = tile_end;
+                    continue;
+                }
+            }
+        }
+        // the step's items: [cp.item, iend), within one segment when skipping
+        const int iend = in_table ? min(G, (cp.item / kSeg + 1) * kSeg) : min(G, cp.item + kSeg);
         const int i0 = cp.item + lane * kPerLane;
         uint32_t bound[kPerLane + 1];
 #pragma unroll
-        for (int j = 0; j <= kPerLane; ++j) bound[j] = iv.start(min(i0 + j, G));
+        for (int j = 0; j <= kPerLane; ++j) bound[j] = iv.start(min(i0 + j, iend));
         uint32_t ab[kPerLane];
 #pragma unroll
         for (int j = 0; j < kPerLane; ++j) {  // G >= 1: the clamped read is in range
             const uint32_t v = f2u(iv.addend(min(i0 + j, G - 1)));
-            ab[j] = i0 + j < G ? v : 0u;
+            ab[j] = i0 + j < iend ? v : 0u;
         }
-        const chain::StepBits bb = chain::binade_bits(sb);
         const uint32_t tm = kDesc ? 0u : chain::threshold_bits(tb, bb.uexp);
         uint32_t nt[kPerLane], lo_e[kPerLane], pre_in[kPerLane + 1];
         bool evj[kPerLane];
@@ -110,8 +154,8 @@ __device__ bool wave_chain_f32(const View& iv, int G, ChainPos& cp, uint32_t L, 
             const uint32_t total = wave::readlane(excl + lane_tot, 63);
             const uint32_t m2 = kDesc ? bb.m - total : bb.m + total;
             sb = (sb >> 23) <= 1u ? m2 : ((sb & 0x7F800000u) | (m2 & 0x7FFFFFu));
-            const int next = cp.item + 64 * kPerLane;
-            const uint32_t tile_end = iv.start(next < G ? next : G);
+            const int next = iend;
+            const uint32_t tile_end = iv.start(next);
             if (tile_end >= L) {  // the last element lies in this step
                 int where = -1;
 #pragma unroll

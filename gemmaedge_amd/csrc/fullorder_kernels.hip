@@ -1619,6 +1619,12 @@ constexpr int kSpecCounters = __builtin_popcount(kSpecWaves);
 static_assert(kSpecBefore + 1 + kSpecAfter <= kSpecGroups, "the picked items fit the candidates");
 static_assert((kSpecWaves & 3u) == 2u, "wave 0 draws, wave 1 picks and counts");
 static_assert(kSpecBatch % kSpecBlock == 0, "a counting round lies in one batch");
+// bf16 rows: the top-p chain's skip table (decide step 5t), in segments of one
+// wave-chain step over LDS items, built by waves 2-7.
+constexpr int kSkipSeg = 64 * LdsView::kPerLane;
+constexpr int kSkipSegs = kStage / kSkipSeg;
+constexpr int kSkipBuilders = 6;
+static_assert((kSpecWaves & 0xFCu) == 0xFCu && kDWaves == 8, "waves 2-7 build the skip table");
 
 struct DecideShared {
     union {
@@ -1642,6 +1648,9 @@ struct DecideShared {
     // kernel's step 6s), made by waves 1.. while wave 0 draws.
     uint32_t spec_cnt[kSpecGroups][kSpecBatches];
     uint32_t spec_key[kSpecGroups], spec_blo[kSpecGroups], spec_bhi[kSpecGroups];
+    uint32_t skip_tot[kSkipSegs];               // the top-p chain's skip table
+    uint32_t skip_flags[(kSkipSegs + 31) / 32];
+    uint32_t skip_built;                        // builder waves done
     uint32_t spec_bdone[kSpecBatches];  // blocks of each batch counted
     uint32_t spec_ulo, spec_uhi;  // the candidates' bins lie in [spec_ulo, spec_uhi]
     uint32_t spec_n;              // candidate groups (0: none)
@@ -2125,10 +2134,17 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     if (lane == 0) sh.ired[wave] = first_low;
     // step 5s (bf16 rows): the counts start at zero, nothing published
     const bool spec_on = !kSorted && !any_nan && V <= kSpecBatches * kSpecBatch;
+    // step 5t (bf16 rows with LDS items): the binade the top-p chain ends in,
+    // that of top_p when it is below 1, else [0.5, 1)
+    const float tpf = p.top_p;
+    const bool skip_on = spec_on && G <= kStage && tpf >= 0x1p-100f && tpf == tpf;
+    const int skip_uexp = chain::binade_bits(f2u(tpf < 1.0f ? tpf : 0.75f)).uexp;
     if (!kSorted) {
         for (int i = tid; i < kSpecGroups * kSpecBatches; i += kDThreads) (&sh.spec_cnt[0][0])[i] = 0u;
         if (tid < kSpecBatches) sh.spec_bdone[tid] = 0u;
+        if (tid < (kSkipSegs + 31) / 32) sh.skip_flags[tid] = 0u;
         if (tid == 0) {
+            sh.skip_built = 0u;
             sh.spec_n = 0u;
             sh.spec_ready = 0u;
             sh.spec_stop = 0u;
@@ -2166,7 +2182,10 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             double s2 = static_cast<double>(q0);
             ChainPos cp{0, 1};
             keep = keff;
-            if (keff > 1 && wave_chain_f32<false>(iv, G, cp, keff, s2, static_cast<double>(p.top_p)))
+            constexpr bool kLds = std::is_same_v<std::decay_t<decltype(iv)>, LdsView>;
+            const SkipTable sk{kLds && skip_on ? sh.skip_tot : nullptr, sh.skip_flags, &sh.skip_built,
+                               kSkipBuilders, skip_uexp};
+            if (keff > 1 && wave_chain_f32<false>(iv, G, cp, keff, s2, static_cast<double>(p.top_p), sk))
                 keep = cp.elem + 1;
             const float mass = static_cast<float>(s2);
             // random.h:1864-1871 and generation.cpp:118-124.
@@ -2294,6 +2313,10 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         if (!kSorted && spec_on)
             while (__builtin_amdgcn_readfirstlane(
                        __hip_atomic_load(&sh.spec_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0)
+                __builtin_amdgcn_s_sleep(2);
+        if (!kSorted && skip_on)
+            while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(&sh.skip_built, __ATOMIC_ACQUIRE,
+                                                                    __HIP_MEMORY_SCOPE_WORKGROUP)) < kSkipBuilders)
                 __builtin_amdgcn_s_sleep(2);
         for (uint32_t x = xs + static_cast<uint32_t>(lane); x < xe; x += 64)
             sh.gx_ids[x - xs] = composite_index(extras[x]);
@@ -2449,6 +2472,46 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             sh.spec_nbat = nbat;
             __hip_atomic_store(&sh.spec_ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
+    };
+    // 5t. bf16 rows with LDS items: waves 2-7 build the top-p chain's skip
+    //     table (chain_wave.h SkipTable) for the binade it ends in, where it
+    //     spends most of its steps (C4: items 711-2830 of about 3050), before
+    //     they count. The chain passes a segment by its total only when that
+    //     is exactly what the segment's step would add.
+    auto skip_build = [&]() {
+        int fl = lane < kDWaves ? sh.ired[lane] : INT_MAX;
+        fl = wave_reduce(fl, [](int x, int y) { return min(x, y); });
+        uint32_t keff = k;  // as the draw's (generation.cpp:106-115)
+        if (q0 < minimum) keff = 1;
+        else if (fl != INT_MAX) keff = min(keff, pre[fl]);
+        const int nseg = (G + kSkipSeg - 1) / kSkipSeg;
+        for (int sg = wave - 2; sg < nseg; sg += kSkipBuilders) {
+            uint32_t lt = 0;
+            bool ev = false;
+#pragma unroll
+            for (int j = 0; j < LdsView::kPerLane; ++j) {
+                const int i = sg * kSkipSeg + lane * LdsView::kPerLane + j;
+                if (i < G) {
+                    const uint32_t n = min(sh.st.pre[i + 1], keff) - min(sh.st.pre[i], keff);
+                    uint32_t D;
+                    bool tie, big;
+                    chain::step_bits(f2u(sh.st.add[i]), skip_uexp, D, tie, big);
+                    if (n) {
+                        ev = ev || tie || big;
+                        const uint64_t t = static_cast<uint64_t>(n) * D;
+                        lt += t > 0x1000000u ? 0x1000000u : static_cast<uint32_t>(t);
+                    }
+                }
+            }
+            lt = min(lt, 0x1000000u);
+            const uint32_t tot = wave::readlane(wave::incl_add(lt), 63);  // <= 64 * 2^24
+            const bool any = __ballot(ev) != 0ull;
+            if (lane == 0) {
+                sh.skip_tot[sg] = min(tot, 0x1000000u);
+                if (any) atomicOr(&sh.skip_flags[sg >> 5], 1u << (sg & 31));
+            }
+        }
+        if (lane == 0) __hip_atomic_fetch_add(&sh.skip_built, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
     auto spec_count = [&]() {  // the counting waves
         while (__builtin_amdgcn_readfirstlane(
@@ -2648,6 +2711,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             if (G <= kStage) spec_pick(LdsView{sh.st.pre, sh.st.add});
             else spec_pick(GlobalView{pre, aux});
         }
+        if (skip_on && wave >= 2) skip_build();
         spec_count();
     }
     __syncthreads();
