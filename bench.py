@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the GemmaEdge token-sampling path on one MI355X.
 
-Headline (BASELINE.json metric): rows/s of the sampler at V=262144, batch 64
+Headline metric: rows/s of the sampler at V=262144, batch 64
 (config C2: fp32 N(0,3) + peaks, softcap 30, T 0.7, top-k 40, top-p 0.9,
 penalty 1.15 over 2048-id histories), with the dominant kernel's achieved HBM
 bandwidth against the 8 TB/s peak; batch-1 latency (C1), C3, C4, C4's rows in
@@ -280,7 +280,7 @@ def bench_c1(torch, sampler, W):
             "bytes_per_launch": w.bytes_per_row()}
         runs[name] = (w, gpu_out)
     # The reference's own dtype with top-k disabled (k = V): the f32 full-order
-    # path for one row (not a BASELINE config; its latency is reported).
+    # path for one row (not one of the headline configs; its latency is reported).
     w = dataclasses.replace(W.c1(), name="C1-f32-full-order", params=dict(W.c1().params, top_k=0))
     b = Bound(sampler, w, torch)
     gpu_out = b.run_once()
@@ -552,7 +552,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
-                                   "(rows shard across GPUs without communication, see DESIGN.md)"}))
+                                   "(rows shard across GPUs without communication)"}))
         sys.exit(2)
     import torch
 
@@ -620,7 +620,7 @@ def main():
             elif name == "C4":
                 e, r = bench_throughput(torch, sampler, W.c4(), "C4")
             elif name == "C4f32":
-                # not a BASELINE config: C4's rows kept in f32 (the f32 full-order path)
+                # not one of the headline configs: C4's rows kept in f32 (the f32 full-order path)
                 e, r = bench_throughput(torch, sampler, W.c4(f32=True), "C4_f32")
             elif name == "C5":
                 c5, run = c5_sweep(torch, sampler, W, args.c5_steps)
