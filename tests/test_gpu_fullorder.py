@@ -323,3 +323,31 @@ def test_scan_skips_batches_on_unaligned_rows(sampler):
                 history=hist, offsets=offs, uniforms=uni)
     assert np.array_equal(tokens.cpu().numpy(), ora.tokens)
     assert np.array_equal(probs.cpu().numpy().view(np.uint32), ora.probs.view(np.uint32))
+
+
+def test_top_p_chain_passes_segments_by_their_totals(sampler):
+    """The top-p chain of bf16 rows passes 128-item segments of its last binade
+    by totals the idle waves wrote while it ran the binades below. Thresholds
+    at and near binade edges (the table's binade is that of top_p), sharp and
+    flat rows (few or many items in that binade), ties, penalised ids and a
+    min-p cut that ends the chain inside the table's segments."""
+    rng = np.random.default_rng(41)
+    V = 70001
+    rows = []
+    for sd in (0.05, 0.1, 0.3, 1.0):
+        rows.append(rng.standard_normal(V) * sd)
+    r = rng.standard_normal(V) * 0.1
+    r = np.round(r * 64) / 64  # heavy ties: long runs, tie flags
+    rows.append(r)
+    x = _bf16(np.stack(rows).astype(np.float32))
+    H = 400
+    hist = rng.integers(0, V, size=x.shape[0] * H).astype(np.int32)
+    offs = (np.arange(x.shape[0] + 1) * H).astype(np.int32)
+    for top_p in (0.25, 0.5, float(np.nextafter(np.float32(0.5), np.float32(1))), 0.75, 0.999, 1.0):
+        for T, min_p, pen in ((1.3, 0.0, 1.0), (0.6, 0.0, 1.2), (1.0, 0.02, 1.0)):
+            w = small_workload(f"skip-p{top_p}-T{T}-m{min_p}-r{pen}", x,
+                               dict(temperature=T, top_k=0, top_p=top_p, min_p=min_p, softcap=30.0,
+                                    repetition_penalty=pen),
+                               history=hist, offsets=offs,
+                               uniforms=W.mt_uniforms(int(top_p * 1000) + int(T * 10), x.shape[0]), dtype="bf16")
+            _check(sampler, w)
