@@ -1018,6 +1018,7 @@ constexpr int kSWaves = kSThreads / 64;
 constexpr int kSSteps = 16;                     // 64-key steps per wave per tile
 constexpr int kSTile = kSThreads * kSSteps;     // 4096 keys
 constexpr int64_t kSplitMaxRows = 160;          // larger f32 slices: fo_sort_kernel
+constexpr int kSplitFuseRows = 8;               // slices up to this: no scan kernel
 
 static_assert(kSTile == 4096, "fo_split_tiles() and fo_tile_words() assume 4096-key tiles");
 
@@ -1169,7 +1170,10 @@ __global__ __launch_bounds__(kSThreads) void fs_scan_kernel(DevArgs a, int T) {
 //     tile's keys of the same digit in position order (ballots per 64-key
 //     step, per-wave LDS counters across steps), the keys grouped by digit in
 //     LDS, each group stored at its output position (consecutive addresses).
-__global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int shift, int src_is_buf1) {
+//     With `fused` (a few rows), the tile computes its output bases from the
+//     tiles' counts itself, as fs_scan_kernel would (which then is not
+//     launched): every tile of a row reads the row's counts.
+__global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int shift, int src_is_buf1, int fused) {
     __shared__ uint32_t staged[kSTile];
     __shared__ uint32_t wc[kSWaves][kDigits];
     __shared__ uint32_t toff[kDigits];
@@ -1192,7 +1196,26 @@ __global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int sh
         key[u] = src[min(i, V - 1)];  // clamped: keys past V unused
     }
     for (int d = lane; d < kDigits; d += 64) wc[wave][d] = 0u;  // only this wave uses its row
-    gb[tid] = split_row(a, row, T).cnt[t * kDigits + tid];
+    if (fused) {
+        // digits before d over all tiles, then digit d in the tiles before t
+        const uint32_t* c = split_row(a, row, T).cnt + tid;
+        constexpr int kB = 16;
+        uint32_t total = 0, part = 0;
+        for (int t0 = 0; t0 < T; t0 += kB) {
+            uint32_t v[kB];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) v[u] = c[min(t0 + u, T - 1) * kDigits];  // clamped
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                const uint32_t x = t0 + u < T ? v[u] : 0u;
+                total += x;
+                part += t0 + u < t ? x : 0u;
+            }
+        }
+        gb[tid] = digit_excl_scan(total, scan, tid) + part;  // (scan[] is read again after a barrier)
+    } else {
+        gb[tid] = split_row(a, row, T).cnt[t * kDigits + tid];
+    }
     const uint64_t below = (1ull << lane) - 1ull;
     uint32_t lr[kSSteps];
 #pragma unroll
@@ -2963,11 +2986,14 @@ hipError_t split_sort_f32(const DevArgs& s, hipStream_t stream) {
     const dim3 rows(static_cast<unsigned>(s.rows));
     hipLaunchKernelGGL(fs_bitmap_kernel, rows, dim3(kSThreads), 0, stream, s);
     hipLaunchKernelGGL(fs_keys_kernel, tiles, dim3(kSThreads), 0, stream, s);
+    // A few rows: each scatter tile scans its row's counts itself (64 KB per
+    // row of V = 262,144 from L2, per tile), one launch fewer per pass.
+    const int fused = s.rows <= kSplitFuseRows ? 1 : 0;
     for (int pass = 0; pass < 4; ++pass) {
         const int src_is_buf1 = pass & 1;  // buf0 -> buf1 -> buf0 -> buf1 -> buf0
         if (pass > 0) hipLaunchKernelGGL(fs_count_kernel, tiles, dim3(kSThreads), 0, stream, s, 8 * pass, src_is_buf1);
-        hipLaunchKernelGGL(fs_scan_kernel, rows, dim3(kSThreads), 0, stream, s, T);
-        hipLaunchKernelGGL(fs_scatter_kernel, tiles, dim3(kSThreads), 0, stream, s, 8 * pass, src_is_buf1);
+        if (!fused) hipLaunchKernelGGL(fs_scan_kernel, rows, dim3(kSThreads), 0, stream, s, T);
+        hipLaunchKernelGGL(fs_scatter_kernel, tiles, dim3(kSThreads), 0, stream, s, 8 * pass, src_is_buf1, fused);
     }
     hipLaunchKernelGGL(fs_bounds_kernel, tiles, dim3(kSThreads), 0, stream, s);
     hipLaunchKernelGGL(fs_istart_kernel, tiles, dim3(kSThreads), 0, stream, s);

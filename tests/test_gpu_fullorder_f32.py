@@ -276,3 +276,19 @@ def test_large_batches_keep_the_per_row_sort():
             _check(s, w)
     finally:
         s.close()
+
+
+def test_tiled_sort_with_and_without_its_scan_kernel(sampler):
+    # Slices of up to 8 rows scan the tiles' digit counts inside the scatter
+    # kernel; larger slices (up to 160) launch the scan kernel. Both, and the
+    # boundary, against the oracle.
+    rng = np.random.default_rng(46)
+    for rows in (8, 9, 24):
+        x = (rng.standard_normal((rows, W.VOCAB)) * rng.uniform(0.1, 3.0, size=(rows, 1))).astype(np.float32)
+        H = 64
+        hist = rng.integers(0, W.VOCAB, size=rows * H).astype(np.int32)
+        offs = (np.arange(rows + 1) * H).astype(np.int32)
+        w = small_workload(f"tiles-{rows}", x, dict(temperature=1.0, top_k=0, top_p=0.95, softcap=30.0,
+                                                    repetition_penalty=1.1),
+                           history=hist, offsets=offs, uniforms=W.mt_uniforms(rows, rows))
+        _check(sampler, w)
