@@ -1065,9 +1065,12 @@ __global__ __launch_bounds__(kSThreads) void fs_bitmap_kernel(DevArgs a) {
 }
 
 // 2. Final keys (generation.cpp:431-437 softcap, then the penalty) of tile t
-//    into buf0, and the tile's count of each lowest digit.
-__global__ __launch_bounds__(kSThreads) void fs_keys_kernel(DevArgs a) {
+//    into buf0, and the tile's count of each lowest digit. With `fused` (a
+//    few rows), the tile also builds its own words of the penalty bitmap from
+//    the history (fs_bitmap_kernel is then not launched).
+__global__ __launch_bounds__(kSThreads) void fs_keys_kernel(DevArgs a, int fused) {
     __shared__ uint32_t h[kDigits];
+    __shared__ uint32_t tbits[kSTile / 32];
     const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     uint32_t k;
     ge_sample_params p;
@@ -1078,9 +1081,23 @@ __global__ __launch_bounds__(kSThreads) void fs_keys_kernel(DevArgs a) {
     history_of(a, row, hist, H);
     const bool pen = H > 0 && !(p.repetition_penalty == 1.0f);
     const float* rowp = static_cast<const float*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
-    const uint32_t* bitmap = a.fo_bitmap + static_cast<int64_t>(row) * a.fo_bitmap_words;
+    uint32_t* bitmap = a.fo_bitmap + static_cast<int64_t>(row) * a.fo_bitmap_words;
     uint32_t* buf0 = reinterpret_cast<uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
     h[tid] = 0u;
+    const int lo = t * kSTile;
+    if (fused && pen) {
+        // this tile's bitmap words (a tile is a whole number of words); the
+        // row's bitmap is all zero between calls
+        for (int w = tid; w < kSTile / 32; w += kSThreads) tbits[w] = 0u;
+        __syncthreads();
+        const int hi = min(lo + kSTile, V);
+        for (int i = tid; i < H; i += kSThreads) {
+            const int32_t id = hist[i];
+            if (id >= lo && id < hi) atomicOr(&tbits[(id - lo) >> 5], 1u << (id & 31));
+        }
+        __syncthreads();
+        for (int w = tid; w < (hi - lo + 31) / 32; w += kSThreads) bitmap[(lo >> 5) + w] = tbits[w];
+    }
     __syncthreads();
     float x[kSSteps];
     uint32_t bw[kSSteps];
@@ -1089,7 +1106,7 @@ __global__ __launch_bounds__(kSThreads) void fs_keys_kernel(DevArgs a) {
         const int i = t * kSTile + u * kSThreads + tid;
         const int ic = min(i, V - 1);  // clamped: no conditional load (values past V unused)
         x[u] = rowp[ic];
-        bw[u] = pen ? bitmap[ic >> 5] : 0u;
+        bw[u] = pen ? (fused ? tbits[(ic - lo) >> 5] : bitmap[ic >> 5]) : 0u;
     }
 #pragma unroll
     for (int u = 0; u < kSSteps; ++u) {
@@ -2984,11 +3001,12 @@ hipError_t split_sort_f32(const DevArgs& s, hipStream_t stream) {
     const int T = fo_split_tiles(s.vocab);
     const dim3 tiles(static_cast<unsigned>(T), static_cast<unsigned>(s.rows));
     const dim3 rows(static_cast<unsigned>(s.rows));
-    hipLaunchKernelGGL(fs_bitmap_kernel, rows, dim3(kSThreads), 0, stream, s);
-    hipLaunchKernelGGL(fs_keys_kernel, tiles, dim3(kSThreads), 0, stream, s);
-    // A few rows: each scatter tile scans its row's counts itself (64 KB per
-    // row of V = 262,144 from L2, per tile), one launch fewer per pass.
+    // A few rows: each keys tile builds its own bitmap words, and each
+    // scatter tile scans its row's counts itself (64 KB per row of
+    // V = 262,144 from L2, per tile): one launch fewer, and one per pass.
     const int fused = s.rows <= kSplitFuseRows ? 1 : 0;
+    if (!fused) hipLaunchKernelGGL(fs_bitmap_kernel, rows, dim3(kSThreads), 0, stream, s);
+    hipLaunchKernelGGL(fs_keys_kernel, tiles, dim3(kSThreads), 0, stream, s, fused);
     for (int pass = 0; pass < 4; ++pass) {
         const int src_is_buf1 = pass & 1;  // buf0 -> buf1 -> buf0 -> buf1 -> buf0
         if (pass > 0) hipLaunchKernelGGL(fs_count_kernel, tiles, dim3(kSThreads), 0, stream, s, 8 * pass, src_is_buf1);
