@@ -3030,8 +3030,8 @@ hipError_t sorted_pass(const DevArgs& a, hipStream_t stream) {
     // while fo_sort_kernel runs up to 256 rows side by side in about the time
     // of one (about equal near 200 rows of V = 262,144). Not with per-row
     // parameters: the host cannot tell whether any row needs this path, and
-    // the many-workgroup sort is 17 launches, about 30 µs even when every row
-    // leaves at once, against two for fo_sort_kernel.
+    // the many-workgroup sort is 12 to 17 launches, about 30 µs even when every
+    // row leaves at once, against two for fo_sort_kernel.
     const bool split = std::is_same<T, float>::value && !a.fo_fallback && a.fo_tiles != nullptr && !a.row_params &&
                        per64 <= kSplitMaxRows && per64 * fo_tile_words(fo_split_tiles(a.vocab)) <= a.fo_tiles_words;
     const int per = static_cast<int>(std::max<int64_t>(1, per64));
