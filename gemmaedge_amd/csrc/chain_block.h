@@ -17,6 +17,13 @@
 // replayed in closed form (chain_math.h asc_run / desc_run) by the thread
 // that holds it, and the scan resumes after it in the new binade. A tile thus
 // costs one pass per binade crossing in it, and ties cost nothing extra.
+//
+// Crossings cluster at the head of a list, where the addends are large next to
+// the accumulator (a C1-shaped row's double sum crosses at items 2, 5 and 30 of
+// its first tile). So a pass first probes: one wave scans the next 64 items the
+// same way, and when the first exit lies among them it is replayed at once,
+// without the block pass. Probes continue while they find the exits; the
+// first that does not hands over to block passes for the rest of the call.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -104,6 +111,10 @@ struct Shared {
     double rs;            // the event item's replay: accumulator after it,
     uint32_t relem;       // next (or event) element,
     int rhit;             // whether the threshold / stop fired
+    double prs[2];        // the same for a probe's event (two buffers: consecutive
+    uint32_t prelem[2];   // probes are one barrier apart)
+    int prhit[2];
+    int pev[2];           // the probe's event item, -1 for none
 };
 
 // Items i .. i + kPer - 1: boundaries pb[0..kPer] (clamped to start(G), so
@@ -157,6 +168,8 @@ __device__ bool block_chain(const uint32_t* pre, const float* add, float scale, 
     int t0 = cp.item / kTile * kTile;
     uint32_t pb[kPer + 1], ab[kPer];
     load_tile(pre, add, scale, G, t0 + tid * kPer, pb, ab);
+    bool probe = true;
+    int pbuf = 0;
     for (;;) {
         // the next tile's loads are in flight while this one is scanned
         uint32_t npb[kPer + 1], nab[kPer];
@@ -167,6 +180,56 @@ __device__ bool block_chain(const uint32_t* pre, const float* add, float scale, 
         for (;;) {  // one pass per binade the tile's remaining items start in
             const typename A::Bin b = A::binade(s, thr);
             const uint32_t e0 = cp.elem;
+            if (probe) {
+                // Wave 0 takes items cp.item .. cp.item + 63 of this tile, one
+                // per lane, with the pass's maps; the first lane whose item
+                // takes the accumulator out of the binade (or to the
+                // threshold) is the pass's event, as the block pass would find.
+                if (wave == 0) {
+                    const int i = cp.item + lane;
+                    const int iend = min(t0 + kTile, G);
+                    const int ic = min(i, iend - 1);  // clamped: no conditional load
+                    const uint32_t lo = max(pre[ic], e0);
+                    const uint32_t hi = min(pre[ic + 1], L);
+                    const uint32_t abits = f2u(add[ic] * scale);
+                    const uint32_t nt = (i < iend && hi > lo) ? hi - lo : 0u;
+                    U D;
+                    bool tie, odd0, big;
+                    A::step(abits, b.uexp, D, tie, odd0, big);
+                    const Map f = chain::run_map<U, A::kCap>(nt, D, tie, odd0, big);
+                    const Map x = map_wave_excl<U, A::kCap>(f);
+                    const U r = chain::apply_from(x, b.m);
+                    const U rn = chain::sat_add_cap<U, A::kCap>(r, chain::apply_from(f, static_cast<U>(b.m + r)));
+                    const uint64_t em = __ballot(nt != 0u && exceeds<kDesc>(b, rn));
+                    if (em == 0ull) {
+                        if (lane == 0) sh.pev[pbuf] = -1;
+                    } else if (lane == static_cast<int>(__builtin_ctzll(em))) {
+                        double sv = A::rebuild(s, b, kDesc ? b.m - r : b.m + r);
+                        bool hit = false;
+                        const uint64_t used = kDesc ? A::desc(sv, static_cast<double>(u2f(abits)), nt, hit)
+                                                    : A::asc(sv, static_cast<double>(u2f(abits)), nt, thr, hit);
+                        sh.prs[pbuf] = sv;
+                        sh.prhit[pbuf] = hit ? 1 : 0;
+                        sh.prelem[pbuf] = hit ? lo + static_cast<uint32_t>(kDesc ? used : used - 1) : hi;
+                        sh.pev[pbuf] = i;
+                    }
+                }
+                __syncthreads();
+                const int pe = sh.pev[pbuf];
+                if (pe >= 0) {
+                    s = sh.prs[pbuf];
+                    cp.elem = sh.prelem[pbuf];
+                    const bool hit = sh.prhit[pbuf] != 0;
+                    pbuf ^= 1;
+                    if (hit || cp.elem >= L) {
+                        cp.item = pe;
+                        return hit;
+                    }
+                    cp.item = pe + 1;
+                    continue;
+                }
+                probe = false;
+            }
             Map f{0, 0};
             int last = -1;
 #pragma unroll

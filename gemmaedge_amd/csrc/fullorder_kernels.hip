@@ -1679,6 +1679,7 @@ struct DecideShared {
     int ired[kDWaves];
     uint32_t ured[kDWaves];
     uint32_t scan[kDWaves];
+    uint32_t tscan[2][kDWaves];  // the token scan's wave sums, by batch parity
     double den;
     uint32_t pos, group_rank, group_total, forward, gx_count;
     uint32_t blo, bhi, nan_group, near, gkey;
@@ -1985,8 +1986,10 @@ __device__ uint32_t wave_partition_point(uint32_t lo, uint32_t hi, Pred pred) {
 // token in them, penalised ones at their final values; raw keys are f32
 // order keys), else from the bf16 histogram (penalised tokens in the
 // extras, raw keys are bf16 bins).
+// bf16 rows run two workgroups per CU (8 waves each: 4 per SIMD, at most 128
+// VGPRs); sorted rows one.
 template <typename T, bool kSorted>
-__global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
+__global__ __launch_bounds__(kDThreads, kSorted ? 2 : 4) void fo_decide_kernel(DevArgs a) {
     constexpr bool kF32 = kSorted;
     __shared__ DecideShared sh;
     const int tid = threadIdx.x;
@@ -2757,17 +2760,24 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
     __syncthreads();
 
     // Locate the token: the rank-th lowest index of the group (or the
-    // (total-1-rank)-th highest), in batches of 8192 tokens from that end;
-    // each thread covers 16 consecutive tokens of a batch, and the next
-    // batch's loads are in flight while this one is scanned. A token is in
-    // the group when its raw key is in [blo, bhi] and it is not penalised;
-    // penalised tokens of the group are the extras run (bf16) or are
-    // evaluated where the bitmap marks them (f32).
+    // (total-1-rank)-th highest), in batches of 16384 tokens from that end;
+    // the next batch's loads are in flight while this one is scanned. Each
+    // wave reads 2048 consecutive tokens of a batch in 16-byte chunks, lane l
+    // taking chunk l of each row of 64 chunks, so that every load reads 1 KB
+    // of consecutive bytes (a lane's own tokens are kChunks chunks, one per
+    // row). Scan order inside a batch is thus wave, chunk row, lane, token.
+    // A token is in the group when its raw key is in [blo, bhi] and it is
+    // not penalised; penalised tokens of the group are the extras run (bf16)
+    // or are evaluated where the bitmap marks them (f32).
     {
-        constexpr int kPer = sizeof(T) == 2 ? 32 : 16;  // 64 bytes per thread per batch
+        constexpr int kPer = 32;                                      // tokens per thread per batch
         constexpr int kBatch = kDThreads * kPer;
-        constexpr int kW = kPer * static_cast<int>(sizeof(T)) / 4;  // 32-bit words per kPer tokens
-        constexpr int kPerVec = 16 / static_cast<int>(sizeof(T));   // tokens per 16-byte load
+        constexpr int kW = kPer * static_cast<int>(sizeof(T)) / 4;    // 32-bit words per thread per batch
+        constexpr int kTokC = 16 / static_cast<int>(sizeof(T));      // tokens per 16-byte chunk
+        constexpr int kChunks = kPer / kTokC;                         // chunks per thread per batch
+        constexpr int kRowC = 64 * kTokC;                             // tokens per chunk row of a wave
+        constexpr int kWaveSpan = 64 * kPer;                          // tokens per wave per batch
+        static_assert(kWaveSpan == 64 * 32, "one history bitmap word per lane covers a wave's tokens");
         const bool fwd = sh.forward != 0;
         uint32_t want = fwd ? sh.group_rank : sh.group_total - 1 - sh.group_rank;
         const uint32_t blo = sh.blo, bhi = sh.bhi;
@@ -2787,25 +2797,33 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             while (b0 < b1) { const uint32_t m = (b0 + b1) >> 1; if (sh.gx_ids[m] < hi) b0 = m + 1; else b1 = m; }
             return b0 - a0;
         };
+        // First token of this thread's chunk q of the batch at token B.
+        auto chunk_tok = [&](int B, int q) { return B + wave * kWaveSpan + q * kRowC + lane * kTokC; };
         // Any batch: its words, the valid tokens, and the history bitmap's
-        // word over them.
-        auto load16 = [&](int lo, uint32_t* w, uint32_t& valid, uint32_t& bw) {
-            bw = pen ? bitmap[min(lo, V - 1) >> 5] : 0u;  // clamped: no conditional load
+        // word B / 32 + wave * 64 + lane (the wave's tokens of the batch lie
+        // in its 64 words).
+        auto load_any = [&](int B, uint32_t* w, uint32_t& valid, uint32_t& bw) {
+            bw = pen ? bitmap[min((B >> 5) + wave * 64 + lane, (V - 1) >> 5)] : 0u;  // clamped: no conditional load
             valid = 0;
-            if (vec && lo + kPer <= V) {
+            if (vec && chunk_tok(B, kChunks - 1) + kTokC <= V) {
+                const T* p0 = rowp + chunk_tok(B, 0);
 #pragma unroll
-                for (int q = 0; q < kW / 4; ++q) {
-                    const uint4 v = *reinterpret_cast<const uint4*>(rowp + lo + q * kPerVec);
+                for (int q = 0; q < kChunks; ++q) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(p0 + q * kRowC);
                     w[4 * q + 0] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
                 }
-                valid = kPer == 32 ? 0xFFFFFFFFu : 0xFFFFu;
+                valid = 0xFFFFFFFFu;
             } else {
                 for (int h = 0; h < kW; ++h) w[h] = 0;
-                for (int h = 0; h < kPer; ++h) {
-                    if (lo + h < V) {
-                        if constexpr (sizeof(T) == 4) w[h] = f2u(rowp[lo + h]);
-                        else w[h >> 1] |= static_cast<uint32_t>(rowp[lo + h]) << ((h & 1) * 16);
-                        valid |= 1u << h;
+                for (int q = 0; q < kChunks; ++q) {
+                    for (int j = 0; j < kTokC; ++j) {
+                        const int t = chunk_tok(B, q) + j;
+                        const int h = q * kTokC + j;
+                        if (t < V) {
+                            if constexpr (sizeof(T) == 4) w[h] = f2u(rowp[t]);
+                            else w[h >> 1] |= static_cast<uint32_t>(rowp[t]) << ((h & 1) * 16);
+                            valid |= 1u << h;
+                        }
                     }
                 }
             }
@@ -2813,54 +2831,84 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
         // A batch wholly inside a 16-byte aligned row: a fixed set of loads
         // with no branch around them. The bitmap is all zero when no history
         // applies: its first word serves.
-        auto load_full = [&](int lo, uint32_t* w, uint32_t& valid, uint32_t& bw) {
-            bw = bitmap[pen ? lo >> 5 : 0];
+        auto load_full = [&](int B, uint32_t* w, uint32_t& valid, uint32_t& bw) {
+            bw = bitmap[pen ? (B >> 5) + wave * 64 + lane : 0];
+            const T* p0 = rowp + chunk_tok(B, 0);
 #pragma unroll
-            for (int q = 0; q < kW / 4; ++q) {
-                const uint4 v = *reinterpret_cast<const uint4*>(rowp + lo + q * kPerVec);
+            for (int q = 0; q < kChunks; ++q) {
+                const uint4 v = *reinterpret_cast<const uint4*>(p0 + q * kRowC);
                 w[4 * q + 0] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
             }
-            valid = kPer == 32 ? 0xFFFFFFFFu : 0xFFFFu;
+            valid = 0xFFFFFFFFu;
         };
-        // Group members among the 16 tokens at lo (bf16: not counting the
-        // penalised ones, which the extras run supplies).
-        auto match16 = [&](int lo, const uint32_t* w, uint32_t valid, uint32_t bw) -> uint32_t {
-            uint32_t mm = 0;
-            // kPer (<= 32) tokens at a multiple of kPer lie in one bitmap word
-            const uint32_t pw = (pen && valid) ? (bw >> (lo & 31)) & valid : 0u;
+        // The penalised ones among the thread's tokens: chunk q of lane l
+        // lies in the bitmap word that lane (q * kRowC + l * kTokC) / 32 loaded.
+        auto pen_mask = [&](int B, uint32_t bw, uint32_t valid) -> uint32_t {
+            if (!pen) return 0u;
+            uint32_t pm = 0;
+#pragma unroll
+            for (int q = 0; q < kChunks; ++q) {
+                const uint32_t word = static_cast<uint32_t>(__shfl(static_cast<int>(bw), (q * kRowC + lane * kTokC) >> 5, 64));
+                const uint32_t at = static_cast<uint32_t>(chunk_tok(B, q)) & 31u;
+                pm |= ((word >> at) & ((1u << kTokC) - 1u)) << (q * kTokC);
+            }
+            return pm & valid;
+        };
+        // Group members among the thread's tokens (bf16: not counting the
+        // penalised ones, which the extras run supplies). f32: branch-free
+        // per token, one range test (raw key - blo <= bhi - blo) and a bit.
+        auto match = [&](int B, const uint32_t* w, uint32_t valid, uint32_t bw) -> uint32_t {
+            const uint32_t pw = pen_mask(B, bw, valid);
             if constexpr (kF32) {
+                const uint32_t span = bhi - blo;
+                const uint32_t some = blo <= bhi ? 0xFFFFFFFFu : 0u;  // (empty when blo > bhi)
+                uint32_t in = 0;
+                auto value = [&](int h) {
+                    return sizeof(T) == 4 ? u2f(w[h]) : u2f(((w[h >> 1] >> ((h & 1) * 16)) & 0xFFFFu) << 16);
+                };
+                if (nan_group) {
 #pragma unroll
-                for (int h = 0; h < kPer; ++h) {
-                    const float x = sizeof(T) == 4 ? u2f(w[h]) : u2f(((w[h >> 1] >> ((h & 1) * 16)) & 0xFFFFu) << 16);
-                    const uint32_t rk = order_key(x);
-                    const bool m = nan_group ? (x != x) : (!((pw >> h) & 1u) && rk >= blo && rk <= bhi);
-                    if (((valid >> h) & 1u) && m) mm |= 1u << h;
-                }
-                if (!nan_group) {
-                    for (uint32_t b = pw; b; b &= b - 1u) {
-                        const int h = __builtin_ctz(b);
-                        // the token's value from the loaded words (a select
-                        // chain: a per-lane index into registers)
-                        uint32_t wv = 0;
-#pragma unroll
-                        for (int q = 0; q < kW; ++q) wv = (sizeof(T) == 4 ? h : h >> 1) == q ? w[q] : wv;
-                        const float x = sizeof(T) == 4 ? u2f(wv) : u2f(((wv >> ((h & 1) * 16)) & 0xFFFFu) << 16);
-                        const float f = penalize(softcap(x, cap), rpen);
-                        if (order_key(f) == gkey) mm |= 1u << h;
+                    for (int h = 0; h < kPer; ++h) {
+                        const float x = value(h);
+                        in |= (x != x ? 1u : 0u) << h;
                     }
+                    return in & valid;
                 }
+#pragma unroll
+                for (int h = 0; h < kPer; ++h) in |= (order_key(value(h)) - blo <= span ? 1u : 0u) << h;
+                uint32_t mm = in & some & valid & ~pw;
+                for (uint32_t b = pw; b; b &= b - 1u) {
+                    const int h = __builtin_ctz(b);
+                    // the token's value from the loaded words (a select
+                    // chain: a per-lane index into registers)
+                    uint32_t wv = 0;
+#pragma unroll
+                    for (int q = 0; q < kW; ++q) wv = (sizeof(T) == 4 ? h : h >> 1) == q ? w[q] : wv;
+                    const float x = sizeof(T) == 4 ? u2f(wv) : u2f(((wv >> ((h & 1) * 16)) & 0xFFFFu) << 16);
+                    const float f = penalize(softcap(x, cap), rpen);
+                    if (order_key(f) == gkey) mm |= 1u << h;
+                }
+                return mm;
             } else {
+                // (bf16 rows run two workgroups per CU: this form keeps the
+                // kernel within 128 VGPRs)
                 auto bin_match = [&](uint32_t bits16) {
                     const uint32_t bin = bin_of(bits16);
                     return nan_group ? bin_is_nan(bin) : (bin >= blo && bin <= bhi);
                 };
+                uint32_t mm = 0;
 #pragma unroll
                 for (int h = 0; h < kPer; ++h) {
                     if (((valid >> h) & 1u) && bin_match((w[h >> 1] >> ((h & 1) * 16)) & 0xFFFFu)) mm |= 1u << h;
                 }
-                mm &= ~pw;
+                return mm & ~pw;
             }
-            return mm;
+        };
+        // bf16: the group's penalised ids in chunk q of the thread (the
+        // extras run).
+        auto gx_chunk = [&](int B, int q) -> uint32_t {
+            const int t0 = chunk_tok(B, q);
+            return (gx && t0 < V) ? gx_in(static_cast<uint32_t>(t0), static_cast<uint32_t>(min(t0 + kTokC, V))) : 0u;
         };
         const int nb = (V + kBatch - 1) / kBatch;
         // Batches the speculative counts (step 5s) show to hold fewer than
@@ -2886,58 +2934,99 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
                 }
             }
         }
-        auto batch_lo = [&](int bi) { return (fwd ? bi : nb - 1 - bi) * kBatch + tid * kPer; };
-        // One batch; true when it holds the token (the scan ends there).
+        auto batch_base = [&](int bi) { return (fwd ? bi : nb - 1 - bi) * kBatch; };
+        // One batch; true when it holds the token (the scan ends there). The
+        // batch's count is a block sum (the waves' sums through LDS, two
+        // buffers in turn: consecutive batches are one barrier apart); only
+        // the batch that holds the token orders its members.
         auto scan_batch = [&](int bi, const uint32_t* w, uint32_t valid, uint32_t bw) -> bool {
-            const int lo = batch_lo(bi);
-            const uint32_t mm = match16(lo, w, valid, bw);
-            const uint32_t hi = static_cast<uint32_t>(min(lo + kPer, V));
+            const int B = batch_base(bi);
+            const uint32_t mm = match(B, w, valid, bw);
             uint32_t cnt = static_cast<uint32_t>(__popc(mm));
-            if constexpr (!kF32) cnt += lo < V ? gx_in(static_cast<uint32_t>(lo), hi) : 0u;
-            uint32_t tot;
-            const uint32_t ex_fwd = dblock_excl_scan(cnt, sh.scan, tot);
-            const uint32_t ex = fwd ? ex_fwd : tot - ex_fwd - cnt;
-            if (want < tot) {
-                if (want >= ex && want < ex + cnt) {
-                    uint32_t r2 = want - ex;
-                    int found = -1;
-                    for (int s2 = 0; s2 < kPer && found < 0; ++s2) {
-                        const int h = fwd ? s2 : kPer - 1 - s2;
-                        if (!((valid >> h) & 1u)) continue;
-                        const uint32_t idx = static_cast<uint32_t>(lo + h);
-                        uint32_t here = (mm >> h) & 1u;
-                        if constexpr (!kF32) {
-                            if (!here && gx) here = gx_in(idx, idx + 1);
-                        }
-                        if (here) {
-                            if (r2 == 0) found = static_cast<int>(idx);
-                            else --r2;
-                        }
-                    }
-                    sh.token = found;
+            if constexpr (!kF32) {
+                if (gx) {
+                    for (int q = 0; q < kChunks; ++q) cnt += gx_chunk(B, q);
                 }
-                return true;
             }
-            want -= tot;
-            return false;
+            uint32_t* wt = sh.tscan[bi & 1];
+            const uint32_t wsum = wave::readlane(wave_incl_u32(cnt), 63);
+            if (lane == 0) wt[wave] = wsum;
+            __syncthreads();
+            uint32_t tot = 0;
+#pragma unroll
+            for (int w2 = 0; w2 < kDWaves; ++w2) tot += wt[w2];
+            if (want >= tot) {
+                want -= tot;
+                return false;
+            }
+            // The token's wave, then its chunk row, lane and token, in scan order.
+            uint32_t r = want;
+            int tw = -1;
+#pragma unroll
+            for (int s2 = 0; s2 < kDWaves; ++s2) {
+                const int w2 = fwd ? s2 : kDWaves - 1 - s2;
+                if (tw < 0) {
+                    if (r < wt[w2]) tw = w2;
+                    else r -= wt[w2];
+                }
+            }
+            if (wave == tw) {
+                for (int s2 = 0; s2 < kChunks; ++s2) {
+                    const int q = fwd ? s2 : kChunks - 1 - s2;
+                    uint32_t cq = static_cast<uint32_t>(__popc((mm >> (q * kTokC)) & ((1u << kTokC) - 1u)));
+                    if constexpr (!kF32) cq += gx_chunk(B, q);
+                    const uint32_t incl = wave_incl_u32(cq);
+                    const uint32_t rowtot = wave::readlane(incl, 63);
+                    if (r >= rowtot) {
+                        r -= rowtot;
+                        continue;
+                    }
+                    const uint32_t ex = fwd ? incl - cq : rowtot - incl;
+                    if (r >= ex && r < ex + cq) {
+                        uint32_t r2 = r - ex;
+                        int found = -1;
+                        const int t0 = chunk_tok(B, q);
+                        for (int s3 = 0; s3 < kTokC && found < 0; ++s3) {
+                            const int j = fwd ? s3 : kTokC - 1 - s3;
+                            const int h = q * kTokC + j;
+                            if (!((valid >> h) & 1u)) continue;
+                            const uint32_t idx = static_cast<uint32_t>(t0 + j);
+                            uint32_t here = (mm >> h) & 1u;
+                            if constexpr (!kF32) {
+                                if (!here && gx) here = gx_in(idx, idx + 1);
+                            }
+                            if (here) {
+                                if (r2 == 0) found = static_cast<int>(idx);
+                                else --r2;
+                            }
+                        }
+                        sh.token = found;
+                    }
+                    break;
+                }
+            }
+            return true;
         };
         // Scan indices [b0, b1) with two buffers in turn, the next batch's
         // loads in flight while this one is matched and scanned, and no
-        // register copy between batches.
+        // register copy between batches. The next loads are issued on every
+        // turn (the last batch again when none is left): with a load issued
+        // on one path only, the compiler's wait before the match covers
+        // every load in flight, the next batch's included.
         auto pipelined = [&](auto&& loader, int b0, int b1) -> bool {
             if (b0 >= b1) return false;
             uint32_t wa[kW], wb[kW];
             uint32_t va = 0, vb = 0, bwa = 0, bwb = 0;
-            loader(batch_lo(b0), wa, va, bwa);
+            loader(batch_base(b0), wa, va, bwa);
             for (int bi = b0; bi < b1; bi += 2) {
                 // (distinct markers keep the compiler from folding the two
                 // halves into one loop body over a single buffer)
                 asm volatile("; token scan: buffer b in flight");
-                if (bi + 1 < b1) loader(batch_lo(bi + 1), wb, vb, bwb);
+                loader(batch_base(min(bi + 1, b1 - 1)), wb, vb, bwb);
                 if (scan_batch(bi, wa, va, bwa)) return true;
                 if (bi + 1 >= b1) break;
                 asm volatile("; token scan: buffer a in flight");
-                if (bi + 2 < b1) loader(batch_lo(bi + 2), wa, va, bwa);
+                loader(batch_base(min(bi + 2, b1 - 1)), wa, va, bwa);
                 if (scan_batch(bi + 1, wb, vb, bwb)) return true;
             }
             return false;
@@ -2950,7 +3039,7 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             bool done = false;
             if (partial && !fwd && b0 == 0) {
                 uint32_t w[kW], v = 0, bw = 0;
-                load16(batch_lo(0), w, v, bw);
+                load_any(batch_base(0), w, v, bw);
                 done = scan_batch(0, w, v, bw);
                 b0 = 1;
             }
@@ -2958,11 +3047,11 @@ __global__ __launch_bounds__(kDThreads) void fo_decide_kernel(DevArgs a) {
             if (!done) done = pipelined(load_full, b0, b1);
             if (!done && partial && fwd && bi0 <= nb - 1) {
                 uint32_t w[kW], v = 0, bw = 0;
-                load16(batch_lo(nb - 1), w, v, bw);
+                load_any(batch_base(nb - 1), w, v, bw);
                 (void)scan_batch(nb - 1, w, v, bw);
             }
         } else {
-            (void)pipelined(load16, bi0, nb);
+            (void)pipelined(load_any, bi0, nb);
         }
     }
     __syncthreads();
