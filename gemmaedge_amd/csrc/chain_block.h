@@ -42,6 +42,14 @@
 namespace ge {
 namespace bchain {
 
+// Address spaces, for code the compiler may keep out of line: there a plain
+// pointer is generic, its accesses become flat instructions, and every wait
+// for an LDS access then also waits for every load in flight.
+#define GE_GLOBAL __attribute__((address_space(1)))
+#define GE_LDS __attribute__((address_space(3)))
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 will not copy from a qualified lvalue)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kPer = 8;  // consecutive items per thread per tile
 
 // Float accumulator (the top-p cumulative and the draw walk).
@@ -106,6 +114,9 @@ template <int kWaves>
 struct Shared {
     uint64_t me[kWaves];  // per-wave maps (magnitudes from an even / odd start)
     uint64_t mo[kWaves];
+    uint64_t pe[kWaves];  // their exclusive composition (the waves before each)
+    uint64_t po[kWaves];
+    uint64_t te, to;      // and the whole tile's
     int ev[kWaves];       // per-wave first event item, INT_MAX for none
     int last;             // item holding element L - 1, when it lies in the tile
     double rs;            // the event item's replay: accumulator after it,
@@ -121,16 +132,16 @@ struct Shared {
 // items past G hold no element) and the bits of their addends, add[i] *
 // scale (one float multiplication, so the addend is exactly the float a
 // separate scaling pass would have stored; scale 1 leaves it unchanged).
-__device__ __forceinline__ void load_tile(const uint32_t* pre, const float* add, float scale, int G, int i,
-                                          uint32_t* pb, uint32_t* ab) {
+__device__ __forceinline__ void load_tile(const GE_GLOBAL uint32_t* pre, const GE_GLOBAL float* add, float scale, int G,
+                                          int i, uint32_t* pb, uint32_t* ab) {
     if (i + kPer <= G) {  // pre has G + 1 entries; i is a multiple of kPer
-        const uint4 p0 = *reinterpret_cast<const uint4*>(pre + i);
-        const uint4 p1 = *reinterpret_cast<const uint4*>(pre + i + 4);
+        const u32x4 p0 = *(const GE_GLOBAL u32x4*)(pre + i);
+        const u32x4 p1 = *(const GE_GLOBAL u32x4*)(pre + i + 4);
         pb[0] = p0.x; pb[1] = p0.y; pb[2] = p0.z; pb[3] = p0.w;
         pb[4] = p1.x; pb[5] = p1.y; pb[6] = p1.z; pb[7] = p1.w;
         pb[8] = pre[i + 8];
-        const float4 a0 = *reinterpret_cast<const float4*>(add + i);
-        const float4 a1 = *reinterpret_cast<const float4*>(add + i + 4);
+        const f32x4 a0 = *(const GE_GLOBAL f32x4*)(add + i);
+        const f32x4 a1 = *(const GE_GLOBAL f32x4*)(add + i + 4);
         ab[0] = f2u(a0.x * scale); ab[1] = f2u(a0.y * scale); ab[2] = f2u(a0.z * scale); ab[3] = f2u(a0.w * scale);
         ab[4] = f2u(a1.x * scale); ab[5] = f2u(a1.y * scale); ab[6] = f2u(a1.z * scale); ab[7] = f2u(a1.w * scale);
     } else {
@@ -155,8 +166,18 @@ __device__ __forceinline__ bool exceeds(const Bin& b, U r) {
 // cp.elem == L and cp.item holding element L - 1. Requires L <= start(G);
 // pre and add 16-byte aligned. Item i's addend is add[i] * scale.
 template <typename A, bool kDesc, int kThreads>
-__device__ bool block_chain(const uint32_t* pre, const float* add, float scale, int G, ChainPos& cp, uint32_t L,
-                            double& s, double thr, Shared<kThreads / 64>& sh) {
+__device__ bool block_chain(const uint32_t* pre_p, const float* add_p, float scale, int G, ChainPos& cp_io, uint32_t L,
+                            double& s_io, double thr, Shared<kThreads / 64>& sh_p) {
+    ChainPos cp = cp_io;  // (locals: the references may be memory of the caller's)
+    double s = s_io;
+    auto leave = [&](bool r) {
+        cp_io = cp;
+        s_io = s;
+        return r;
+    };
+    const GE_GLOBAL uint32_t* pre = (const GE_GLOBAL uint32_t*)pre_p;
+    const GE_GLOBAL float* add = (const GE_GLOBAL float*)add_p;
+    GE_LDS Shared<kThreads / 64>& sh = *(GE_LDS Shared<kThreads / 64>*)&sh_p;
     using U = typename A::U;
     using Map = chain::ParityMap<U>;
     constexpr int kWaves = kThreads / 64;
@@ -164,17 +185,20 @@ __device__ bool block_chain(const uint32_t* pre, const float* add, float scale, 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    if (!(cp.elem < L && cp.item < G)) return false;
+    if (!(cp.elem < L && cp.item < G)) return leave(false);
     int t0 = cp.item / kTile * kTile;
     uint32_t pb[kPer + 1], ab[kPer];
     load_tile(pre, add, scale, G, t0 + tid * kPer, pb, ab);
     bool probe = true;
     int pbuf = 0;
     for (;;) {
-        // the next tile's loads are in flight while this one is scanned
+        // The next tile's loads are in flight while this one is scanned. They
+        // are issued on every tile (the last one loads itself again): with
+        // loads issued on one path only, the compiler's wait for this tile's
+        // values would cover them too.
         uint32_t npb[kPer + 1], nab[kPer];
         const bool more = t0 + kTile < G;
-        if (more) load_tile(pre, add, scale, G, t0 + kTile + tid * kPer, npb, nab);
+        load_tile(pre, add, scale, G, (more ? t0 + kTile : t0) + tid * kPer, npb, nab);
         const uint32_t tile_end = pre[min(t0 + kTile, G)];
         const int ibase = t0 + tid * kPer;
         for (;;) {  // one pass per binade the tile's remaining items start in
@@ -223,7 +247,7 @@ __device__ bool block_chain(const uint32_t* pre, const float* add, float scale, 
                     pbuf ^= 1;
                     if (hit || cp.elem >= L) {
                         cp.item = pe;
-                        return hit;
+                        return leave(hit);
                     }
                     cp.item = pe + 1;
                     continue;
@@ -250,13 +274,22 @@ __device__ bool block_chain(const uint32_t* pre, const float* add, float scale, 
                 sh.mo[wave] = wt.o;
             }
             __syncthreads();
-            Map pw{0, 0}, tot{0, 0};
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                const Map t{static_cast<U>(sh.me[w]), static_cast<U>(sh.mo[w])};
-                if (w < wave) pw = chain::compose<U, A::kCap>(pw, t);
-                tot = chain::compose<U, A::kCap>(tot, t);
+            if (wave == 0) {  // one wave composes the waves' maps for all
+                const Map t = lane < kWaves ? Map{static_cast<U>(sh.me[lane]), static_cast<U>(sh.mo[lane])} : Map{0, 0};
+                const Map ex = map_wave_excl<U, A::kCap>(t);
+                if (lane < kWaves) {
+                    sh.pe[lane] = ex.e;
+                    sh.po[lane] = ex.o;
+                }
+                if (lane == kWaves - 1) {
+                    const Map in = chain::compose<U, A::kCap>(ex, t);
+                    sh.te = in.e;
+                    sh.to = in.o;
+                }
             }
+            __syncthreads();
+            const Map pw{static_cast<U>(sh.pe[wave]), static_cast<U>(sh.po[wave])};
+            const Map tot{static_cast<U>(sh.te), static_cast<U>(sh.to)};
             const U r0 = chain::apply_from(chain::compose<U, A::kCap>(pw, x), b.m);
             const U r_end = chain::sat_add_cap<U, A::kCap>(r0, chain::apply_from(f, static_cast<U>(b.m + r0)));
             int ev = INT_MAX;
@@ -293,7 +326,7 @@ __device__ bool block_chain(const uint32_t* pre, const float* add, float scale, 
                 if (tile_end >= L) {
                     cp.elem = L;
                     cp.item = sh.last;
-                    return false;
+                    return leave(false);
                 }
                 cp.elem = tile_end;
                 cp.item = t0 + kTile;
@@ -326,11 +359,11 @@ __device__ bool block_chain(const uint32_t* pre, const float* add, float scale, 
             const bool hit = sh.rhit != 0;
             if (hit || cp.elem >= L) {
                 cp.item = fe;
-                return hit;
+                return leave(hit);
             }
             cp.item = fe + 1;
         }
-        if (!more) return false;  // unreachable while L <= start(G)
+        if (!more) return leave(false);  // unreachable while L <= start(G)
         t0 += kTile;
 #pragma unroll
         for (int j = 0; j <= kPer; ++j) pb[j] = npb[j];

@@ -2874,8 +2874,17 @@ __global__ __launch_bounds__(kDThreads, kSorted ? 2 : 4) void fo_decide_kernel(D
                     }
                     return in & valid;
                 }
+                if (blo > 0x80000000u || bhi < 0x80000000u) {
+                    // keys of one sign: the raw bits of that sign's floats
+                    // follow the keys (positive: key = bits | 2^31; negative:
+                    // key = ~bits), and the others, zero and NaN fall outside
+                    const uint32_t rlo = blo > 0x80000000u ? (blo & 0x7FFFFFFFu) : ~bhi;
 #pragma unroll
-                for (int h = 0; h < kPer; ++h) in |= (order_key(value(h)) - blo <= span ? 1u : 0u) << h;
+                    for (int h = 0; h < kPer; ++h) in |= (f2u(value(h)) - rlo <= span ? 1u : 0u) << h;
+                } else {
+#pragma unroll
+                    for (int h = 0; h < kPer; ++h) in |= (order_key(value(h)) - blo <= span ? 1u : 0u) << h;
+                }
                 uint32_t mm = in & some & valid & ~pw;
                 for (uint32_t b = pw; b; b &= b - 1u) {
                     const int h = __builtin_ctz(b);
