@@ -1982,6 +1982,26 @@ __device__ uint32_t wave_partition_point(uint32_t lo, uint32_t hi, Pred pred) {
     return lo;
 }
 
+// The same partition point, searched first in the 64 keys from w0 = c - 32
+// (clamped into [lo, hi)) around a guess c: one round when the boundary lies
+// there, else the search above over the side it lies on. Exact whatever the
+// guess (pred is monotone: true, then false).
+template <typename Pred>
+__device__ uint32_t wave_partition_point_near(uint32_t lo, uint32_t hi, uint32_t c, Pred pred) {
+    if (hi <= lo) return lo;
+    uint32_t w0 = c > lo + 32u ? c - 32u : lo;
+    w0 = min(w0, hi - 1u);
+    const uint32_t wn = min(64u, hi - w0);  // keys of the window inside [lo, hi)
+    const uint32_t probe = w0 + static_cast<uint32_t>(__lane_id());
+    const uint64_t m = __ballot(probe - w0 < wn && pred(probe));
+    if (m & 1ull) {  // pred(w0): the boundary is in the window or after it
+        const uint32_t n = static_cast<uint32_t>(__popcll(m));
+        if (n < wn) return w0 + n;
+        return w0 + wn >= hi ? hi : wave_partition_point(w0 + wn, hi, pred);
+    }
+    return w0 == lo ? lo : wave_partition_point(lo, w0, pred);
+}
+
 // T: the logits' type. kSorted: the items come from the sort kernel (every
 // token in them, penalised ones at their final values; raw keys are f32
 // order keys), else from the bf16 histogram (penalised tokens in the
@@ -2324,8 +2344,14 @@ __global__ __launch_bounds__(kDThreads, kSorted ? 2 : 4) void fo_decide_kernel(D
         if (!nan_group) {
             if constexpr (kF32) {
                 auto fk = [&](uint32_t b) { return order_key(softcap(key_value(b), cap)); };
-                blo = wave_partition_point(kKeyNegInf, kKeyPosInf + 1, [&](uint32_t b) { return fk(b) < key; });
-                bhi = wave_partition_point(blo, kKeyPosInf + 1, [&](uint32_t b) { return fk(b) <= key; }) - 1;
+                // guess: the raw value cap * atanh(v / cap) (v itself without
+                // a cap); a raw key's members are usually few
+                uint32_t guess = key;
+                const float v = key_value(key);
+                if (cap > 0.0f && __builtin_fabsf(v) < cap && key != kKeyNaN)
+                    guess = order_key(static_cast<float>(static_cast<double>(cap) * atanh(static_cast<double>(v) / cap)));
+                blo = wave_partition_point_near(kKeyNegInf, kKeyPosInf + 1, guess, [&](uint32_t b) { return fk(b) < key; });
+                bhi = wave_partition_point_near(blo, kKeyPosInf + 1, blo + 32u, [&](uint32_t b) { return fk(b) <= key; }) - 1;
             } else {
                 blo = wave_partition_point(kLowBin, kHighBin + 1, [&](uint32_t b) { return bin_key(b, cap) < key; });
                 bhi = wave_partition_point(blo, kHighBin + 1, [&](uint32_t b) { return bin_key(b, cap) <= key; }) - 1;
