@@ -1017,6 +1017,9 @@ constexpr int kSThreads = 256;
 constexpr int kSWaves = kSThreads / 64;
 constexpr int kSSteps = 16;                     // 64-key steps per wave per tile
 constexpr int kSTile = kSThreads * kSSteps;     // 4096 keys
+constexpr int kKThreads = 1024;                  // fs_keys_kernel's workgroup
+constexpr int kKSteps = kSTile / kKThreads;
+static_assert(kKThreads >= kDigits && kSTile % kKThreads == 0, "the keys kernel's layout");
 constexpr int64_t kSplitMaxRows = 160;          // larger f32 slices: fo_sort_kernel
 constexpr int kSplitFuseRows = 8;               // slices up to this: no scan kernel
 
@@ -1068,7 +1071,9 @@ __global__ __launch_bounds__(kSThreads) void fs_bitmap_kernel(DevArgs a) {
 //    into buf0, and the tile's count of each lowest digit. With `fused` (a
 //    few rows), the tile also builds its own words of the penalty bitmap from
 //    the history (fs_bitmap_kernel is then not launched).
-__global__ __launch_bounds__(kSThreads) void fs_keys_kernel(DevArgs a, int fused) {
+// (1024 threads: 16 waves per CU hide the softcap's dependent latency, where
+// one wave per SIMD did not)
+__global__ __launch_bounds__(kKThreads) void fs_keys_kernel(DevArgs a, int fused) {
     __shared__ uint32_t h[kDigits];
     __shared__ uint32_t tbits[kSTile / 32];
     const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
@@ -1083,34 +1088,34 @@ __global__ __launch_bounds__(kSThreads) void fs_keys_kernel(DevArgs a, int fused
     const float* rowp = static_cast<const float*>(a.logits) + static_cast<int64_t>(row) * a.row_stride;
     uint32_t* bitmap = a.fo_bitmap + static_cast<int64_t>(row) * a.fo_bitmap_words;
     uint32_t* buf0 = reinterpret_cast<uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
-    h[tid] = 0u;
+    if (tid < kDigits) h[tid] = 0u;
     const int lo = t * kSTile;
     if (fused && pen) {
         // this tile's bitmap words (a tile is a whole number of words); the
         // row's bitmap is all zero between calls
-        for (int w = tid; w < kSTile / 32; w += kSThreads) tbits[w] = 0u;
+        for (int w = tid; w < kSTile / 32; w += kKThreads) tbits[w] = 0u;
         __syncthreads();
         const int hi = min(lo + kSTile, V);
-        for (int i = tid; i < H; i += kSThreads) {
+        for (int i = tid; i < H; i += kKThreads) {
             const int32_t id = hist[i];
             if (id >= lo && id < hi) atomicOr(&tbits[(id - lo) >> 5], 1u << (id & 31));
         }
         __syncthreads();
-        for (int w = tid; w < (hi - lo + 31) / 32; w += kSThreads) bitmap[(lo >> 5) + w] = tbits[w];
+        for (int w = tid; w < (hi - lo + 31) / 32; w += kKThreads) bitmap[(lo >> 5) + w] = tbits[w];
     }
     __syncthreads();
-    float x[kSSteps];
-    uint32_t bw[kSSteps];
+    float x[kKSteps];
+    uint32_t bw[kKSteps];
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + u * kSThreads + tid;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + u * kKThreads + tid;
         const int ic = min(i, V - 1);  // clamped: no conditional load (values past V unused)
         x[u] = rowp[ic];
         bw[u] = pen ? (fused ? tbits[(ic - lo) >> 5] : bitmap[ic >> 5]) : 0u;
     }
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + u * kSThreads + tid;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + u * kKThreads + tid;
         if (i < V) {
             float f = softcap(x[u], p.softcap);
             if ((bw[u] >> (i & 31)) & 1u) f = penalize(f, p.repetition_penalty);
@@ -1120,7 +1125,7 @@ __global__ __launch_bounds__(kSThreads) void fs_keys_kernel(DevArgs a, int fused
         }
     }
     __syncthreads();
-    split_row(a, row, T).cnt[t * kDigits + tid] = h[tid];
+    if (tid < kDigits) split_row(a, row, T).cnt[t * kDigits + tid] = h[tid];
 }
 
 // 3a. The tile's count of each digit of pass `shift` (passes after the first).
@@ -3130,7 +3135,7 @@ hipError_t split_sort_f32(const DevArgs& s, hipStream_t stream) {
     // V = 262,144 from L2, per tile): one launch fewer, and one per pass.
     const int fused = s.rows <= kSplitFuseRows ? 1 : 0;
     if (!fused) hipLaunchKernelGGL(fs_bitmap_kernel, rows, dim3(kSThreads), 0, stream, s);
-    hipLaunchKernelGGL(fs_keys_kernel, tiles, dim3(kSThreads), 0, stream, s, fused);
+    hipLaunchKernelGGL(fs_keys_kernel, tiles, dim3(kKThreads), 0, stream, s, fused);
     for (int pass = 0; pass < 4; ++pass) {
         const int src_is_buf1 = pass & 1;  // buf0 -> buf1 -> buf0 -> buf1 -> buf0
         if (pass > 0) hipLaunchKernelGGL(fs_count_kernel, tiles, dim3(kSThreads), 0, stream, s, 8 * pass, src_is_buf1);
