@@ -1375,11 +1375,12 @@ __global__ __launch_bounds__(kSThreads) void fs_istart_kernel(DevArgs a) {
 //     item's value), and the tile's part of the certificate of the top k's
 //     double sum: the sum, the lowest set bit, any NaN. aux held the sorted
 //     keys, which 4b was the last to read.
-__global__ __launch_bounds__(kSThreads) void fs_exps_kernel(DevArgs a) {
+__global__ __launch_bounds__(kKThreads) void fs_exps_kernel(DevArgs a) {  // (1024 threads, as fs_keys_kernel)
+    constexpr int kKWaves = kKThreads / 64;
     __shared__ uint32_t base_s;
-    __shared__ double dred[kSWaves];
-    __shared__ int ired[kSWaves];
-    __shared__ uint32_t ured[kSWaves];
+    __shared__ double dred[kKWaves];
+    __shared__ int ired[kKWaves];
+    __shared__ uint32_t ured[kKWaves];
     const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const int lane = __lane_id(), wave = tid >> 6;
     uint32_t k;
@@ -1401,20 +1402,20 @@ __global__ __launch_bounds__(kSThreads) void fs_exps_kernel(DevArgs a) {
     double S = 0.0;
     int minlsb = INT_MAX;
     bool nan = false;
-    uint64_t itv[kSSteps];
-    uint32_t stv[kSSteps], env[kSSteps];
+    uint64_t itv[kKSteps];
+    uint32_t stv[kKSteps], env[kKSteps];
     if (nj > 0u) {
 #pragma unroll
-        for (int u = 0; u < kSSteps; ++u) {  // nj <= kSTile; clamped indices, no conditional load
-            const uint32_t q = min(static_cast<uint32_t>(u * kSThreads + tid), nj - 1u);
+        for (int u = 0; u < kKSteps; ++u) {  // nj <= kSTile; clamped indices, no conditional load
+            const uint32_t q = min(static_cast<uint32_t>(u * kKThreads + tid), nj - 1u);
             itv[u] = items[j0 + q];
             stv[u] = istart[j0 + q];
             env[u] = istart[j0 + q + 1];
         }
     }
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const uint32_t q = static_cast<uint32_t>(u * kSThreads + tid);
+    for (int u = 0; u < kKSteps; ++u) {
+        const uint32_t q = static_cast<uint32_t>(u * kKThreads + tid);
         if (q < nj) {
             const uint32_t n = env[u] - stv[u];
             const uint32_t vb = static_cast<uint32_t>(itv[u] >> 32);
@@ -1444,7 +1445,7 @@ __global__ __launch_bounds__(kSThreads) void fs_exps_kernel(DevArgs a) {
         double Sp = 0.0;
         int ml = INT_MAX;
         uint32_t nn = 0;
-        for (int w = 0; w < kSWaves; ++w) {
+        for (int w = 0; w < kKWaves; ++w) {
             Sp += dred[w];
             ml = min(ml, ired[w]);
             nn |= ured[w];
@@ -3144,7 +3145,7 @@ hipError_t split_sort_f32(const DevArgs& s, hipStream_t stream) {
     }
     hipLaunchKernelGGL(fs_bounds_kernel, tiles, dim3(kSThreads), 0, stream, s);
     hipLaunchKernelGGL(fs_istart_kernel, tiles, dim3(kSThreads), 0, stream, s);
-    hipLaunchKernelGGL(fs_exps_kernel, tiles, dim3(kSThreads), 0, stream, s);
+    hipLaunchKernelGGL(fs_exps_kernel, tiles, dim3(kKThreads), 0, stream, s);
     hipLaunchKernelGGL(fs_meta_kernel, rows, dim3(64), 0, stream, s, T);
     return hipGetLastError();
 }
