@@ -1129,7 +1129,7 @@ __global__ __launch_bounds__(kKThreads) void fs_keys_kernel(DevArgs a, int fused
 }
 
 // 3a. The tile's count of each digit of pass `shift` (passes after the first).
-__global__ __launch_bounds__(kSThreads) void fs_count_kernel(DevArgs a, int shift, int src_is_buf1) {
+__global__ __launch_bounds__(kKThreads) void fs_count_kernel(DevArgs a, int shift, int src_is_buf1) {  // (1024 threads)
     __shared__ uint32_t h[kDigits];
     const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     uint32_t k;
@@ -1138,21 +1138,21 @@ __global__ __launch_bounds__(kSThreads) void fs_count_kernel(DevArgs a, int shif
     const int V = a.vocab, T = gridDim.x;
     const uint32_t* src = src_is_buf1 ? a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride
                                       : reinterpret_cast<const uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
-    h[tid] = 0u;
+    if (tid < kDigits) h[tid] = 0u;
     __syncthreads();
-    uint32_t kv[kSSteps];
+    uint32_t kv[kKSteps];
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + u * kSThreads + tid;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + u * kKThreads + tid;
         kv[u] = src[min(i, V - 1)];  // clamped: keys past V unused
     }
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + u * kSThreads + tid;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + u * kKThreads + tid;
         if (i < V) atomicAdd(&h[(kv[u] >> shift) & 255u], 1u);
     }
     __syncthreads();
-    split_row(a, row, T).cnt[t * kDigits + tid] = h[tid];
+    if (tid < kDigits) split_row(a, row, T).cnt[t * kDigits + tid] = h[tid];
 }
 
 // 3b. Output position of each (digit, tile) group: digits in order, tiles in
@@ -1195,12 +1195,14 @@ __global__ __launch_bounds__(kSThreads) void fs_scan_kernel(DevArgs a, int T) {
 //     With `fused` (a few rows), the tile computes its output bases from the
 //     tiles' counts itself, as fs_scan_kernel would (which then is not
 //     launched): every tile of a row reads the row's counts.
-__global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int shift, int src_is_buf1, int fused) {
+// (1024 threads, as fs_keys_kernel: threads tid < 256 hold the per-digit work)
+__global__ __launch_bounds__(kKThreads) void fs_scatter_kernel(DevArgs a, int shift, int src_is_buf1, int fused) {
+    constexpr int kKWaves = kKThreads / 64;
     __shared__ uint32_t staged[kSTile];
-    __shared__ uint32_t wc[kSWaves][kDigits];
+    __shared__ uint32_t wc[kKWaves][kDigits];
     __shared__ uint32_t toff[kDigits];
     __shared__ uint32_t gb[kDigits];
-    __shared__ uint32_t scan[kSWaves];
+    __shared__ uint32_t scan[kKWaves];
     const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const int lane = __lane_id(), wave = tid >> 6;
     uint32_t k;
@@ -1211,19 +1213,19 @@ __global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int sh
     uint32_t* b1 = a.fo_pre + static_cast<int64_t>(row) * a.fo_items_stride;
     const uint32_t* src = src_is_buf1 ? b1 : b0;
     uint32_t* dst = src_is_buf1 ? b0 : b1;
-    uint32_t key[kSSteps];
+    uint32_t key[kKSteps];
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kKSteps) + u * 64 + lane;
         key[u] = src[min(i, V - 1)];  // clamped: keys past V unused
     }
     for (int d = lane; d < kDigits; d += 64) wc[wave][d] = 0u;  // only this wave uses its row
     if (fused) {
         // digits before d over all tiles, then digit d in the tiles before t
-        const uint32_t* c = split_row(a, row, T).cnt + tid;
+        const uint32_t* c = split_row(a, row, T).cnt + min(tid, kDigits - 1);
         constexpr int kB = 16;
         uint32_t total = 0, part = 0;
-        for (int t0 = 0; t0 < T; t0 += kB) {
+        for (int t0 = 0; t0 < (tid < kDigits ? T : 0); t0 += kB) {
             uint32_t v[kB];
 #pragma unroll
             for (int u = 0; u < kB; ++u) v[u] = c[min(t0 + u, T - 1) * kDigits];  // clamped
@@ -1234,15 +1236,16 @@ __global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int sh
                 part += t0 + u < t ? x : 0u;
             }
         }
-        gb[tid] = digit_excl_scan(total, scan, tid) + part;  // (scan[] is read again after a barrier)
-    } else {
+        const uint32_t ex = digit_excl_scan(total, scan, tid);  // (scan[] is read again after a barrier)
+        if (tid < kDigits) gb[tid] = ex + part;
+    } else if (tid < kDigits) {
         gb[tid] = split_row(a, row, T).cnt[t * kDigits + tid];
     }
     const uint64_t below = (1ull << lane) - 1ull;
-    uint32_t lr[kSSteps];
+    uint32_t lr[kKSteps];
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kKSteps) + u * 64 + lane;
         const bool act = i < V;
         const uint64_t am = __ballot(act);
         const uint32_t d = (key[u] >> shift) & 255u;
@@ -1258,16 +1261,19 @@ __global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int sh
     }
     __syncthreads();
     uint32_t tot = 0;
-    for (int w = 0; w < kSWaves; ++w) {  // thread d: each wave's offset among the tile's keys of digit d
-        const uint32_t c = wc[w][tid];
-        wc[w][tid] = tot;
-        tot += c;
+    if (tid < kDigits) {
+        for (int w = 0; w < kKWaves; ++w) {  // thread d: each wave's offset among the tile's keys of digit d
+            const uint32_t c = wc[w][tid];
+            wc[w][tid] = tot;
+            tot += c;
+        }
     }
-    toff[tid] = digit_excl_scan(tot, scan, tid);
+    const uint32_t te = digit_excl_scan(tot, scan, tid);
+    if (tid < kDigits) toff[tid] = te;
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kKSteps) + u * 64 + lane;
         if (i < V) {
             const uint32_t d = (key[u] >> shift) & 255u;
             staged[toff[d] + wc[wave][d] + lr[u]] = key[u];
@@ -1276,8 +1282,8 @@ __global__ __launch_bounds__(kSThreads) void fs_scatter_kernel(DevArgs a, int sh
     __syncthreads();
     const int nt = min(kSTile, V - t * kSTile);
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int q = u * kSThreads + tid;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int q = u * kKThreads + tid;
         if (q < nt) {
             const uint32_t kv = staged[q];
             const uint32_t d = (kv >> shift) & 255u;
@@ -3139,9 +3145,9 @@ hipError_t split_sort_f32(const DevArgs& s, hipStream_t stream) {
     hipLaunchKernelGGL(fs_keys_kernel, tiles, dim3(kKThreads), 0, stream, s, fused);
     for (int pass = 0; pass < 4; ++pass) {
         const int src_is_buf1 = pass & 1;  // buf0 -> buf1 -> buf0 -> buf1 -> buf0
-        if (pass > 0) hipLaunchKernelGGL(fs_count_kernel, tiles, dim3(kSThreads), 0, stream, s, 8 * pass, src_is_buf1);
+        if (pass > 0) hipLaunchKernelGGL(fs_count_kernel, tiles, dim3(kKThreads), 0, stream, s, 8 * pass, src_is_buf1);
         if (!fused) hipLaunchKernelGGL(fs_scan_kernel, rows, dim3(kSThreads), 0, stream, s, T);
-        hipLaunchKernelGGL(fs_scatter_kernel, tiles, dim3(kSThreads), 0, stream, s, 8 * pass, src_is_buf1, fused);
+        hipLaunchKernelGGL(fs_scatter_kernel, tiles, dim3(kKThreads), 0, stream, s, 8 * pass, src_is_buf1, fused);
     }
     hipLaunchKernelGGL(fs_bounds_kernel, tiles, dim3(kSThreads), 0, stream, s);
     hipLaunchKernelGGL(fs_istart_kernel, tiles, dim3(kSThreads), 0, stream, s);
