@@ -1299,8 +1299,9 @@ __device__ __forceinline__ bool is_boundary(const uint32_t* s, int i, int V, uin
 }
 
 // 4a. Items starting in tile t.
-__global__ __launch_bounds__(kSThreads) void fs_bounds_kernel(DevArgs a) {
-    __shared__ uint32_t red[kSWaves];
+__global__ __launch_bounds__(kKThreads) void fs_bounds_kernel(DevArgs a) {  // (1024 threads)
+    constexpr int kKWaves = kKThreads / 64;
+    __shared__ uint32_t red[kKWaves];
     const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     uint32_t k;
     ge_sample_params p;
@@ -1309,22 +1310,27 @@ __global__ __launch_bounds__(kSThreads) void fs_bounds_kernel(DevArgs a) {
     const uint32_t* s = reinterpret_cast<const uint32_t*>(a.fo_aux) + static_cast<int64_t>(row) * a.fo_items_stride;
     uint32_t n = 0;
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + u * kSThreads + tid;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + u * kKThreads + tid;
         const uint32_t kv = s[min(i, V - 1)];  // clamped: is_boundary checks i < V
         n += is_boundary(s, i, V, kv) ? 1u : 0u;
     }
     n = wave::readlane(wave::incl_add(n), 63);
     if (__lane_id() == 0) red[tid >> 6] = n;
     __syncthreads();
-    if (tid == 0) split_row(a, row, T).bc[t] = red[0] + red[1] + red[2] + red[3];
+    if (tid == 0) {
+        uint32_t c = 0;
+        for (int w = 0; w < kKWaves; ++w) c += red[w];
+        split_row(a, row, T).bc[t] = c;
+    }
 }
 
 // 4b. Each item's first element into pre (buf1), in position order, and its
 //     value into the high word of its items entry (4c adds the count); the
 //     last tile also writes pre[G] = V.
-__global__ __launch_bounds__(kSThreads) void fs_istart_kernel(DevArgs a) {
-    __shared__ uint32_t scan[kSWaves];
+__global__ __launch_bounds__(kKThreads) void fs_istart_kernel(DevArgs a) {  // (1024 threads)
+    constexpr int kKWaves = kKThreads / 64;
+    __shared__ uint32_t scan[kKWaves];
     __shared__ uint32_t base_s;
     const int t = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const int lane = __lane_id(), wave = tid >> 6;
@@ -1340,18 +1346,18 @@ __global__ __launch_bounds__(kSThreads) void fs_istart_kernel(DevArgs a) {
         const uint32_t b = items_before(sr.bc, t);
         if (lane == 0) base_s = b;
     }
-    // wave w owns positions [w * 1024, (w + 1) * 1024) of the tile
-    uint32_t kv[kSSteps];
-    bool bnd[kSSteps];
+    // wave w owns positions [w * 256, (w + 1) * 256) of the tile
+    uint32_t kv[kKSteps];
+    bool bnd[kKSteps];
     uint32_t nb = 0;
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kKSteps) + u * 64 + lane;
         kv[u] = s[min(i, V - 1)];  // clamped: is_boundary checks i < V
     }
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kKSteps) + u * 64 + lane;
         bnd[u] = is_boundary(s, i, V, kv[u]);
         nb += static_cast<uint32_t>(__popcll(__ballot(bnd[u])));
     }
@@ -1361,8 +1367,8 @@ __global__ __launch_bounds__(kSThreads) void fs_istart_kernel(DevArgs a) {
     for (int w = 0; w < wave; ++w) j += scan[w];
     const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
-    for (int u = 0; u < kSSteps; ++u) {
-        const int i = t * kSTile + wave * (64 * kSSteps) + u * 64 + lane;
+    for (int u = 0; u < kKSteps; ++u) {
+        const int i = t * kSTile + wave * (64 * kKSteps) + u * 64 + lane;
         const uint64_t m = __ballot(bnd[u]);
         if (bnd[u]) {
             const uint32_t jj = j + static_cast<uint32_t>(__popcll(m & below));
@@ -1372,7 +1378,11 @@ __global__ __launch_bounds__(kSThreads) void fs_istart_kernel(DevArgs a) {
         }
         j += static_cast<uint32_t>(__popcll(m));
     }
-    if (t == T - 1 && tid == 0) istart[base_s + scan[0] + scan[1] + scan[2] + scan[3]] = static_cast<uint32_t>(V);
+    if (t == T - 1 && tid == 0) {
+        uint32_t c = base_s;
+        for (int w = 0; w < kKWaves; ++w) c += scan[w];
+        istart[c] = static_cast<uint32_t>(V);
+    }
 }
 
 // 4c. The items that start in tile t: each one's count (from the next
@@ -3149,8 +3159,8 @@ hipError_t split_sort_f32(const DevArgs& s, hipStream_t stream) {
         if (!fused) hipLaunchKernelGGL(fs_scan_kernel, rows, dim3(kSThreads), 0, stream, s, T);
         hipLaunchKernelGGL(fs_scatter_kernel, tiles, dim3(kKThreads), 0, stream, s, 8 * pass, src_is_buf1, fused);
     }
-    hipLaunchKernelGGL(fs_bounds_kernel, tiles, dim3(kSThreads), 0, stream, s);
-    hipLaunchKernelGGL(fs_istart_kernel, tiles, dim3(kSThreads), 0, stream, s);
+    hipLaunchKernelGGL(fs_bounds_kernel, tiles, dim3(kKThreads), 0, stream, s);
+    hipLaunchKernelGGL(fs_istart_kernel, tiles, dim3(kKThreads), 0, stream, s);
     hipLaunchKernelGGL(fs_exps_kernel, tiles, dim3(kKThreads), 0, stream, s);
     hipLaunchKernelGGL(fs_meta_kernel, rows, dim3(64), 0, stream, s, T);
     return hipGetLastError();
