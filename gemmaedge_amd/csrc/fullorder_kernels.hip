@@ -1740,14 +1740,15 @@ struct DecideShared {
 constexpr int kMapTile = kDThreads * bchain::kPer;  // items per tile: block_chain's tile
 constexpr int kMapSub = 4;                           // parts per tile, one workgroup each
 constexpr int kMapSubItems = kMapTile / kMapSub;
-constexpr int kMapThreads = 256;
-constexpr int kMapPer = kMapSubItems / kMapThreads;  // items per thread
+constexpr int kMapGroup = 256;                       // threads per binade slot
+constexpr int kMapPer = kMapSubItems / kMapGroup;    // items per thread
 constexpr int kMapBins = 3;                          // binades bhi - 2 .. bhi (bhi: the sum's, plus one)
 constexpr int kMapRowGroups = 16;                    // grid rows: row r is served by grid row r % 16
 constexpr int kMapPartWords = kMapBins * 4;          // 4 u32 (e, o) per binade
 using DMap = chain::ParityMap<uint64_t>;
 constexpr uint64_t kMapCap = bchain::F64Acc::kCap;
-static_assert(kMapSubItems % kMapThreads == 0, "whole items per thread");
+static_assert(kMapSubItems % kMapGroup == 0, "whole items per thread");
+constexpr int kMapThreads = kMapGroup * kMapBins;   // the slots side by side, one group each
 static_assert(kMapTile == 4096 && kMapSub * kMapPartWords <= 256 + 1 + 4, "a tile's maps fit its share of the tile area");
 
 // Words of one row's maps.
@@ -1813,55 +1814,58 @@ __device__ __forceinline__ void map_part(const DevArgs& a, int row, int part, ui
     const double lb = max(lb1, lb2);
     const int blo = lb >= 1.0 ? exp_of(lb) : 0;
     const int bhi = den_top_binade(S);
-    // This thread's items (clamped loads: items past G hold no element).
+    // Each group of kMapGroup threads composes one slot's map (the slots
+    // side by side: one wave per SIMD left their dependent steps
+    // latency-bound). This thread's items (clamped loads: items past G hold
+    // no element).
+    const int slot = tid / kMapGroup;
+    const int gt = tid % kMapGroup;
+    constexpr int kGW = kMapGroup / 64;  // waves per group
     uint32_t pb[kMapPer + 1];
     uint32_t ab[kMapPer];
-    const int ib = i0 + tid * kMapPer;
+    const int ib = i0 + gt * kMapPer;
 #pragma unroll
     for (int j = 0; j <= kMapPer; ++j) pb[j] = min(pre[min(ib + j, G)], k);
 #pragma unroll
     for (int j = 0; j < kMapPer; ++j) ab[j] = f2u(aux[min(ib + j, G - 1)]);
-    for (int slot = 0; slot < kMapBins; ++slot) {
-        const int b = bhi - (kMapBins - 1) + slot;
-        DMap tot{kMapCap, kMapCap};
-        if (b >= blo && b >= 0) {
-            const int uexp = b - 52;
-            DMap f{0, 0};
+    const int b = bhi - (kMapBins - 1) + slot;
+    const bool live = b >= blo && b >= 0;  // (uniform in the group)
+    if (live) {
+        const int uexp = b - 52;
+        DMap f{0, 0};
 #pragma unroll
-            for (int j = 0; j < kMapPer; ++j) {
-                const uint32_t lo = max(pb[j], 1u);
-                const uint32_t nt = pb[j + 1] > lo ? pb[j + 1] - lo : 0u;
-                uint64_t D;
-                bool tie, odd0, big;
-                chain::step_bits64(ab[j], uexp, D, tie, odd0, big);
-                f = chain::compose<uint64_t, kMapCap>(f, chain::run_map<uint64_t, kMapCap>(nt, D, tie, odd0, big));
-            }
-            const DMap x = map_wave_excl<uint64_t, kMapCap>(f);
-            if (lane == 63) {
-                const DMap wt = chain::compose<uint64_t, kMapCap>(x, f);
-                wmap[0][wave] = wt.e;
-                wmap[1][wave] = wt.o;
-            }
-            __syncthreads();
-            tot = DMap{0, 0};
-#pragma unroll
-            for (int w = 0; w < kMapThreads / 64; ++w)
-                tot = chain::compose<uint64_t, kMapCap>(tot, DMap{wmap[0][w], wmap[1][w]});
-            __syncthreads();
+        for (int j = 0; j < kMapPer; ++j) {
+            const uint32_t lo = max(pb[j], 1u);
+            const uint32_t nt = pb[j + 1] > lo ? pb[j + 1] - lo : 0u;
+            uint64_t D;
+            bool tie, odd0, big;
+            chain::step_bits64(ab[j], uexp, D, tie, odd0, big);
+            f = chain::compose<uint64_t, kMapCap>(f, chain::run_map<uint64_t, kMapCap>(nt, D, tie, odd0, big));
         }
-        if (tid == 0) {
-            out[4 * slot + 0] = static_cast<uint32_t>(tot.e);
-            out[4 * slot + 1] = static_cast<uint32_t>(tot.e >> 32);
-            out[4 * slot + 2] = static_cast<uint32_t>(tot.o);
-            out[4 * slot + 3] = static_cast<uint32_t>(tot.o >> 32);
+        const DMap x = map_wave_excl<uint64_t, kMapCap>(f);
+        if (lane == 63) {
+            const DMap wt = chain::compose<uint64_t, kMapCap>(x, f);
+            wmap[0][wave] = wt.e;
+            wmap[1][wave] = wt.o;
         }
     }
+    __syncthreads();
+    if (gt == 0) {
+        DMap tot{kMapCap, kMapCap};
+        if (live) {
+            tot = DMap{0, 0};
+#pragma unroll
+            for (int w = 0; w < kGW; ++w)
+                tot = chain::compose<uint64_t, kMapCap>(tot, DMap{wmap[0][slot * kGW + w], wmap[1][slot * kGW + w]});
+        }
+        out[4 * slot + 0] = static_cast<uint32_t>(tot.e);
+        out[4 * slot + 1] = static_cast<uint32_t>(tot.e >> 32);
+        out[4 * slot + 2] = static_cast<uint32_t>(tot.o);
+        out[4 * slot + 3] = static_cast<uint32_t>(tot.o >> 32);
+    }
+    __syncthreads();  // wmap is read before the next part writes it
 }
 
-// Grid (parts, min(rows, kMapRowGroups)); grid row y serves rows y, y + 16,
-// ... (at most 64 of them: slices hold at most 256 rows), whose need the
-// lanes of wave 0 check side by side first, so a slice whose sums all
-// certify costs one round of loads per workgroup.
 __global__ __launch_bounds__(kMapThreads) void fo_denmap_kernel(DevArgs a) {
     __shared__ uint64_t wmap[2][kMapThreads / 64];
     __shared__ uint64_t need_rows;
